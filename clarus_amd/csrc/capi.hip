@@ -1,0 +1,31 @@
+// Library-wide C entry points: ABI version, struct sizes, per-thread error text.
+#include <string.h>
+
+#include "capi.hpp"
+
+namespace clarus {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+}  // namespace clarus
+
+extern "C" {
+
+int clarus_hip_abi_version(void) { return CLARUS_HIP_ABI_VERSION; }
+
+size_t clarus_hip_sizeof_gemm_args(void) { return sizeof(ClarusGemmArgs); }
+
+size_t clarus_hip_sizeof_conv_args(void) { return sizeof(ClarusConvArgs); }
+
+const char* clarus_hip_last_error(void) { return clarus::g_err; }
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// Device helpers shared by the gfx950 kernels of libclarus_hip.so.
+//
+// MFMA conventions used throughout (CDNA3/CDNA4 16x16 family, wave64, lane l):
+//   D = A . B with A [16 x K], B [K x 16], D [16 x 16] fp32.
+//   D:  lane l holds D[4 * (l / 16) + j][l % 16], j = 0..3.
+//   A / B: lane l supplies row (A) / column (B) l % 16; the K values a lane supplies are
+//   selected by l / 16. Both operands use the same K selection, so which physical k each
+//   (lane, slot) pair stands for is free as long as A and B agree; the kernels load 8
+//   consecutive k per lane (k = 8 * (l / 16) + i) for every instruction flavour:
+//     bf16 16x16x32: slot i of the 8-vector is k = 8 * (l / 16) + i
+//     fp32 16x16x4 : instruction i (of 8) uses slot i, covering k = 8 * (l / 16) + i
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace clarus {
+
+typedef __bf16 bf16_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+enum : int { DT_F32 = 0, DT_BF16 = 1 };
+
+struct f32x8 {
+  float v[8];
+};
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short h) {
+  return __uint_as_float(((unsigned int)h) << 16);
+}
+
+// round-to-nearest-even fp32 -> bf16 bits (torch's Tensor.to(bfloat16) rounding); NaN stays NaN
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float f) {
+  bf16_t b = (bf16_t)f;
+  return __builtin_bit_cast(unsigned short, b);
+}
+
+// 8 consecutive elements at p (16-byte aligned for bf16, 32-byte for fp32) as fp32
+template <int DT>
+__device__ __forceinline__ f32x8 load8(const void* p) {
+  f32x8 r;
+  if constexpr (DT == DT_BF16) {
+    u32x4 q = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.v[2 * i] = __uint_as_float(q[i] << 16);
+      r.v[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+    }
+  } else {
+    f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.v[i] = a[i];
+      r.v[4 + i] = b[i];
+    }
+  }
+  return r;
+}
+
+__device__ __forceinline__ f32x8 zero8() {
+  f32x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.v[i] = 0.f;
+  return r;
+}
+
+__device__ __forceinline__ float load1(const void* p, int dt, int64_t i) {
+  if (dt == DT_BF16) return bf16_to_f32(reinterpret_cast<const unsigned short*>(p)[i]);
+  return reinterpret_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store1(void* p, int dt, int64_t i, float v) {
+  if (dt == DT_BF16)
+    reinterpret_cast<unsigned short*>(p)[i] = f32_to_bf16_bits(v);
+  else
+    reinterpret_cast<float*>(p)[i] = v;
+}
+
+// pack 8 fp32 into 8 bf16 (RNE)
+__device__ __forceinline__ bf16x8 pack_bf16(const f32x8& a) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (bf16_t)a.v[i];
+  return r;
+}
+
+// a = hi + lo with hi, lo bf16: |a - hi - lo| <= 2^-16 |a| (both roundings RNE)
+__device__ __forceinline__ void split_bf16(const f32x8& a, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16_t h = (bf16_t)a.v[i];
+    hi[i] = h;
+    lo[i] = (bf16_t)(a.v[i] - (float)h);
+  }
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// exact-erf GELU (torch.nn.functional.gelu default)
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+
+// sum over the 4 lanes {l, l^16, l^32, l^48} (the lanes that share an MFMA column)
+__device__ __forceinline__ float sum_col4(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace clarus

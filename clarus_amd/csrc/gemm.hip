@@ -1,0 +1,235 @@
+// C entry points of the fused GEMM family: clarus_hip_gemm, clarus_hip_conv3x3,
+// clarus_hip_intro3x3. Argument checks happen here, before any launch.
+#include "capi.hpp"
+#include "gemm_dispatch.hpp"
+
+namespace clarus {
+
+static int esize(int dt) { return dt == DT_BF16 ? 2 : 4; }
+static bool dt_ok(int dt) { return dt == DT_F32 || dt == DT_BF16; }
+
+static int operand_mode(int a_dt, int w_dt, bool transformed) {
+  if (w_dt == DT_F32) return OPM_F32;
+  if (a_dt == DT_BF16 && !transformed) return OPM_BF16;
+  return OPM_SPLIT;
+}
+
+// tile id for a problem: channel tile from n, pixel tile from the amount of parallel work
+static int auto_tile(int64_t m, int64_t n, int64_t batch, bool gate, int opm) {
+  int t;
+  if (n <= 16) t = 0;
+  else if (n <= 32) t = 1;
+  else if (n <= 64 || gate || opm == OPM_F32) t = 3;
+  else t = 6;
+  const int64_t tn = 16 * kTileNB[t];
+  const int64_t wgs = cdiv(m, 64 * kTilePB[t]) * cdiv(n, tn) * batch;
+  if (wgs < 1024) {
+    if (t == 3) t = 2;
+    if (t == 6) t = 5;
+  }
+  return t;
+}
+
+// persistent grid: when W^T fits in one LDS chunk a workgroup keeps it and walks several
+// pixel tiles; aim for ~1024 resident workgroups (256 CUs x 4)
+static dim3 grid_for(int64_t ptiles, int64_t ntiles, int64_t batch, int64_t k, int kc) {
+  int64_t gx = ptiles;
+  if (k <= kc) {
+    const int64_t target = 1024;
+    int64_t per = ntiles * batch;
+    int64_t want = (target + per - 1) / per;
+    if (want < 1) want = 1;
+    if (want < ptiles) {
+      const int64_t tiles_per = cdiv(ptiles, want);
+      gx = cdiv(ptiles, tiles_per);
+    }
+  }
+  return dim3((unsigned)gx, (unsigned)ntiles, (unsigned)batch);
+}
+
+static int launch(GemmP& p, int am, bool gate, int opm, int ta, int tile, int64_t batch,
+                  hipStream_t s, const char* what) {
+  if (tile < 0 || tile >= kNumTiles) {
+    set_error("%s: tile id %d out of range", what, tile + 1);
+    return CLARUS_EINVAL;
+  }
+  GemmLaunch fn = nullptr;
+  if (am == AM_ROWS) fn = pick_gemm_rows(tile, gate, opm, ta);
+  else if (am == AM_S2D) fn = pick_gemm_s2d(tile, opm, ta);
+  else fn = pick_gemm_conv(tile, opm, ta);
+  if (!fn) {
+    set_error("%s: no kernel for tile %d gate %d operand mode %d A dtype %d", what, tile, (int)gate,
+              opm, ta);
+    return CLARUS_EINVAL;
+  }
+  const int64_t tn = 16 * kTileNB[tile];
+  const int64_t tp = 64 * kTilePB[tile];
+  p.ptiles = cdiv(p.m, tp);
+  dim3 g = grid_for(p.ptiles, cdiv(p.n, tn), batch, p.k, kc_for(opm));
+  fn(p, g, s);
+  return check_launch(what);
+}
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(a != nullptr, "gemm: null args");
+  CLARUS_REQUIRE(a->a && a->wt && a->c, "gemm: null operand");
+  CLARUS_REQUIRE(a->m > 0 && a->n > 0 && a->k > 0 && a->batch > 0, "gemm: empty problem m=%lld n=%lld k=%lld",
+                 (long long)a->m, (long long)a->n, (long long)a->k);
+  CLARUS_REQUIRE(dt_ok(a->a_dtype) && dt_ok(a->w_dtype) && dt_ok(a->c_dtype), "gemm: bad dtype code");
+  CLARUS_REQUIRE(a->k % 8 == 0, "gemm: K=%lld must be a multiple of 8", (long long)a->k);
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS || a->a_mode == CLARUS_A_S2D, "gemm: bad a_mode %d", a->a_mode);
+  CLARUS_REQUIRE(a->c_mode == CLARUS_C_ROWS || a->c_mode == CLARUS_C_SHUFFLE, "gemm: bad c_mode %d", a->c_mode);
+  CLARUS_REQUIRE(a->pro == PRO_NONE || a->pro == PRO_LN || a->pro == PRO_MUL || a->pro == PRO_RMS ||
+                     a->pro == PRO_LNMUL, "gemm: bad prologue %d", a->pro);
+  CLARUS_REQUIRE(a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU, "gemm: bad act %d", a->act);
+  CLARUS_REQUIRE(!(a->gate && a->a_mode != CLARUS_A_ROWS), "gemm: gate only with row operands");
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS || a->pro == PRO_NONE, "gemm: prologues only with row operands");
+  const int ea = esize(a->a_dtype), ew = esize(a->w_dtype);
+  CLARUS_REQUIRE(aligned(a->a, 16) && aligned(a->wt, 16), "gemm: A and W must be 16-byte aligned");
+  CLARUS_REQUIRE(a->batch == 1 || (a->a_bstride * ea) % 16 == 0, "gemm: A batch stride alignment");
+  CLARUS_REQUIRE(a->batch == 1 || (a->w_bstride * ew) % 16 == 0, "gemm: W batch stride alignment");
+
+  GemmP p{};
+  p.a = a->a; p.wt = a->wt; p.c = a->c;
+  p.bias = a->bias; p.scale = a->scale; p.res = a->res;
+  p.small = a->small; p.m2 = a->m2; p.lnw = a->lnw; p.lnb = a->lnb;
+  p.m = a->m; p.n = a->n; p.k = a->k;
+  p.lda = a->lda; p.ldc = a->ldc; p.ldr = a->ldr; p.ldm2 = a->ldm2;
+  p.a_bs = a->a_bstride; p.w_bs = a->w_bstride; p.c_bs = a->c_bstride; p.r_bs = a->r_bstride;
+  p.s_bs = 0; p.m2_bs = 0;
+  p.c_dt = a->c_dtype; p.r_dt = a->r_dtype; p.s_dt = a->s_dtype; p.m2_dt = a->m2_dtype;
+  p.h = a->h; p.w = a->w; p.oh = a->oh; p.ow = a->ow; p.pt = a->pt; p.pl = a->pl;
+  p.pro = a->pro; p.c_mode = a->c_mode; p.act = a->act; p.m2_act = a->m2_act;
+  p.has_bias = a->bias != nullptr; p.has_scale = a->scale != nullptr; p.has_res = a->res != nullptr;
+  p.ln_eps = a->ln_eps; p.out_scale = a->out_scale; p.slope = a->slope;
+  p.up2 = 0;
+
+  if (a->a_mode == CLARUS_A_ROWS) {
+    CLARUS_REQUIRE((a->lda * ea) % 16 == 0 && a->lda >= a->k, "gemm: lda=%lld must cover K and keep 16-byte rows",
+                   (long long)a->lda);
+  } else {
+    CLARUS_REQUIRE(a->k % 32 == 0, "gemm: space-to-depth needs K = 4 * cin with cin %% 8 == 0");
+    CLARUS_REQUIRE(a->h > 1 && a->w > 1, "gemm: space-to-depth needs h, w >= 2");
+    CLARUS_REQUIRE(a->m % ((int64_t)(a->h / 2) * (a->w / 2)) == 0 && a->batch == 1,
+                   "gemm: space-to-depth rows must be whole output images");
+    p.cin = (int)(a->k / 4);
+    p.lda = p.cin;
+  }
+  if (a->pro == PRO_MUL) {
+    CLARUS_REQUIRE(a->small && dt_ok(a->s_dtype) && aligned(a->small, 16), "gemm: mul prologue needs an aligned map");
+    CLARUS_REQUIRE(a->h > 0 && a->w > 0 && a->oh > 0 && a->ow > 0 && a->m % ((int64_t)a->h * a->w) == 0 &&
+                       a->batch == 1, "gemm: mul prologue geometry");
+  }
+  if (a->pro == PRO_LNMUL) {
+    CLARUS_REQUIRE(a->m2 && a->lnw && a->lnb && dt_ok(a->m2_dtype), "gemm: LN-mul prologue operands");
+    CLARUS_REQUIRE(aligned(a->m2, 16) && (a->ldm2 * esize(a->m2_dtype)) % 16 == 0 && aligned(a->lnw, 16) &&
+                       aligned(a->lnb, 16) && a->batch == 1, "gemm: LN-mul operand alignment");
+  }
+  if (a->res) CLARUS_REQUIRE(dt_ok(a->r_dtype), "gemm: bad residual dtype");
+  const int ec = esize(a->c_dtype);
+  if (a->c_mode == CLARUS_C_SHUFFLE) {
+    CLARUS_REQUIRE(a->n % 16 == 0 && a->h > 0 && a->w > 0 && a->m % ((int64_t)a->h * a->w) == 0 && a->batch == 1,
+                   "gemm: pixel-shuffle output needs N %% 16 == 0 and whole images");
+    p.vec_out = aligned(a->c, 4 * ec);
+    p.vec_res = a->res ? aligned(a->res, 4 * esize(a->r_dtype)) : 0;
+  } else {
+    CLARUS_REQUIRE(a->ldc >= a->n, "gemm: ldc < n");
+    p.vec_out = aligned(a->c, 4 * ec) && a->ldc % 4 == 0 && (a->c_bstride % 4 == 0);
+    p.vec_res = a->res ? (aligned(a->res, 4 * esize(a->r_dtype)) && a->ldr % 4 == 0 && a->r_bstride % 4 == 0) : 0;
+  }
+
+  const bool transformed = a->pro != PRO_NONE;
+  const int opm = operand_mode(a->a_dtype, a->w_dtype, transformed);
+  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(a->m, a->n, a->batch, a->gate != 0, opm);
+  return launch(p, a->a_mode == CLARUS_A_ROWS ? AM_ROWS : AM_S2D, a->gate != 0, opm, a->a_dtype, tile, a->batch,
+                (hipStream_t)stream, "gemm");
+}
+
+extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(a != nullptr, "conv3x3: null args");
+  CLARUS_REQUIRE(a->x && a->wt && a->out, "conv3x3: null operand");
+  CLARUS_REQUIRE(a->batch > 0 && a->h > 0 && a->w > 0 && a->cin > 0 && a->cout > 0, "conv3x3: empty problem");
+  CLARUS_REQUIRE(dt_ok(a->x_dtype) && dt_ok(a->w_dtype) && dt_ok(a->o_dtype), "conv3x3: bad dtype code");
+  CLARUS_REQUIRE(a->cin % 8 == 0, "conv3x3: cin=%lld must be a multiple of 8", (long long)a->cin);
+  CLARUS_REQUIRE(a->act == ACT_NONE || a->act == ACT_LRELU, "conv3x3: act must be none or lrelu");
+  CLARUS_REQUIRE(a->c_mode == CLARUS_C_ROWS || a->c_mode == CLARUS_C_NCHW, "conv3x3: bad c_mode");
+  const int ex = esize(a->x_dtype);
+  CLARUS_REQUIRE(aligned(a->x, 16) && (a->ldx * ex) % 16 == 0 && a->ldx >= a->cin,
+                 "conv3x3: x must be 16-byte aligned with a 16-byte pixel stride");
+  CLARUS_REQUIRE(aligned(a->wt, 16), "conv3x3: weights must be 16-byte aligned");
+  if (a->res) CLARUS_REQUIRE(dt_ok(a->r_dtype), "conv3x3: bad residual dtype");
+
+  GemmP p{};
+  const int64_t H = a->h << (a->up2 ? 1 : 0), W = a->w << (a->up2 ? 1 : 0);
+  p.a = a->x; p.wt = a->wt; p.c = a->out;
+  p.bias = a->bias; p.scale = nullptr; p.res = a->res;
+  p.m = a->batch * H * W; p.n = a->cout; p.k = 9 * a->cin;
+  p.lda = a->ldx; p.ldc = a->ldo; p.ldr = a->ldr;
+  p.c_dt = a->o_dtype; p.r_dt = a->r_dtype;
+  p.h = (int)a->h; p.w = (int)a->w; p.cin = (int)a->cin; p.up2 = a->up2 ? 1 : 0;
+  p.pro = PRO_NONE; p.c_mode = a->c_mode; p.act = a->act;
+  p.has_bias = a->bias != nullptr; p.has_scale = 0; p.has_res = a->res != nullptr;
+  p.out_scale = a->out_scale; p.slope = a->slope; p.ln_eps = 0.f;
+  const int eo = esize(a->o_dtype);
+  if (a->c_mode == CLARUS_C_ROWS) {
+    CLARUS_REQUIRE(a->ldo >= a->cout && (!a->res || a->ldr >= a->cout), "conv3x3: pixel strides smaller than cout");
+    p.vec_out = aligned(a->out, 4 * eo) && a->ldo % 4 == 0;
+    p.vec_res = a->res ? (aligned(a->res, 4 * esize(a->r_dtype)) && a->ldr % 4 == 0) : 0;
+  } else {
+    p.vec_out = 0;
+    p.vec_res = 0;
+  }
+  const int opm = operand_mode(a->x_dtype, a->w_dtype, false);
+  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(p.m, p.n, 1, false, opm);
+  return launch(p, AM_CONV3, false, opm, a->x_dtype, tile, 1, (hipStream_t)stream, "conv3x3");
+}
+
+// ------------------------------------------------------------------- intro 3 -> C conv
+// One thread per (pixel, 4-channel group): 27 loads of the 3x3x3 window, 27 x 4 FMAs.
+__global__ void __launch_bounds__(256) intro_kernel(const float* __restrict__ inp, const float* __restrict__ wt,
+                                                    const float* __restrict__ bias, void* out, int out_dt,
+                                                    int64_t m, int h, int w, int cout) {
+  const int groups = (cout + 3) / 4;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= m * groups) return;
+  const int64_t q = t / groups;
+  const int c0 = (int)(t - q * groups) * 4;
+  const int64_t hw = (int64_t)h * w;
+  const int64_t img = q / hw;
+  const int rr = (int)(q - img * hw);
+  const int y = rr / w, x = rr - (rr / w) * w;
+  float acc[4];
+  for (int i = 0; i < 4; ++i) acc[i] = (c0 + i < cout) ? bias[c0 + i] : 0.f;
+  for (int tap = 0; tap < 9; ++tap) {
+    const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+    if (yy < 0 || yy >= h || xx < 0 || xx >= w) continue;
+    for (int c = 0; c < 3; ++c) {
+      const float v = inp[(img * 3 + c) * hw + (int64_t)yy * w + xx];
+      const float* wr = wt + (tap * 3 + c) * cout + c0;
+      for (int i = 0; i < 4; ++i)
+        if (c0 + i < cout) acc[i] = fmaf(v, wr[i], acc[i]);
+    }
+  }
+  for (int i = 0; i < 4; ++i)
+    if (c0 + i < cout) store1(out, out_dt, q * cout + c0 + i, acc[i]);
+}
+
+extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, void* out,
+                                   int32_t out_dtype, int64_t batch, int64_t h, int64_t w, int64_t cout,
+                                   void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(inp && wt && bias && out, "intro3x3: null operand");
+  CLARUS_REQUIRE(batch > 0 && h > 0 && w > 0 && cout > 0, "intro3x3: empty problem");
+  CLARUS_REQUIRE(dt_ok(out_dtype), "intro3x3: bad dtype");
+  const int64_t m = batch * h * w;
+  const int64_t work = m * ((cout + 3) / 4);
+  hipLaunchKernelGGL(intro_kernel, dim3((unsigned)cdiv(work, 256)), dim3(256), 0, (hipStream_t)stream, inp, wt,
+                     bias, out, out_dtype, m, (int)h, (int)w, (int)cout);
+  return check_launch("intro3x3");
+}

@@ -1,0 +1,360 @@
+"""`hip` operator backend: clarus's GEMM-family ops on MI355X (gfx950) HIP kernels.
+
+Registers as backend "hip" in the per-operator dispatch (python/clarus/ops/__init__.py:41-51),
+so a runtime config `backends: [hip, torch]` runs these kernels and falls back to the PyTorch
+reference backend for anything they decline. Each op has the signature and semantics of the
+reference backend (python/clarus/ops/torch_ref.py) and the acceptance rules of the Triton
+adapter (python/clarus/ops/triton_cuda.py): arguments the kernels do not handle raise
+`Unsupported` BEFORE anything is launched; a failure inside the library raises RuntimeError.
+
+Ops served: linear, down, up, intro, ending, conv3x3, channel_attention, linear_per_image,
+patch_filter, linear_patch_filter, patch_corr, ln_mul_linear.
+
+Capture safety: kernels launch on torch's current stream, scratch comes from torch's
+allocator, weight re-layouts are computed once through `Backend.cached` (in the eager warm-up
+pass), and no call synchronises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .dft import dft_matrices
+from .dispatch import Backend, BackendUnavailable, Unsupported, register_backend
+from .geometry import is_small
+
+_KDT = (torch.bfloat16, torch.float32)
+
+
+# ------------------------------------------------------------------ acceptance predicates
+def _dense(*ts) -> bool:
+    """All given tensors (None skipped) are contiguous."""
+    return all(t is None or t.is_contiguous() for t in ts)
+
+
+def _same(t, shape) -> bool:
+    """t is None, or contiguous with exactly `shape`."""
+    return t is None or (t.is_contiguous() and tuple(t.shape) == tuple(shape))
+
+
+def _pix_rows(t: torch.Tensor) -> bool:
+    """NHWC addressable as pixel * stride(2) + channel: unit channel stride and one uniform
+    pixel stride across rows and images (a channel slice of a wider buffer qualifies)."""
+    n, h, w, _ = t.shape
+    s = t.stride()
+    return s[3] == 1 and (h == 1 or s[1] == w * s[2]) and (n == 1 or s[0] == h * w * s[2])
+
+
+def _kdt(*ts) -> bool:
+    return all(t is None or t.dtype in _KDT for t in ts)
+
+
+def _vec16(t: torch.Tensor, *strides: int) -> bool:
+    """Base pointer and the given element strides keep 16-byte alignment."""
+    es = t.element_size()
+    return t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in strides)
+
+
+@register_backend("hip")
+class HipOps(Backend):
+    name = "hip"
+
+    def __init__(self, dtype, device):
+        super().__init__(dtype, device)
+        dev = torch.device(device)
+        if torch.version.hip is None:
+            raise BackendUnavailable("needs a ROCm build of torch")
+        if dev.type != "cuda":
+            raise BackendUnavailable(f"needs a HIP device (torch type 'cuda'), got {dev}")
+        if dtype not in _KDT:
+            raise BackendUnavailable(f"runs bf16 / fp32 activations, got {dtype}")
+        if not torch.cuda.is_available():
+            raise BackendUnavailable("no HIP device is visible")
+        if dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
+        if arch != "gfx950":
+            raise BackendUnavailable(f"kernels are built for gfx950, device is {arch}")
+        try:
+            self.lib = _lib.load()
+        except (OSError, RuntimeError) as exc:
+            raise BackendUnavailable(f"libclarus_hip.so: {exc}") from exc
+        self.dev = dev
+
+    # ------------------------------------------------------------------ plumbing
+    def cached(self, t: torch.Tensor, tag: str, fn):
+        """Weight re-layout computed once per (tensor, tag).
+
+        Keyed like the base class on the storage address, plus strides and dtype, and the entry
+        keeps a reference to the source tensor: while an entry lives its address cannot be
+        recycled by the caching allocator for a different weight, and an in-place update of the
+        weight (its version counter) recomputes the entry."""
+        key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, tag)
+        hit = self._cache.get(key)
+        if hit is None or hit[1] != t._version:
+            hit = (t, t._version, fn(t))
+            self._cache[key] = hit
+        return hit[2]
+
+    def _stream(self, t: torch.Tensor) -> int:
+        return torch.cuda.current_stream(t.device).cuda_stream
+
+    def _bias(self, b):
+        """fp32 contiguous copy of a (weight-like) vector, once per tensor."""
+        if b is None:
+            return None
+        if b.dtype == torch.float32 and b.is_contiguous():
+            return b
+        return self.cached(b, "f32", lambda t: t.float().contiguous())
+
+    def _wt(self, w: torch.Tensor) -> torch.Tensor:
+        """[K, N] weight -> W^T [N, K] (K contiguous), kept in its dtype."""
+        return self.cached(w, "wt", lambda t: t.t().contiguous())
+
+    def _mats(self, device):
+        key = ("dft8", str(device))
+        m = self._cache.get(key)
+        if m is None:
+            fwd, inv = dft_matrices(8)
+            m = (torch.tensor(fwd, dtype=torch.float32, device=device).contiguous(),
+                 torch.tensor(inv, dtype=torch.float32, device=device).contiguous())
+            self._cache[key] = m
+        return m
+
+    def _gemm(self, what, *, a, wt, c, m, n, k, lda, ldc, bias=None, scale=None, res=None, ldr=0,
+              gate=False, act=0, pro=0, a_mode=0, c_mode=0, batch=1, a_bs=0, w_bs=0, c_bs=0, r_bs=0,
+              small=None, geom=(0, 0, 0, 0, 0, 0), m2=None, ldm2=0, lnw=None, lnb=None, m2_act=0,
+              ln_eps=1e-6, out_scale=1.0, tile=0):
+        h, w, oh, ow, pt, pl = geom
+        args = _lib.GemmArgs(
+            a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
+            res=_lib.ptr(res), small=_lib.ptr(small), m2=_lib.ptr(m2), lnw=_lib.ptr(lnw), lnb=_lib.ptr(lnb),
+            m=m, n=n, k=k, batch=batch, lda=lda, ldc=ldc, ldr=ldr, ldm2=ldm2,
+            a_bstride=a_bs, w_bstride=w_bs, c_bstride=c_bs, r_bstride=r_bs,
+            a_dtype=_lib.dtype_code(a.dtype), w_dtype=_lib.dtype_code(wt.dtype), c_dtype=_lib.dtype_code(c.dtype),
+            r_dtype=_lib.dtype_code(res.dtype) if res is not None else 0,
+            s_dtype=_lib.dtype_code(small.dtype) if small is not None else 0,
+            m2_dtype=_lib.dtype_code(m2.dtype) if m2 is not None else 0,
+            h=h, w=w, oh=oh, ow=ow, pt=pt, pl=pl, pro=pro, a_mode=a_mode, c_mode=c_mode, gate=int(gate),
+            act=act, m2_act=m2_act, ln_eps=ln_eps, out_scale=out_scale, slope=0.0, tile=tile)
+        _lib.check(self.lib.clarus_hip_gemm(ctypes.byref(args), self._stream(a)), what)
+        return c
+
+    # ------------------------------------------------------------------ GEMMs
+    def linear(self, x, w, bias=None, ln=False, act=None, gate=False, scale=None,
+               residual=None, mul=None, out_dtype=None, ln_eps=1e-6):
+        if is_small(x):
+            return x.with_data(self.linear(x.data, w, bias, ln, act, gate, scale, residual, mul, out_dtype, ln_eps))
+        if ln and mul is not None:
+            raise Unsupported("linear: LayerNorm and mul prologues together")
+        if act not in (None, "gelu") or ln not in (False, True, "rms"):
+            raise Unsupported(f"linear: act={act!r} ln={ln!r}")
+        n, h, wd, k = x.shape
+        if gate and w.shape[1] % 2:
+            raise Unsupported("linear: gate needs an even number of weight columns")
+        nout = w.shape[1] // 2 if gate else w.shape[1]
+        odt = out_dtype or self.dtype
+        sm = mul.data if mul is not None else None
+        if not (_dense(x, w, bias, scale) and _same(residual, (n, h, wd, nout))
+                and (sm is None or (sm.is_contiguous() and tuple(sm.shape[::3]) == (n, k)
+                                    and (mul.H, mul.W) == (h, wd)))):
+            raise Unsupported("linear: contiguous x / weights / mul map, residual of the output's shape")
+        if not (_kdt(x, w, residual, sm) and odt in _KDT and w.shape[0] == k and k % 8 == 0
+                and _vec16(x) and (sm is None or _vec16(sm))):
+            raise Unsupported("linear: bf16 / fp32 operands, K % 8 == 0, 16-byte aligned rows")
+        out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
+        if out.numel() == 0:
+            return out
+        pro = _lib.PRO_NONE
+        geom = (0, 0, 0, 0, 0, 0)
+        if ln:
+            pro = _lib.PRO_RMS if ln == "rms" else _lib.PRO_LN
+        elif sm is not None:
+            pro = _lib.PRO_MUL
+            geom = (h, wd, sm.shape[1], sm.shape[2], mul.pt, mul.pl)
+        return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=n * h * wd, n=nout, k=k, lda=k, ldc=nout,
+                          bias=self._bias(bias), scale=self._bias(scale), res=residual, ldr=nout, gate=gate,
+                          act=_lib.ACT_GELU if act == "gelu" else 0, pro=pro, small=sm, geom=geom,
+                          ln_eps=float(ln_eps))
+
+    def down(self, x, w4d, b, out_dtype=None):
+        if tuple(w4d.shape[-2:]) != (2, 2) or not _dense(x, b):
+            raise Unsupported("down: only 2x2 stride-2 convs, contiguous input")
+        n, h, wd, c = x.shape
+        cout = w4d.shape[0]
+        odt = out_dtype or self.dtype
+        if not (_kdt(x, w4d) and odt in _KDT and w4d.shape[1] == c and c % 8 == 0 and h >= 2 and wd >= 2
+                and _vec16(x)):
+            raise Unsupported("down: bf16 / fp32, cin % 8 == 0, at least 2x2 input")
+        wt = self.cached(w4d, "s2d", lambda t: t.permute(0, 2, 3, 1).reshape(t.shape[0], -1).contiguous())
+        out = torch.empty((n, h // 2, wd // 2, cout), device=x.device, dtype=odt)
+        return self._gemm("down", a=x, wt=wt, c=out, m=n * (h // 2) * (wd // 2), n=cout, k=4 * c, lda=c, ldc=cout,
+                          bias=self._bias(b), a_mode=_lib.A_S2D, geom=(h, wd, 0, 0, 0, 0))
+
+    def up(self, x, w, residual=None, out_dtype=None):
+        n, h, wd, c = x.shape
+        cq = w.shape[1] // 4
+        if w.shape[1] % 16 or not (_dense(x, w) and _same(residual, (n, 2 * h, 2 * wd, cq))):
+            raise Unsupported("up: 4 C' % 16 == 0, contiguous x, residual of the output's shape")
+        odt = out_dtype or self.dtype
+        if not (_kdt(x, w, residual) and odt in _KDT and w.shape[0] == c and c % 8 == 0 and _vec16(x)):
+            raise Unsupported("up: bf16 / fp32, K % 8 == 0")
+        out = torch.empty((n, 2 * h, 2 * wd, cq), device=x.device, dtype=odt)
+        return self._gemm("up", a=x, wt=self._wt(w), c=out, m=n * h * wd, n=4 * cq, k=c, lda=c, ldc=4 * cq,
+                          res=residual, c_mode=_lib.C_SHUFFLE, geom=(h, wd, 0, 0, 0, 0))
+
+    # ------------------------------------------------------------------ convolutions
+    def _conv_wt(self, w):
+        return self.cached(w, "conv3", lambda t: t.permute(0, 2, 3, 1).reshape(t.shape[0], -1).contiguous())
+
+    def intro(self, inp, w, b, out_dtype=None):
+        if tuple(w.shape[1:]) != (3, 3, 3) or b is None or inp.dim() != 4 or inp.shape[1] != 3:
+            raise Unsupported("intro: 3-channel input, 3x3, bias")
+        odt = out_dtype or self.dtype
+        if odt not in _KDT:
+            raise Unsupported("intro: bf16 / fp32 output")
+        n, _, h, wd = inp.shape
+        cout = w.shape[0]
+        x = inp if (inp.dtype == torch.float32 and inp.is_contiguous()) else inp.float().contiguous()
+        wt = self.cached(w, "intro", lambda t: t.permute(2, 3, 1, 0).reshape(27, t.shape[0]).float().contiguous())
+        out = torch.empty((n, h, wd, cout), device=inp.device, dtype=odt)
+        _lib.check(self.lib.clarus_hip_intro3x3(x.data_ptr(), wt.data_ptr(), self._bias(b).data_ptr(),
+                                                out.data_ptr(), _lib.dtype_code(odt), n, h, wd, cout,
+                                                self._stream(x)), "intro")
+        return out
+
+    def _conv(self, x, w, b, *, odt, act, residual, out_scale, up2, out, slope, nchw=False):
+        n, h, wd, cin = x.shape
+        cout = w.shape[0]
+        hh, ww = (2 * h, 2 * wd) if up2 else (h, wd)
+        if out is None:
+            shape = (n, cout, hh, ww) if nchw else (n, hh, ww, cout)
+            out = torch.empty(shape, device=x.device, dtype=odt)
+        args = _lib.ConvArgs(
+            x=x.data_ptr(), wt=self._conv_wt(w).data_ptr(), out=out.data_ptr(), bias=_lib.ptr(self._bias(b)),
+            res=_lib.ptr(residual), batch=n, h=h, w=wd, cin=cin, cout=cout, ldx=x.stride(2),
+            ldo=0 if nchw else out.stride(2), ldr=(residual.stride(2) if (residual is not None and not nchw) else 0),
+            x_dtype=_lib.dtype_code(x.dtype), w_dtype=_lib.dtype_code(w.dtype), o_dtype=_lib.dtype_code(out.dtype),
+            r_dtype=_lib.dtype_code(residual.dtype) if residual is not None else 0,
+            act=_lib.ACT_LRELU if act == "lrelu" else 0, up2=int(bool(up2)),
+            c_mode=_lib.C_NCHW if nchw else _lib.C_ROWS, out_scale=float(out_scale), slope=float(slope), tile=0)
+        _lib.check(self.lib.clarus_hip_conv3x3(ctypes.byref(args), self._stream(x)), "conv3x3")
+        return out
+
+    def ending(self, x, w, b, inp):
+        n, h, wd, cin = x.shape
+        if (tuple(w.shape[-2:]) != (3, 3) or tuple(inp.shape) != (n, w.shape[0], h, wd) or b is None
+                or not _pix_rows(x)):
+            raise Unsupported("ending: 3x3 with global residual of the output's shape, NHWC rows")
+        if not (_kdt(x, w) and w.shape[1] == cin and cin % 8 == 0 and _vec16(x, x.stride(2))):
+            raise Unsupported("ending: bf16 / fp32, cin % 8 == 0, 16-byte pixel rows")
+        res = inp if (inp.dtype == torch.float32 and inp.is_contiguous()) else inp.float().contiguous()
+        return self._conv(x, w, b, odt=torch.float32, act=None, residual=res, out_scale=1.0, up2=False, out=None,
+                          slope=0.2, nchw=True)
+
+    def conv3x3(self, x, w, b=None, out_dtype=None, act=None, residual=None, out_scale=1.0, up2=False,
+                out=None, slope=0.2):
+        n, h, wd, cin = x.shape
+        oshape = (n, 2 * h, 2 * wd, w.shape[0]) if up2 else (n, h, wd, w.shape[0])
+        if act not in (None, "lrelu") or tuple(w.shape[-2:]) != (3, 3) or w.shape[1] != cin:
+            raise Unsupported("conv3x3: 3x3, activation none / lrelu")
+        if not (_pix_rows(x) and all(t is None or (tuple(t.shape) == oshape and _pix_rows(t)) for t in (residual, out))):
+            raise Unsupported("conv3x3: NHWC tensors with a uniform pixel stride, residual / out of the output's shape")
+        odt = out.dtype if out is not None else (out_dtype or self.dtype)
+        if not (_kdt(x, w, residual) and odt in _KDT and cin % 8 == 0 and _vec16(x, x.stride(2))):
+            raise Unsupported("conv3x3: bf16 / fp32, cin % 8 == 0, 16-byte pixel rows")
+        return self._conv(x, w, b, odt=odt, act=act, residual=residual, out_scale=out_scale, up2=up2, out=out,
+                          slope=slope)
+
+    # ------------------------------------------------------------------ attention
+    def channel_attention(self, qkv, heads, temperature):
+        if not qkv.is_contiguous():
+            raise Unsupported("channel_attention: contiguous qkv only")
+        n, h, wd, c3 = qkv.shape
+        c = c3 // 3
+        if c3 % 3 or c % heads or not _kdt(qkv) or (c // heads) % 8 or c // heads > 64 or not _vec16(qkv, c):
+            raise Unsupported("channel_attention: head width a multiple of 8, <= 64; bf16 / fp32")
+        ch = c // heads
+        t = temperature.reshape(heads)
+        t = t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous()
+        need = self.lib.clarus_hip_channel_attention_workspace(n, h * wd, c, heads)
+        scratch = torch.empty(max(need, 16), dtype=torch.uint8, device=qkv.device)
+        out = torch.empty((n, heads, ch, ch), dtype=torch.float32, device=qkv.device)
+        _lib.check(self.lib.clarus_hip_channel_attention(qkv.data_ptr(), _lib.dtype_code(qkv.dtype), t.data_ptr(),
+                                                         out.data_ptr(), n, h * wd, c, heads, scratch.data_ptr(),
+                                                         scratch.numel(), self._stream(qkv)), "channel_attention")
+        return out
+
+    def linear_per_image(self, x, w, residual=None, out_dtype=None, bias=None):
+        n, h, wd, k = x.shape
+        nout = w.shape[-1]
+        if (x.stride(-1) != 1 or x.stride(1) != wd * x.stride(2) or tuple(w.shape[:2]) != (n, k)
+                or not (_dense(bias) and _same(residual, (n, h, wd, nout)))):
+            raise Unsupported("linear_per_image: NHWC rows with a uniform pixel stride, residual of the output's shape")
+        odt = out_dtype or self.dtype
+        if not (_kdt(x, w, residual) and odt in _KDT and k % 8 == 0 and _vec16(x, x.stride(2), x.stride(0))):
+            raise Unsupported("linear_per_image: bf16 / fp32, K % 8 == 0, 16-byte rows")
+        out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
+        wt = w.transpose(1, 2).contiguous()  # per-image weights change every call: not cached
+        return self._gemm("linear_per_image", a=x, wt=wt, c=out, m=h * wd, n=nout, k=k, lda=x.stride(2), ldc=nout,
+                          bias=self._bias(bias), res=residual, ldr=nout, batch=n, a_bs=x.stride(0),
+                          w_bs=nout * k, c_bs=h * wd * nout, r_bs=h * wd * nout)
+
+    # ------------------------------------------------------------------ frequency ops
+    def patch_filter(self, x, f, residual=None, out_dtype=None):
+        n, h, wd, c = x.shape
+        pad_h, pad_w = (-h) % 8, (-wd) % 8
+        if (f.dim() != 3 or tuple(f.shape) != (c, 8, 5) or not _pix_rows(x) or not _same(residual, (n, h, wd, c))
+                or (pad_h and pad_h >= h) or (pad_w and pad_w >= wd)):
+            raise Unsupported("patch_filter: 8x8 patches, NHWC rows, residual of the output's shape")
+        odt = out_dtype or self.dtype
+        if not (_kdt(x, residual) and odt in _KDT):
+            raise Unsupported("patch_filter: bf16 / fp32")
+        fwd, inv = self._mats(x.device)
+        gain = self.cached(f, "gain", lambda t: t.float().reshape(t.shape[0], -1).repeat_interleave(2, dim=1)
+                           .contiguous())
+        out = torch.empty((n, h, wd, c), device=x.device, dtype=odt)
+        _lib.check(self.lib.clarus_hip_patch_filter(
+            x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(2), fwd.data_ptr(), inv.data_ptr(), gain.data_ptr(),
+            _lib.ptr(residual), _lib.dtype_code(residual.dtype) if residual is not None else 0, out.data_ptr(),
+            _lib.dtype_code(odt), n, h, wd, c, self._stream(x)), "patch_filter")
+        return out
+
+    def linear_patch_filter(self, x, w, bias, f, ln=False, ln_eps=1e-6, residual=None):
+        n, h, wd, k = x.shape
+        if (tuple(f.shape[1:]) != (8, 5) or f.shape[0] != w.shape[1] or min(h, wd) < 9 or bias is None
+                or x.dtype != self.dtype or not _dense(x, w, bias) or not _same(residual, (n, h, wd, w.shape[1]))):
+            raise Unsupported("linear_patch_filter: 8x8 patches, H, W >= 9, contiguous, bias, x in the compute "
+                              "dtype, residual of the output's shape")
+        y = self.linear(x, w, bias, ln=ln, ln_eps=ln_eps, out_dtype=torch.float32)
+        return self.patch_filter(y, f, residual=residual)
+
+    def patch_corr(self, x, c, p=8):
+        n, h, w, cx = x.shape
+        if p != 8 or h % 8 or w % 8 or x.stride(-1) != 1 or cx < 2 * c or not _kdt(x):
+            raise Unsupported("patch_corr: 8x8 patches, H and W multiples of 8, unit channel stride, >= 2c channels")
+        fwd, inv = self._mats(x.device)
+        out = torch.empty((n, h, w, c), device=x.device, dtype=torch.float32)
+        _lib.check(self.lib.clarus_hip_patch_corr(x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), x.stride(1),
+                                                  x.stride(2), fwd.data_ptr(), inv.data_ptr(), out.data_ptr(), n, h,
+                                                  w, c, self._stream(x)), "patch_corr")
+        return out
+
+    def ln_mul_linear(self, x, ln_w, ln_b, m, w, bias=None, m_act=None, residual=None, ln_eps=1e-5,
+                      out_dtype=None):
+        n, h, wd, k = x.shape
+        if (not _dense(x, ln_w, ln_b, w, bias) or tuple(m.shape) != tuple(x.shape) or not _pix_rows(m)
+                or not _same(residual, (n, h, wd, w.shape[1]))):
+            raise Unsupported("ln_mul_linear: contiguous x, NHWC m with a uniform pixel stride, "
+                              "residual of the output's shape")
+        odt = out_dtype or self.dtype
+        if not (_kdt(x, m, w, residual) and odt in _KDT and m_act in (None, "gelu") and k % 8 == 0
+                and _vec16(x) and _vec16(m, m.stride(2))):
+            raise Unsupported("ln_mul_linear: bf16 / fp32, K % 8 == 0, 16-byte rows")
+        out = torch.empty((n, h, wd, w.shape[1]), device=x.device, dtype=odt)
+        return self._gemm("ln_mul_linear", a=x, wt=self._wt(w), c=out, m=n * h * wd, n=w.shape[1], k=k, lda=k,
+                          ldc=w.shape[1], bias=self._bias(bias), res=residual, ldr=w.shape[1], pro=_lib.PRO_LNMUL,
+                          m2=m, ldm2=m.stride(2), lnw=self._bias(ln_w), lnb=self._bias(ln_b),
+                          m2_act=_lib.ACT_GELU if m_act == "gelu" else 0, ln_eps=float(ln_eps))

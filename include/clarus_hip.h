@@ -1,0 +1,191 @@
+/*
+ * clarus_hip.h - C ABI of libclarus_hip.so, the MI355X (gfx950) kernels behind the `hip`
+ * operator backend of clarus.
+ *
+ * The reference has no native FFI on this path: its Python adapter
+ * (python/clarus/ops/triton_cuda.py) calls Triton launch wrappers. Each entry point below
+ * replaces one of those wrappers (cited per function); the Python adapter
+ * clarus_amd/hip_ops.py binds them with ctypes. Conventions:
+ *
+ *   - Plain device pointers, int64 sizes and strides in ELEMENTS, dtype codes, and an opaque
+ *     stream (a hipStream_t passed as void*; NULL = the null stream).
+ *   - The library owns no device memory. Scratch space (split-K partials) is passed in.
+ *   - Every call validates its arguments before launching anything and returns 0 on success,
+ *     CLARUS_EINVAL for arguments the kernels do not handle, or CLARUS_ELAUNCH when the HIP
+ *     launch failed. clarus_hip_last_error() describes the last failure of the calling thread.
+ *   - No call synchronizes, allocates or loads modules, so all of them may be recorded into a
+ *     HIP graph.
+ *   - Activations are NHWC. A "pixel stride" is the element distance between consecutive
+ *     pixels, which lets an operand be a channel slice of a wider NHWC buffer.
+ */
+#ifndef CLARUS_HIP_H
+#define CLARUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CLARUS_HIP_ABI_VERSION 1
+
+/* return codes */
+#define CLARUS_OK 0
+#define CLARUS_EINVAL 1
+#define CLARUS_ELAUNCH 2
+
+/* element types */
+#define CLARUS_F32 0
+#define CLARUS_BF16 1
+
+/* prologue on A, applied in fp32 before the product (python/clarus/kernels/gemm.py:5-10) */
+#define CLARUS_PRO_NONE 0  /* a                                                   */
+#define CLARUS_PRO_LN 1    /* (a - mean) * rstd over the K channels (eps ln_eps)   */
+#define CLARUS_PRO_MUL 2   /* a * S[clamp(y - pt), clamp(x - pl), k] (TLC map)      */
+#define CLARUS_PRO_RMS 3   /* a * rsqrt(mean(a^2) + eps)                            */
+#define CLARUS_PRO_LNMUL 5 /* ((a - mean) * rstd * lnw[k] + lnb[k]) * act(m2[p, k]) */
+
+/* A addressing */
+#define CLARUS_A_ROWS 0  /* row p at a + p * lda                                    */
+#define CLARUS_A_S2D 1   /* 2x2 stride-2 conv: K = (dy, dx, cin), input [*, h, w, K/4] */
+
+/* C addressing */
+#define CLARUS_C_ROWS 0    /* out[p * ldc + n]                                      */
+#define CLARUS_C_SHUFFLE 1 /* PixelShuffle(2): N = (dy, dx, c'), output [*, 2h, 2w, N/4] */
+#define CLARUS_C_NCHW 2    /* out[((img * N + n) * h + y) * w + x] (conv only)      */
+
+/* activations */
+#define CLARUS_ACT_NONE 0
+#define CLARUS_ACT_GELU 1  /* exact erf GELU                                        */
+#define CLARUS_ACT_LRELU 2 /* LeakyReLU(slope)                                      */
+
+/*
+ * Fused NHWC GEMM:  out[p, n] = epilogue( prologue(A)[p, :] . W[:, n] ), fp32 accumulation.
+ *
+ * W is passed TRANSPOSED, wt[n_cols][k] with k contiguous (n_cols = 2n when gate), in bf16
+ * or fp32. Operand handling (chosen by the library from the dtypes and the prologue):
+ *   bf16 A, no prologue, bf16 W  -> bf16 MFMA (products exact in fp32)
+ *   fp32 A or a prologue, bf16 W -> A split into bf16 hi + lo, two bf16 MFMAs
+ *   any A, fp32 W                -> fp32 MFMA
+ * Epilogue order (python/clarus/ops/torch_ref.py:119-131):
+ *   + bias[n] (and bias[n + N] on the gate half) -> SimpleGate o1 * o2 -> act -> * scale[n]
+ *   -> * out_scale -> + residual -> cast to c_dtype.
+ * batch > 1 runs `batch` independent GEMMs of m rows (linear_per_image) using the batch strides.
+ * out may alias residual exactly (same pointer and strides).
+ */
+typedef struct ClarusGemmArgs {
+  const void* a;
+  const void* wt;
+  void* c;
+  const float* bias;  /* [n] or [2n] with gate; NULL for none        */
+  const float* scale; /* [n]; NULL for none                          */
+  const void* res;    /* residual addressed like the output; NULL    */
+  const void* small;  /* PRO_MUL map [batch, oh, ow, k]              */
+  const void* m2;     /* PRO_LNMUL multiplier rows, pixel stride ldm2 */
+  const float* lnw;   /* PRO_LNMUL LayerNorm affine [k]              */
+  const float* lnb;
+  int64_t m;          /* rows (output pixels) per batch entry         */
+  int64_t n;          /* output channels                              */
+  int64_t k;          /* reduction length                             */
+  int64_t batch;
+  int64_t lda, ldc, ldr, ldm2;       /* pixel strides (elements)        */
+  int64_t a_bstride, w_bstride, c_bstride, r_bstride; /* batch strides */
+  int32_t a_dtype, w_dtype, c_dtype, r_dtype, s_dtype, m2_dtype;
+  int32_t h, w;       /* A_S2D: input size; C_SHUFFLE: input size; PRO_MUL: image size */
+  int32_t oh, ow, pt, pl; /* PRO_MUL map geometry (torch_ref.py:18-41)                  */
+  int32_t pro, a_mode, c_mode, gate, act, m2_act;
+  float ln_eps, out_scale, slope;
+  int32_t tile;       /* 0 = library's choice; else a tile id for sweeps */
+} ClarusGemmArgs;
+
+/* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */
+int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
+
+/*
+ * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:
+ *   y = act(conv3x3(up2 ? nearest_x2(x) : x) + bias) * out_scale (+ residual)
+ * x [batch, h, w, cin] with pixel stride ldx (h, w = INPUT size); wt [cout][9 * cin] with
+ * the reduction ordered (ky, kx, cin). Output [batch, H, W, cout] (H = 2h with up2) with
+ * pixel stride ldo, or NCHW fp32 [batch, cout, H, W] with c_mode = CLARUS_C_NCHW (then the
+ * residual is NCHW too). cin must be a multiple of 8.
+ */
+typedef struct ClarusConvArgs {
+  const void* x;
+  const void* wt;
+  void* out;
+  const float* bias; /* [cout] or NULL */
+  const void* res;
+  int64_t batch, h, w, cin, cout;
+  int64_t ldx, ldo, ldr;
+  int32_t x_dtype, w_dtype, o_dtype, r_dtype;
+  int32_t act, up2, c_mode;
+  float out_scale, slope;
+  int32_t tile;
+} ClarusConvArgs;
+
+/* replaces kernels/conv3x3.py:123-168 conv3x3 (and the `ending` use of it) */
+int clarus_hip_conv3x3(const ClarusConvArgs* args, void* stream);
+
+/*
+ * 3 -> cout 3x3 conv (padding 1) from an NCHW fp32 image [batch, 3, h, w] to NHWC
+ * [batch, h, w, cout]; wt [27][cout] fp32 ordered (ky, kx, c); bias [cout] fp32.
+ * replaces kernels/conv3x3.py:196-204 intro3x3
+ */
+int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, void* out,
+                        int32_t out_dtype, int64_t batch, int64_t h, int64_t w, int64_t cout,
+                        void* stream);
+
+/*
+ * Restormer MDTA attention map (python/clarus/ops/torch_ref.py:220-235):
+ *   A[n, hd] = softmax((q / |q|) (k / |k|)^T * temperature[hd]) over c_h x c_h,
+ * norms over all pixels. qkv [batch, h, w, 3c] contiguous (q | k | v channel blocks),
+ * dtype qkv_dtype; out fp32 [batch, heads, c_h, c_h]; temperature fp32 [heads].
+ * The pixel reduction is split over workgroups (deterministic two-stage sum); scratch must
+ * hold clarus_hip_channel_attention_workspace(...) bytes.
+ * replaces kernels/attention.py:252-270 gram + ops/triton_cuda.py:174-181
+ */
+size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads);
+int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature,
+                                 float* out, int64_t batch, int64_t hw, int64_t c,
+                                 int64_t heads, void* scratch, size_t scratch_bytes,
+                                 void* stream);
+
+/*
+ * Per 8x8 patch and channel: y = irfft2(rfft2(patch) * g[c]) (+ residual), as the dense
+ * real products  y = Inv[64 x 80] . (g_c * (Fwd[80 x 64] . x))  on fp32 MFMA.
+ * fwd [80][64] and inv [64][80] fp32 (rows of re/im coefficients, see clarus_amd/dft.py);
+ * gain [c][80] fp32 (the filter per coefficient). x [batch, h, w, c] NHWC with pixel
+ * stride ldx; h, w multiples of 8 (the caller reflect-pads other sizes).
+ * out [batch, h, w, c] contiguous, dtype o_dtype; residual contiguous like out or NULL.
+ * replaces ops/torch_ref.py:253-270 patch_filter (torch-only in the reference)
+ */
+int clarus_hip_patch_filter(const void* x, int32_t x_dtype, int64_t ldx, const float* fwd,
+                            const float* inv, const float* gain, const void* res,
+                            int32_t r_dtype, void* out, int32_t o_dtype, int64_t batch,
+                            int64_t h, int64_t w, int64_t c, void* stream);
+
+/*
+ * FFTformer FSAS correlation (ops/torch_ref.py:278-288): per 8x8 patch,
+ * irfft2(rfft2(q) * rfft2(k)) with q = x[..., :c], k = x[..., c:2c]; x has unit channel
+ * stride and arbitrary batch / row / pixel strides (elements); out fp32 [batch, h, w, c].
+ * fwd [80][64], inv [64][80] as above.
+ * replaces kernels/freq.py:165-186 patch_corr
+ */
+int clarus_hip_patch_corr(const void* x, int32_t x_dtype, int64_t sn, int64_t sh, int64_t sw,
+                          const float* fwd, const float* inv, float* out, int64_t batch,
+                          int64_t h, int64_t w, int64_t c, void* stream);
+
+/* ABI version (CLARUS_HIP_ABI_VERSION) and struct sizes, for binding checks. */
+int clarus_hip_abi_version(void);
+size_t clarus_hip_sizeof_gemm_args(void);
+size_t clarus_hip_sizeof_conv_args(void);
+
+/* Text of the calling thread's last failure ("" if none). */
+const char* clarus_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLARUS_HIP_H */

@@ -1,0 +1,57 @@
+"""CPU: the C-ABI library loads, exports every entry point include/clarus_hip.h declares, its
+struct layouts match the ctypes binding, and argument validation rejects bad calls before any
+launch (those calls never touch a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from clarus_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "clarus_hip.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(clarus_hip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} is not built: run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_header_declares_the_bound_functions():
+    assert declared_functions() == sorted(_lib.SIGNATURES), "binding and header disagree"
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [f for f in declared_functions() if not hasattr(raw, f)]
+    assert not missing, missing
+
+
+def test_abi_version_and_struct_sizes(lib):
+    assert lib.clarus_hip_abi_version() == _lib.ABI_VERSION
+    assert lib.clarus_hip_sizeof_gemm_args() == ctypes.sizeof(_lib.GemmArgs)
+    assert lib.clarus_hip_sizeof_conv_args() == ctypes.sizeof(_lib.ConvArgs)
+
+
+def test_validation_rejects_before_launch(lib):
+    assert lib.clarus_hip_gemm(None, None) == _lib.EINVAL
+    assert b"null" in lib.clarus_hip_last_error()
+    a = _lib.GemmArgs(a=16, wt=16, c=16, m=10, n=8, k=12, batch=1, lda=12, ldc=8)
+    assert lib.clarus_hip_gemm(ctypes.byref(a), None) == _lib.EINVAL  # K % 8 != 0
+    assert b"multiple of 8" in lib.clarus_hip_last_error()
+    cv = _lib.ConvArgs(x=16, wt=16, out=16, batch=1, h=4, w=4, cin=12, cout=8, ldx=12, ldo=8)
+    assert lib.clarus_hip_conv3x3(ctypes.byref(cv), None) == _lib.EINVAL  # cin % 8 != 0
+    assert lib.clarus_hip_channel_attention(16, 1, 16, 16, 1, 64, 30, 2, 16, 0, None) == _lib.EINVAL
+    assert lib.clarus_hip_patch_corr(16, 0, 0, 0, 0, 16, 16, 16, 1, 12, 16, 8, None) == _lib.EINVAL  # h % 8
+    assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
+    assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0

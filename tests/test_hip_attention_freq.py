@@ -1,0 +1,144 @@
+"""GPU parity: Restormer channel attention (split-K Gram + norms + softmax) and the FFTformer
+patch-DFT ops (patch_filter, linear_patch_filter, patch_corr) vs the oracle.
+
+Cases follow tools/test_kernels.py:200-208,237-247, tools/test_ops_contracts.py:128-141 and
+BASELINE configs 3 (patch DFT at C = 48 / 96 / 192, 720p / 360p / 180p) and 4 (MDTA levels).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _tol import assert_bf16, assert_fp32
+from oracle.torch_ref import TorchRef
+
+pytestmark = pytest.mark.gpu
+REF = TorchRef(torch.float32, "cpu")
+
+
+@pytest.fixture(scope="module")
+def hip_bf16(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.bfloat16, gpu_device)
+
+
+@pytest.fixture(scope="module")
+def hip_f32(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.float32, gpu_device)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rnd(g, *shape, scale=1.0, dtype=torch.float32):
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+# ------------------------------------------------------------------ channel attention
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_channel_attention_small(dt, hip_bf16, hip_f32):
+    """tools/test_kernels.py:200-208 shape: n=2, 21x34, 4 heads of 48 channels."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(1)
+    heads, ch = 4, 48
+    qkv = rnd(g, 2, 21, 34, 3 * heads * ch, dtype=dt)
+    t = torch.rand(heads, generator=g) * 1.5 + 0.5
+    got = hip.channel_attention(qkv.cuda(), heads, t.cuda())
+    ref = REF.channel_attention(qkv, heads, t)
+    assert_fp32(got.cpu(), ref, rel=1e-5, what=f"channel_attention {dt}")
+    assert torch.allclose(got.sum(-1).cpu(), torch.ones(2, heads, ch), atol=1e-5)
+
+
+@pytest.mark.parametrize("ch", [8, 24, 64])
+def test_channel_attention_head_widths(ch, hip_f32):
+    g = gen(2)
+    heads = 2
+    qkv = rnd(g, 1, 17, 23, 3 * heads * ch)
+    t = torch.rand(heads, generator=g) + 0.5
+    assert_fp32(hip_f32.channel_attention(qkv.cuda(), heads, t.cuda()).cpu(), REF.channel_attention(qkv, heads, t),
+                rel=1e-5, what=f"channel_attention ch{ch}")
+
+
+CONFIG4 = [(0, 720, 1280), (1, 360, 640), (2, 180, 320), (3, 90, 160)]
+
+
+@pytest.mark.parametrize("lvl,h,w", CONFIG4)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_config4_mdta(lvl, h, w, dt, hip_bf16, hip_f32):
+    """BASELINE config 4 at level l: C = 48 * 2^l, heads 2^l, HW = 921600 / 4^l; Q, K, V from
+    N(0, 1); temperature U(0.5, 2). Attention map, then attn . V as the per-image mix
+    (blockdiag(A^T), the Restormer fold) through linear_per_image."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(40 + lvl)
+    c, heads = 48 * 2 ** lvl, 2 ** lvl
+    qkv = rnd(g, 1, h, w, 3 * c, dtype=dt)
+    t = torch.rand(heads, generator=g) * 1.5 + 0.5
+    a = hip.channel_attention(qkv.cuda(), heads, t.cuda())
+    ra = REF.channel_attention(qkv, heads, t)
+    assert_fp32(a.cpu(), ra, rel=1e-5 if dt == torch.float32 else 1e-4, what=f"mdta attention l{lvl} {dt}")
+    bd = torch.zeros(1, c, c)
+    for hh in range(heads):
+        bd[:, hh * 48:(hh + 1) * 48, hh * 48:(hh + 1) * 48] = ra[:, hh].transpose(1, 2)
+    got = hip.linear_per_image(qkv.cuda()[..., 2 * c:], bd.cuda(), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.linear_per_image(qkv[..., 2 * c:], bd, out_dtype=torch.float32), rel=1e-5,
+                what=f"mdta attn.V l{lvl} {dt}")
+
+
+# ------------------------------------------------------------------ patch DFT ops
+@pytest.mark.parametrize("h,w", [(64, 96), (45, 81), (16, 8)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_patch_filter(h, w, dt, hip_bf16, hip_f32):
+    """Non-symmetric random filter (irfft2's v = 0 / 4 handling matters), reflect padding for
+    sizes that are not multiples of 8, residual."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(3)
+    c = 40
+    x, f, res = rnd(g, 2, h, w, c, dtype=dt), rnd(g, c, 8, 5), rnd(g, 2, h, w, c, dtype=dt)
+    got = hip.patch_filter(x.cuda(), f.cuda(), residual=res.cuda(), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.patch_filter(x, f, residual=res), rel=1e-5, what=f"patch_filter {h}x{w} {dt}")
+
+
+CONFIG3 = [(48, 720, 1280), (96, 360, 640), (192, 180, 320)]
+
+
+@pytest.mark.parametrize("c,h,w", CONFIG3)
+def test_config3_patch_filter(c, h, w, hip_f32):
+    """fp32 patches [1, C, H/8, W/8, 8, 8] (stored NHWC), fwd DFT 64 -> 80,
+    seeded frequency-domain filter, inverse 80 -> 64."""
+    g = gen(30 + c)
+    x, f = torch.randn(1, h, w, c, generator=g), torch.randn(c, 8, 5, generator=g)
+    got = hip_f32.patch_filter(x.cuda(), f.cuda())
+    assert_fp32(got.cpu(), REF.patch_filter(x, f), rel=1e-5, what=f"config3 C{c}")
+
+
+@pytest.mark.parametrize("h,w,k,nout,ln,res", [(64, 96, 48, 288, True, False), (40, 64, 192, 256, True, False),
+                                               (90, 45, 144, 48, False, True), (52, 76, 96, 96, "rms", True)])
+def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
+    """tools/test_kernels.py:237-245 cases."""
+    g = gen(4)
+    x, f = rnd(g, 1, h, w, k).bfloat16(), rnd(g, nout, 8, 5)
+    wl, b = rnd(g, k, nout, scale=k ** -0.5).bfloat16(), rnd(g, nout)
+    rr = rnd(g, 1, h, w, nout).bfloat16() if res else None
+    got = hip_bf16.linear_patch_filter(x.cuda(), wl.cuda(), b.cuda(), f.cuda(), ln=ln, ln_eps=1e-5,
+                                       residual=rr.cuda() if res else None)
+    ref = REF.linear_patch_filter(x, wl, b, f, ln=ln, ln_eps=1e-5, residual=rr)
+    assert_bf16(got.cpu(), ref, f"linear_patch_filter {h}x{w} k{k} ln={ln}")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_patch_corr(dt, hip_bf16, hip_f32):
+    """tools/test_kernels.py:246-247 (q, k channel slices) and the stride cases of
+    tools/test_ops_contracts.py:128-141 (batch stride 2HWC, batch stride 0, channel slice,
+    H/W-transposed view)."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(5)
+    x = rnd(g, 2, 64, 96, 288, dtype=dt)
+    assert_fp32(hip.patch_corr(x.cuda(), 96).cpu(), REF.patch_corr(x, 96), rel=1e-5, what=f"patch_corr {dt}")
+    c = 32
+    base = rnd(g, 4, 16, 24, 2 * c + 16, dtype=dt)
+    bd = base.cuda()
+    for name, fn in [("batch stride 2HWC", lambda t: t[::2]), ("batch stride 0", lambda t: t[:1].expand(3, -1, -1, -1)),
+                     ("channel slice", lambda t: t[..., 8:8 + 2 * c]), ("H/W transposed", lambda t: t.transpose(1, 2))]:
+        assert_fp32(hip.patch_corr(fn(bd), c).cpu(), REF.patch_corr(fn(base), c), rel=1e-5, what=f"patch_corr {name}")

@@ -1,0 +1,143 @@
+"""GPU parity: implicit-GEMM 3x3 convolutions (conv3x3, ending) and intro vs the oracle.
+
+Cases follow tools/test_kernels.py:134-191 (channel-slice in / out, LeakyReLU, out_scale,
+residual, nearest-x2 input, NCHW fp32 ending with global residual, intro 3 -> C) and BASELINE
+config 5 (RRDBNet dense block convs on a 256x384 feature map and the x2 up-convs).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _tol import assert_bf16, assert_fp32
+from oracle.torch_ref import TorchRef
+
+pytestmark = pytest.mark.gpu
+REF = TorchRef(torch.float32, "cpu")
+
+
+@pytest.fixture(scope="module")
+def hip_bf16(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.bfloat16, gpu_device)
+
+
+@pytest.fixture(scope="module")
+def hip_f32(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.float32, gpu_device)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rnd(g, *shape, scale=1.0, dtype=torch.float32):
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def check(got, ref32, what):
+    if got.dtype == torch.bfloat16:
+        return assert_bf16(got, ref32, what)
+    return assert_fp32(got.float(), ref32, what=what)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_conv3x3_plain(dt, hip_bf16, hip_f32):
+    """cout 27 (no padding needed), odd sizes."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(1)
+    x, w, b = rnd(g, 2, 19, 27, 64, dtype=dt), rnd(g, 27, 64, 3, 3, scale=0.1, dtype=dt), rnd(g, 27)
+    got = hip.conv3x3(x.cuda(), w.cuda(), b.cuda(), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.conv3x3(x, w, b), what=f"conv3x3 cout27 {dt}")
+
+
+def test_conv3x3_slices_lrelu_scale_res(hip_bf16):
+    """Input / output channel slices of one buffer, LeakyReLU, out_scale, residual."""
+    g = gen(2)
+    n, h, w = 2, 21, 34
+    buf = rnd(g, n, h, w, 96, dtype=torch.bfloat16)
+    wt, b, res = rnd(g, 32, 64, 3, 3, scale=0.05, dtype=torch.bfloat16), rnd(g, 32), rnd(g, n, h, w, 32,
+                                                                                          dtype=torch.bfloat16)
+    ref = REF.conv3x3(buf[..., :64], wt, b, act="lrelu", out_scale=0.2, residual=res, out_dtype=torch.float32)
+    bd = buf.cuda()
+    got = hip_bf16.conv3x3(bd[..., :64], wt.cuda(), b.cuda(), act="lrelu", out_scale=0.2, residual=res.cuda(),
+                           out=bd[..., 64:])
+    assert got.data_ptr() == bd[..., 64:].data_ptr()
+    check(bd[..., 64:].cpu(), ref, "conv3x3 slice+lrelu+scale+res")
+    assert torch.equal(bd[..., :64].cpu(), buf[..., :64]), "input slice was modified"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_conv3x3_up2(dt, hip_bf16, hip_f32):
+    """Nearest-x2 upsample fused into the input addressing, cout 40."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(3)
+    x, w, b = rnd(g, 2, 21, 34, 48, dtype=dt), rnd(g, 40, 48, 3, 3, scale=0.05, dtype=dt), rnd(g, 40)
+    got = hip.conv3x3(x.cuda(), w.cuda(), b.cuda(), up2=True, act="lrelu")
+    check(got.cpu(), REF.conv3x3(x, w, b, up2=True, act="lrelu"), f"conv3x3 up2 {dt}")
+
+
+def test_ending_and_intro(hip_bf16):
+    """ending: fp32 input at |x| ~ 300, NCHW fp32 output + global residual; intro 3 -> 64 / 48."""
+    g = gen(4)
+    n, h, w = 2, 19, 27
+    x3 = torch.rand(n, 3, h, w, generator=g)
+    xe = rnd(g, n, h, w, 64, scale=300.0)
+    we, be = rnd(g, 3, 64, 3, 3, scale=0.1, dtype=torch.bfloat16), rnd(g, 3)
+    got = hip_bf16.ending(xe.cuda(), we.cuda(), be.cuda(), x3.cuda())
+    assert_fp32(got.cpu(), REF.ending(xe, we, be, x3), what="ending fp32-in NCHW + res")
+    for c in (64, 48):
+        wi, bi = rnd(g, c, 3, 3, 3, scale=0.3), rnd(g, c)
+        got = hip_bf16.intro(x3.cuda(), wi.cuda(), bi.cuda(), out_dtype=torch.float32)
+        assert_fp32(got.cpu(), REF.intro(x3, wi, bi, out_dtype=torch.float32), what=f"intro 3->{c}")
+
+
+@pytest.mark.parametrize("mag", [2.0 ** -18, 1.0, 6e4, 1e7])
+def test_conv3x3_fp32_input_range(mag, hip_bf16):
+    """fp32 input, bf16 weights, per-row relative vs float64 (tools/test_kernel_contracts.py:119-126)."""
+    g = gen(5)
+    x = rnd(g, 2, 10, 14, 48, scale=mag)
+    w = rnd(g, 32, 48, 3, 3, scale=0.1, dtype=torch.bfloat16)
+    got = hip_bf16.conv3x3(x.cuda(), w.cuda(), None, out_dtype=torch.float32).cpu().double().reshape(-1, 32)
+    ref = torch.nn.functional.conv2d(x.double().permute(0, 3, 1, 2), w.double(), padding=1)
+    ref = ref.permute(0, 2, 3, 1).reshape(-1, 32)
+    row_rel = ((got - ref).abs().amax(1) / ref.abs().amax(1)).max().item()
+    assert row_rel < 1e-4, row_rel
+
+
+def test_config5_dense_block(hip_bf16):
+    """one RRDB dense block on a 1x256x384 feature map (64 features, growth
+    32) inside one [1, 256, 384, 192] NHWC buffer, convs 64/96/128/160 -> 32 (+ LeakyReLU) into
+    the next slice, then 192 -> 64 * 0.2 + x into a second buffer. Weights kaiming-normal x 0.1."""
+    g = gen(0)
+    h, w = 256, 384
+    buf = torch.zeros(1, h, w, 192).bfloat16()
+    buf[..., :64] = torch.randn(1, h, w, 64, generator=g).bfloat16()
+    ws = []
+    for cin in (64, 96, 128, 160):
+        ws.append(((torch.randn(32, cin, 3, 3, generator=g) * (2.0 / (cin * 9)) ** 0.5) * 0.1).bfloat16())
+    w5 = ((torch.randn(64, 192, 3, 3, generator=g) * (2.0 / (192 * 9)) ** 0.5) * 0.1).bfloat16()
+    bs = [torch.zeros(32) for _ in range(4)] + [torch.zeros(64)]
+    ref_buf = buf.clone()
+    bd = buf.cuda()
+    for i, cin in enumerate((64, 96, 128, 160)):
+        hip_bf16.conv3x3(bd[..., :cin], ws[i].cuda(), bs[i].cuda(), act="lrelu", out=bd[..., cin:cin + 32])
+        r = REF.conv3x3(ref_buf[..., :cin], ws[i], bs[i], act="lrelu", out_dtype=torch.float32)
+        check(bd[..., cin:cin + 32].cpu(), r, f"config5 conv{i + 1} {cin}->32")
+        ref_buf[..., cin:cin + 32] = bd[..., cin:cin + 32].cpu()  # continue from identical inputs
+    out = torch.empty(1, h, w, 192, dtype=torch.bfloat16, device="cuda")
+    hip_bf16.conv3x3(bd, w5.cuda(), bs[4].cuda(), out_scale=0.2, residual=bd[..., :64], out=out[..., :64])
+    r = REF.conv3x3(ref_buf, w5, bs[4], out_scale=0.2, residual=ref_buf[..., :64], out_dtype=torch.float32)
+    check(out[..., :64].cpu(), r, "config5 conv5 192->64 *0.2 + x")
+
+
+@pytest.mark.parametrize("h,w", [(256, 384), (512, 768)])
+def test_config5_upconv(h, w, hip_bf16):
+    """BASELINE config 5 up-convs: nearest x2 + 3x3 64 -> 64 + LeakyReLU (out 512x768, 1024x1536)."""
+    g = gen(7)
+    x = torch.randn(1, h, w, 64, generator=g).bfloat16()
+    wt = ((torch.randn(64, 64, 3, 3, generator=g) * (2.0 / 576) ** 0.5) * 0.1).bfloat16()
+    b = torch.zeros(64)
+    got = hip_bf16.conv3x3(x.cuda(), wt.cuda(), b.cuda(), act="lrelu", up2=True)
+    check(got.cpu(), REF.conv3x3(x, wt, b, act="lrelu", up2=True, out_dtype=torch.float32), f"upconv {h}x{w}")

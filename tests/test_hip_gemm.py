@@ -1,0 +1,279 @@
+"""GPU parity: the HIP fused-GEMM ops (linear, down, up, ln_mul_linear, linear_per_image) vs the
+oracle (CPU restatement of the reference PyTorch backend) on seeded inputs.
+
+Cases follow the reference's own kernel tests (tools/test_kernels.py:53-98,209-219,249-258,
+tools/test_ops_contracts.py:76-111, tools/test_kernel_contracts.py:65-96) plus BASELINE
+configs 1 (fp32 NAFNet pointwise chain) and 2 (NAFNet-w64 720p pointwise GEMMs, bf16).
+Tolerances: tests/_tol.py (fp32: 1e-5 relative; bf16: 2e-2 absolute up to rounding flips).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from _tol import assert_bf16, assert_fp32
+from oracle.torch_ref import Small, TorchRef, box_geometry
+
+pytestmark = pytest.mark.gpu
+REF = TorchRef(torch.float32, "cpu")
+
+
+@pytest.fixture(scope="module")
+def hip_bf16(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.bfloat16, gpu_device)
+
+
+@pytest.fixture(scope="module")
+def hip_f32(gpu_device):
+    from clarus_amd.hip_ops import HipOps
+    return HipOps(torch.float32, gpu_device)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rnd(g, *shape, scale=1.0, dtype=torch.float32):
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def dev(*ts, device="cuda"):
+    return [None if t is None else t.to(device) for t in ts]
+
+
+def check(got, ref32, what):
+    if got.dtype == torch.bfloat16:
+        return assert_bf16(got, ref32, what)
+    return assert_fp32(got.float(), ref32, what=what)
+
+
+# --------------------------------------------------------------------- linear epilogues
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_linear_ln_gate_scale_res(dt, hip_bf16, hip_f32):
+    """tools/test_kernels.py:53-66 shape: LN + gate + scale + residual, odd M, N = 80."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(1)
+    n, h, w, k, c = 2, 13, 21, 96, 80
+    x, wt = rnd(g, n, h, w, k, dtype=dt), rnd(g, k, 2 * c, scale=0.1, dtype=dt)
+    b, sc, res = rnd(g, 2 * c), rnd(g, c), rnd(g, n, h, w, c, dtype=dt)
+    for odt in (None, torch.float32):
+        got = hip.linear(*dev(x, wt, b), ln=True, gate=True, scale=sc.cuda(), residual=res.cuda(), out_dtype=odt)
+        ref = REF.linear(x, wt, b, ln=True, gate=True, scale=sc, residual=res)
+        check(got.cpu(), ref, f"linear ln+gate+scale+res {dt} out {odt}")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("k,nout", [(96, 160), (48, 27), (256, 64), (40, 96)])
+def test_linear_gelu_and_shapes(dt, k, nout, hip_bf16, hip_f32):
+    """GELU epilogue (tools/test_kernels.py:68-70) over K / N tails (K % 32 != 0, N % 4 != 0)."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(2)
+    x, wt, b = rnd(g, 2, 13, 21, k, dtype=dt), rnd(g, k, nout, scale=0.1, dtype=dt), rnd(g, nout)
+    got = hip.linear(*dev(x, wt, b), act="gelu")
+    check(got.cpu(), REF.linear(x, wt, b, act="gelu"), f"linear gelu k{k} n{nout} {dt}")
+
+
+@pytest.mark.parametrize("k", [64, 96, 192, 512])
+@pytest.mark.parametrize("mode", [True, "rms"])
+def test_linear_layernorm(k, mode, hip_bf16):
+    """In-kernel two-pass LN / RMS over K (inline for every K), eps 1e-5 and 1e-6, on rows with
+    a large common offset (mean 30, std 1): exercises the two-pass variance."""
+    g = gen(3)
+    x = (30 + rnd(g, 2, 9, 11, k)).to(torch.bfloat16)
+    wt, b = rnd(g, k, 48, scale=k ** -0.5, dtype=torch.bfloat16), rnd(g, 48)
+    for eps in (1e-6, 1e-5):
+        got = hip_bf16.linear(*dev(x, wt, b), ln=mode, ln_eps=eps, out_dtype=torch.float32)
+        ref = REF.linear(x, wt, b, ln=mode, ln_eps=eps)
+        assert_fp32(got.cpu(), ref, rel=1e-4, what=f"linear ln={mode} k{k} eps{eps}")
+
+
+@pytest.mark.parametrize("k", [64, 256])
+def test_linear_mul_prologue(k, hip_bf16):
+    """TLC local-mean multiply fused into the prologue (tools/test_kernels.py:72-77) and the
+    large-magnitude case of tools/test_ops_contracts.py:87-95 (|x|, |S| ~ 20, |w| ~ 200)."""
+    g = gen(4)
+    n, h, w = 2, 13, 21
+    k1, k2, oh, ow, pt, pl = box_geometry(h, w, 8)
+    x = rnd(g, n, h, w, k, dtype=torch.bfloat16)
+    s = Small(rnd(g, n, oh, ow, k, dtype=torch.bfloat16), pt, pl, h, w)
+    wt = rnd(g, k, 40, scale=0.1, dtype=torch.bfloat16)
+    got = hip_bf16.linear(x.cuda(), wt.cuda(), mul=Small(s.data.cuda(), pt, pl, h, w), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.linear(x, wt, mul=s), rel=1e-5, what=f"linear mul k{k}")
+    # large magnitudes
+    x = (20 + rnd(g, n, 8, 12, k)).to(torch.bfloat16)
+    k1, k2, oh, ow, pt, pl = box_geometry(8, 12, (4, 4))
+    s = Small((20 + rnd(g, n, oh, ow, k)).to(torch.bfloat16), pt, pl, 8, 12)
+    wt = (200 + rnd(g, k, 32, scale=20)).to(torch.bfloat16)
+    sc = torch.full((32,), 1e-4)
+    got = hip_bf16.linear(x.cuda(), wt.cuda(), mul=Small(s.data.cuda(), pt, pl, 8, 12), scale=sc.cuda(),
+                          out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.linear(x, wt, mul=s, scale=sc), rel=1e-5, what=f"linear mul large k{k}")
+
+
+@pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
+def test_linear_range(k, nout, gate, hip_bf16):
+    """|x| ~ 400, |w| ~ 200, scale 1e-4 -> fp32 (tools/test_ops_contracts.py:76-86): bf16
+    products are exact in fp32, so the result matches the fp32 reference to summation order."""
+    g = gen(5)
+    x = (400 + rnd(g, 2, 8, 12, k, scale=40)).to(torch.bfloat16)
+    wt = (200 + rnd(g, k, 2 * nout if gate else nout, scale=20)).to(torch.bfloat16)
+    b = rnd(g, 2 * nout if gate else nout)
+    sc = torch.full((nout,), 1e-4)
+    got = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), gate=gate, out_dtype=torch.float32)
+    ref = REF.linear(x, wt, b, scale=sc, gate=gate)
+    assert_fp32(got.cpu(), ref, rel=1e-5, what=f"linear range k{k} n{nout} gate{gate}")
+
+
+def test_linear_known_answers(hip_bf16):
+    """Exact results (tools/test_kernel_contracts.py:65-96, tools/test_ops_contracts.py:108-111)."""
+    dv = "cuda"
+    # fp32 A through the hi/lo split: (256 * 1/16 * 16)^2 = 65536
+    x = torch.full((1, 1, 1, 16), 256.0, device=dv)
+    w = torch.full((16, 32), 1 / 16, device=dv, dtype=torch.bfloat16)
+    y = hip_bf16.linear(x, w, gate=True, out_dtype=torch.float32)
+    assert bool((y == 65536).all()), y.flatten()[:4]
+    # bf16 A: (2 * 1/16 * 16)^2 = 4
+    y = hip_bf16.linear(torch.full((1, 1, 1, 16), 2.0, device=dv, dtype=torch.bfloat16), w, gate=True,
+                        out_dtype=torch.float32)
+    assert bool((y == 4).all()), y.flatten()[:4]
+    # 16 * 2^-18 * 256 = 2^-6
+    y = hip_bf16.linear(torch.full((1, 1, 1, 16), 2.0 ** -18, device=dv),
+                        torch.full((16, 16), 256.0, device=dv, dtype=torch.bfloat16), out_dtype=torch.float32)
+    assert bool((y == 2.0 ** -6).all()), y.flatten()[:4]
+    # 400 * 200 * 64 * 1e-4 = 512
+    y = hip_bf16.linear(torch.full((1, 1, 1, 64), 400.0, device=dv, dtype=torch.bfloat16),
+                        torch.full((64, 4), 200.0, device=dv, dtype=torch.bfloat16),
+                        scale=torch.full((4,), 1e-4, device=dv), out_dtype=torch.float32)
+    assert bool((y == 512.0).all()), y.flatten()
+
+
+@pytest.mark.parametrize("mag", [2.0 ** -18, 1.0, 6e4, 1e7])
+def test_linear_fp32_input_range(mag, hip_bf16):
+    """fp32 A (the fp32 residual stream) x bf16 W at magnitudes 2^-18 .. 1e7, per-row relative
+    vs float64 (tools/test_kernel_contracts.py:91-134): the hi/lo split keeps ~16 bits of A."""
+    g = gen(6)
+    x = rnd(g, 2, 10, 14, 128, scale=mag)
+    w = rnd(g, 128, 96, scale=0.1, dtype=torch.bfloat16)
+    got = hip_bf16.linear(x.cuda(), w.cuda(), out_dtype=torch.float32).cpu().double().reshape(-1, 96)
+    ref = (x.double() @ w.double()).reshape(-1, 96)
+    row_rel = ((got - ref).abs().amax(1) / ref.abs().amax(1)).max().item()
+    assert row_rel < 1e-4, row_rel
+
+
+# --------------------------------------------------------------------- down / up
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hh,ww", [(14, 22), (15, 23)])
+def test_down(dt, hh, ww, hip_bf16, hip_f32):
+    """2x2 stride-2 conv as GEMM with space-to-depth A (tools/test_kernels.py:79-88); odd sizes floor."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(7)
+    x, w4, b = rnd(g, 2, hh, ww, 32, dtype=dt), rnd(g, 64, 32, 2, 2, scale=0.1, dtype=dt), rnd(g, 64)
+    got = hip.down(*dev(x, w4, b))
+    check(got.cpu(), REF.down(x, w4, b), f"down {hh}x{ww} {dt}")
+
+
+def test_down_fp32_input(hip_bf16):
+    """fp32 activations into a bf16-weight down conv (tools/test_kernels.py:154-163)."""
+    g = gen(8)
+    x, w4, b = rnd(g, 2, 18, 26, 32, scale=1000.0), rnd(g, 64, 32, 2, 2, scale=0.1, dtype=torch.bfloat16), rnd(g, 64)
+    got = hip_bf16.down(*dev(x, w4, b), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.down(x, w4, b), rel=1e-5, what="down fp32-in")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_up(dt, hip_bf16, hip_f32):
+    """1x1 conv + PixelShuffle(2) in the store addressing + residual (tools/test_kernels.py:90-98)."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(9)
+    n, hh, ww = 2, 14, 22
+    x = rnd(g, n, hh, ww, 32, dtype=dt)
+    wu = rnd(g, 4 * 48, 32, scale=0.1)  # torch layout [4C', C], out channel o = c*4 + dy*2 + dx
+    wkn = wu.reshape(48, 2, 2, 32).permute(1, 2, 0, 3).reshape(192, 32).t().contiguous().to(dt)
+    res = rnd(g, n, 2 * hh, 2 * ww, 48, dtype=dt)
+    got = hip.up(*dev(x, wkn), residual=res.cuda())
+    ref = REF.up(x, wkn, residual=res)
+    check(got.cpu(), ref, f"up {dt}")
+
+
+# --------------------------------------------------------------------- ln_mul_linear / per image
+def test_ln_mul_linear(hip_bf16):
+    """tools/test_kernels.py:251-258: m a channel slice; GELU(m) with fp32 x at 1e4."""
+    g = gen(10)
+    x, hid = rnd(g, 2, 20, 30, 96), rnd(g, 2, 20, 30, 288)
+    lw, lb, wl, b, res = rnd(g, 96), rnd(g, 96), rnd(g, 96, 48, scale=0.1), rnd(g, 48), rnd(g, 2, 20, 30, 48)
+    xb, hb, wb, rb = x.bfloat16(), hid.bfloat16(), wl.bfloat16(), res.bfloat16()
+    got = hip_bf16.ln_mul_linear(xb.cuda(), lw.cuda(), lb.cuda(), hb.cuda()[..., 192:], wb.cuda(), b.cuda(),
+                                 residual=rb.cuda())
+    check(got.cpu(), REF.ln_mul_linear(xb, lw, lb, hb[..., 192:], wb, b, residual=rb), "ln_mul_linear slice")
+    got = hip_bf16.ln_mul_linear((x * 1e4).cuda(), lw.cuda(), lb.cuda(), xb.cuda(), wb.cuda(), m_act="gelu",
+                                 out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.ln_mul_linear(x * 1e4, lw, lb, xb, wb, m_act="gelu"), rel=1e-4,
+                what="ln_mul_linear gelu fp32 x")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_linear_per_image(dt, hip_bf16, hip_f32):
+    """Per-image mix (Restormer attn.V folded into project_out): x a channel slice of qkv."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(11)
+    n, h, w, c = 2, 21, 34, 96
+    qkv = rnd(g, n, h, w, 3 * c, dtype=dt)
+    mix, b, res = rnd(g, n, c, c, scale=0.1), rnd(g, c), rnd(g, n, h, w, c, dtype=dt)
+    got = hip.linear_per_image(qkv.cuda()[..., 2 * c:], mix.cuda(), residual=res.cuda(), bias=b.cuda())
+    check(got.cpu(), REF.linear_per_image(qkv[..., 2 * c:], mix, residual=res, bias=b), f"linear_per_image {dt}")
+
+
+# --------------------------------------------------------------------- BASELINE configs 1 and 2
+def _kaiming_uniform(g, cout, cin):
+    bound = 1.0 / math.sqrt(cin)  # nn.Conv2d default init (kaiming_uniform_, a=sqrt(5)), 1x1 kernel
+    return (torch.rand(cout, cin, 1, 1, generator=g) * 2 - 1) * bound
+
+
+def config1_inputs():
+    g = gen(0)
+    x = torch.randn(1, 256, 256, 32, generator=g)
+    w1 = _kaiming_uniform(g, 64, 32)
+    b1 = torch.rand(64, generator=g) * 0.2 - 0.1
+    w2 = _kaiming_uniform(g, 32, 32)
+    b2 = torch.rand(32, generator=g) * 0.2 - 0.1
+    beta = torch.randn(32, generator=g) * 0.1
+    return x, w1.flatten(1).t().contiguous(), b1, w2.flatten(1).t().contiguous(), b2, beta
+
+
+def test_config1_fp32_chain(hip_f32):
+    """conv1x1 32->64 + bias + SimpleGate, conv1x1 32->32 + bias, * beta + x."""
+    x, w1, b1, w2, b2, beta = config1_inputs()
+    u = hip_f32.linear(*dev(x, w1, b1), gate=True)
+    y = hip_f32.linear(u, w2.cuda(), b2.cuda(), scale=beta.cuda(), residual=x.cuda())
+    ru = REF.linear(x, w1, b1, gate=True)
+    ry = REF.linear(ru, w2, b2, scale=beta, residual=x)
+    assert_fp32(u.cpu(), ru, what="config1 gate")
+    assert_fp32(y.cpu(), ry, what="config1 chain")
+
+
+CONFIG2 = [(64, 720, 1280), (128, 360, 640), (256, 180, 320), (512, 90, 160), (1024, 45, 80)]
+
+
+@pytest.mark.parametrize("c,h,w", CONFIG2)
+def test_config2_nafnet_gemms(c, h, w, hip_bf16):
+    """BASELINE config 2 at full 720p size: expand c->2c + bias + SimpleGate and c->c + bias
+    + beta * . + residual (fp32 residual / output from level 3, c >= 512)."""
+    g = gen(100 + c)
+    x = torch.randn(1, h, w, c, generator=g).bfloat16()
+    we = (_kaiming_uniform(g, 2 * c, c).flatten(1).t().contiguous()).bfloat16()
+    be = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+    u = hip_bf16.linear(*dev(x, we, be), gate=True)
+    ru32 = REF.linear(x, we, be, gate=True, out_dtype=torch.float32)
+    check(u.cpu(), ru32, f"config2 expand c{c}")
+    rdt = torch.float32 if c >= 512 else torch.bfloat16
+    res = torch.randn(1, h, w, c, generator=g).to(rdt)
+    wc = (_kaiming_uniform(g, c, c).flatten(1).t().contiguous()).bfloat16()
+    bc = torch.rand(c, generator=g) * 0.2 - 0.1
+    beta = torch.randn(c, generator=g) * 0.1
+    ub = ru32.bfloat16()  # the oracle's bf16 activation, so both sides see the same input
+    y = hip_bf16.linear(ub.cuda(), wc.cuda(), bc.cuda(), scale=beta.cuda(), residual=res.cuda(), out_dtype=rdt)
+    ry = REF.linear(ub, wc, bc, scale=beta, residual=res, out_dtype=torch.float32)
+    check(y.cpu(), ry, f"config2 c->c c{c}")
