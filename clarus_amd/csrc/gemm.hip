@@ -2,11 +2,22 @@
 // clarus_hip_intro3x3. Argument checks happen here, before any launch.
 #include "capi.hpp"
 #include "gemm_dispatch.hpp"
+#include "gemm_stream_dispatch.hpp"
 
 namespace clarus {
 
 static int esize(int dt) { return dt == DT_BF16 ? 2 : 4; }
 static bool dt_ok(int dt) { return dt == DT_F32 || dt == DT_BF16; }
+
+// widest vector access that keeps every channel run aligned: 2 = 16 B, 1 = 8 B / quad, 0 = scalar
+static int vec_level(const void* base, int es, int64_t ld, int64_t bstride) {
+  auto ok = [&](int bytes) {
+    return aligned(base, bytes) && (ld * es) % bytes == 0 && (bstride * es) % bytes == 0;
+  };
+  if (ok(16)) return 2;
+  if (ok(4 * es)) return 1;
+  return 0;
+}
 
 static int operand_mode(int a_dt, int w_dt, bool transformed) {
   if (w_dt == DT_F32) return OPM_F32;
@@ -14,13 +25,15 @@ static int operand_mode(int a_dt, int w_dt, bool transformed) {
   return OPM_SPLIT;
 }
 
-// tile id for a problem: channel tile from n, pixel tile from the amount of parallel work
-static int auto_tile(int64_t m, int64_t n, int64_t batch, bool gate, int opm) {
+// tile id for a problem: channel tile from n, pixel tile from the amount of parallel work.
+// run_div: the lane's channel run (4 * NB) must divide it (pixel-shuffle quadrant width), 0 = any
+static int auto_tile(int64_t m, int64_t n, int64_t k, int64_t batch, bool gate, int opm, int64_t run_div) {
   int t;
   if (n <= 16) t = 0;
   else if (n <= 32) t = 1;
-  else if (n <= 64 || gate || opm == OPM_F32) t = 3;
+  else if (n <= 64 || gate || opm == OPM_F32 || k > kc_for(opm)) t = 3;
   else t = 6;
+  while (run_div && (run_div % (4 * kTileNB[t])) != 0) t = (kTileNB[t] == 8) ? 3 : (kTileNB[t] == 4 ? 1 : 0);
   const int64_t tn = 16 * kTileNB[t];
   const int64_t wgs = cdiv(m, 64 * kTilePB[t]) * cdiv(n, tn) * batch;
   if (wgs < 1024) {
@@ -66,7 +79,7 @@ static int launch(GemmP& p, int am, bool gate, int opm, int ta, int tile, int64_
   const int64_t tp = 64 * kTilePB[tile];
   p.ptiles = cdiv(p.m, tp);
   dim3 g = grid_for(p.ptiles, cdiv(p.n, tn), batch, p.k, kc_for(opm));
-  fn(p, g, s);
+  fn(p, g, s, p.k <= kc_for(opm) ? 1 : 2);
   return check_launch(what);
 }
 
@@ -101,11 +114,10 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   p.m = a->m; p.n = a->n; p.k = a->k;
   p.lda = a->lda; p.ldc = a->ldc; p.ldr = a->ldr; p.ldm2 = a->ldm2;
   p.a_bs = a->a_bstride; p.w_bs = a->w_bstride; p.c_bs = a->c_bstride; p.r_bs = a->r_bstride;
-  p.s_bs = 0; p.m2_bs = 0;
   p.c_dt = a->c_dtype; p.r_dt = a->r_dtype; p.s_dt = a->s_dtype; p.m2_dt = a->m2_dtype;
   p.h = a->h; p.w = a->w; p.oh = a->oh; p.ow = a->ow; p.pt = a->pt; p.pl = a->pl;
   p.pro = a->pro; p.c_mode = a->c_mode; p.act = a->act; p.m2_act = a->m2_act;
-  p.has_bias = a->bias != nullptr; p.has_scale = a->scale != nullptr; p.has_res = a->res != nullptr;
+  p.has_res = a->res != nullptr;
   p.ln_eps = a->ln_eps; p.out_scale = a->out_scale; p.slope = a->slope;
   p.up2 = 0;
 
@@ -135,17 +147,36 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   if (a->c_mode == CLARUS_C_SHUFFLE) {
     CLARUS_REQUIRE(a->n % 16 == 0 && a->h > 0 && a->w > 0 && a->m % ((int64_t)a->h * a->w) == 0 && a->batch == 1,
                    "gemm: pixel-shuffle output needs N %% 16 == 0 and whole images");
-    p.vec_out = aligned(a->c, 4 * ec);
-    p.vec_res = a->res ? aligned(a->res, 4 * esize(a->r_dtype)) : 0;
+    p.vec_out = vec_level(a->c, ec, 0, 0);
+    p.vec_res = a->res ? vec_level(a->res, esize(a->r_dtype), 0, 0) : 0;
   } else {
     CLARUS_REQUIRE(a->ldc >= a->n, "gemm: ldc < n");
-    p.vec_out = aligned(a->c, 4 * ec) && a->ldc % 4 == 0 && (a->c_bstride % 4 == 0);
-    p.vec_res = a->res ? (aligned(a->res, 4 * esize(a->r_dtype)) && a->ldr % 4 == 0 && a->r_bstride % 4 == 0) : 0;
+    p.vec_out = vec_level(a->c, ec, a->ldc, a->c_bstride);
+    p.vec_res = a->res ? vec_level(a->res, esize(a->r_dtype), a->ldr, a->r_bstride) : 0;
   }
 
   const bool transformed = a->pro != PRO_NONE;
   const int opm = operand_mode(a->a_dtype, a->w_dtype, transformed);
-  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(a->m, a->n, a->batch, a->gate != 0, opm);
+  const int64_t run_div = a->c_mode == CLARUS_C_SHUFFLE ? a->n / 4 : 0;
+  // W-resident streaming kernel for row operands with K <= 256 (bf16 A) / 128 (fp32 A) (tile 0 = auto, 8 / 9 = force
+  // NB 4 / 8); the tiled kernel otherwise (tiles 1..7 force one of its tile shapes)
+  if (a->a_mode == CLARUS_A_ROWS && opm != OPM_F32 && (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
+    const int ks = stream_ks_for(a->k, a->a_dtype);
+    int nb = a->tile == 8 ? 4 : a->tile == 9 ? 8 : ((a->n <= 64 || a->gate) ? 4 : 8);
+    if (run_div && run_div % (4 * nb)) nb = 4;
+    const bool x2 = a->pro == PRO_MUL || a->pro == PRO_LNMUL;
+    GemmLaunch fn = (ks && (!run_div || run_div % (4 * nb) == 0)) ? pick_gemm_stream(nb, a->gate != 0, opm, a->a_dtype, ks, x2)
+                                                                : nullptr;
+    if (fn) {
+      p.ptiles = 0;
+      fn(p, dim3(0, (unsigned)cdiv(a->n, 16 * nb), (unsigned)a->batch), (hipStream_t)stream, 1);
+      return check_launch("gemm");
+    }
+    CLARUS_REQUIRE(a->tile == 0, "gemm: no streaming kernel for K=%lld nb=%d", (long long)a->k, nb);
+  }
+  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(a->m, a->n, a->k, a->batch, a->gate != 0, opm, run_div);
+  CLARUS_REQUIRE(tile >= 0 && tile < kNumTiles && (!run_div || run_div % (4 * kTileNB[tile]) == 0),
+                 "gemm: tile %d does not fit the pixel-shuffle quadrant width", tile + 1);
   return launch(p, a->a_mode == CLARUS_A_ROWS ? AM_ROWS : AM_S2D, a->gate != 0, opm, a->a_dtype, tile, a->batch,
                 (hipStream_t)stream, "gemm");
 }
@@ -174,19 +205,19 @@ extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
   p.c_dt = a->o_dtype; p.r_dt = a->r_dtype;
   p.h = (int)a->h; p.w = (int)a->w; p.cin = (int)a->cin; p.up2 = a->up2 ? 1 : 0;
   p.pro = PRO_NONE; p.c_mode = a->c_mode; p.act = a->act;
-  p.has_bias = a->bias != nullptr; p.has_scale = 0; p.has_res = a->res != nullptr;
+  p.has_res = a->res != nullptr;
   p.out_scale = a->out_scale; p.slope = a->slope; p.ln_eps = 0.f;
   const int eo = esize(a->o_dtype);
   if (a->c_mode == CLARUS_C_ROWS) {
     CLARUS_REQUIRE(a->ldo >= a->cout && (!a->res || a->ldr >= a->cout), "conv3x3: pixel strides smaller than cout");
-    p.vec_out = aligned(a->out, 4 * eo) && a->ldo % 4 == 0;
-    p.vec_res = a->res ? (aligned(a->res, 4 * esize(a->r_dtype)) && a->ldr % 4 == 0) : 0;
+    p.vec_out = vec_level(a->out, eo, a->ldo, 0);
+    p.vec_res = a->res ? vec_level(a->res, esize(a->r_dtype), a->ldr, 0) : 0;
   } else {
     p.vec_out = 0;
     p.vec_res = 0;
   }
   const int opm = operand_mode(a->x_dtype, a->w_dtype, false);
-  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(p.m, p.n, 1, false, opm);
+  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(p.m, p.n, p.k, 1, false, opm, 0);
   return launch(p, AM_CONV3, false, opm, a->x_dtype, tile, 1, (hipStream_t)stream, "conv3x3");
 }
 

@@ -5,16 +5,25 @@
 
 namespace clarus {
 
-using GemmLaunch = void (*)(const GemmP&, dim3, hipStream_t);
+using GemmLaunch = void (*)(const GemmP&, dim3, hipStream_t, int);
 
 // tile id -> (NB, PB): TN = 16 * NB output channels, TP = 64 * PB pixels per workgroup
 constexpr int kTileNB[] = {1, 2, 4, 4, 4, 8, 8};
 constexpr int kTilePB[] = {4, 4, 1, 2, 4, 1, 2};
 constexpr int kNumTiles = 7;
 
+// nbuf = 1 when K fits one chunk (W resident), 2 for the double-buffered K loop
 template <int NB, int PB, bool GATE, int OPM, int TA, int AM, int KC>
-void launch_gemm_one(const GemmP& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((gemm_kernel<NB, PB, GATE, OPM, TA, AM, KC>), grid, dim3(256), 0, s, p);
+void launch_gemm_one(const GemmP& p, dim3 grid, hipStream_t s, int nbuf) {
+  static const bool attr_set = [] {
+    // dynamic LDS above 64 KiB must be allowed explicitly (gfx950 has 160 KiB per CU)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<NB, PB, GATE, OPM, TA, AM, KC>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    return true;
+  }();
+  (void)attr_set;
+  const size_t lds = gemm_epi_bytes(NB) + (size_t)nbuf * gemm_wbuf_bytes(NB, GATE, OPM, KC);
+  hipLaunchKernelGGL((gemm_kernel<NB, PB, GATE, OPM, TA, AM, KC>), grid, dim3(256), lds, s, p);
 }
 
 #define CLARUS_TILE_SWITCH(TILE, F) \

@@ -302,6 +302,31 @@ class HipOps(Backend):
                           bias=self._bias(bias), res=residual, ldr=nout, batch=n, a_bs=x.stride(0),
                           w_bs=nout * k, c_bs=h * wd * nout, r_bs=h * wd * nout)
 
+    def attention_apply(self, qkv, attn_t, residual=None, out_dtype=None):
+        """attn . V of Restormer's MDTA per head: out[p, hd*ch + j] = sum_i v[p, hd*ch + i]
+        * attn_t[n, hd, i, j], with v = qkv[..., 2C:] and attn_t = A^T per head [N, heads, ch, ch].
+        Equals linear_per_image(v, blockdiag(attn_t)) (the block-diagonal mix the Restormer block
+        builds, python/clarus/models/restormer/__init__.py:203-210) without the zero blocks:
+        one batched GEMM launch per image with the heads as the batch."""
+        n, h, wd, c3 = qkv.shape
+        c = c3 // 3
+        if attn_t.dim() == 3:
+            attn_t = attn_t.unsqueeze(0)
+        heads, ch = attn_t.shape[1], attn_t.shape[2]
+        if (not qkv.is_contiguous() or c3 % 3 or heads * ch != c or tuple(attn_t.shape) != (n, heads, ch, ch)
+                or not _same(residual, (n, h, wd, c))):
+            raise Unsupported("attention_apply: contiguous qkv, attn [N, heads, ch, ch], residual of the output's shape")
+        odt = out_dtype or self.dtype
+        if not (_kdt(qkv, attn_t, residual) and odt in _KDT and ch % 8 == 0 and _vec16(qkv, c3, ch)):
+            raise Unsupported("attention_apply: bf16 / fp32, head width % 8 == 0")
+        out = torch.empty((n, h, wd, c), device=qkv.device, dtype=odt)
+        wt = attn_t.transpose(2, 3).contiguous()  # W^T per head: [n, heads, j, i]
+        for i in range(n):
+            self._gemm("attention_apply", a=qkv[i, ..., 2 * c:], wt=wt[i], c=out[i], m=h * wd, n=ch, k=ch, lda=c3,
+                       ldc=c, res=residual[i] if residual is not None else None, ldr=c, batch=heads, a_bs=ch,
+                       w_bs=ch * ch, c_bs=ch, r_bs=ch)
+        return out
+
     # ------------------------------------------------------------------ frequency ops
     def patch_filter(self, x, f, residual=None, out_dtype=None):
         n, h, wd, c = x.shape

@@ -1,0 +1,173 @@
+"""Benchmark workloads of the GEMM-family hot path.
+
+Each case holds seeded inputs resident on the device, a closure that runs the op once through
+the `hip` backend, and its ALGORITHMIC flop and byte counts (the formulas of the measurement
+plan; they are fixed by the op and shape, not read from counters):
+
+  config 2 (NAFNet-w64 720p pointwise GEMMs, bf16, M = H * W pixels)
+    expand c -> 2c + bias + SimpleGate : F = 4 M c^2, B = 2Mc (A) + 2Mc (out) + 4c^2 + 8c
+    c -> c + bias, * beta, + residual  : F = 2 M c^2, B = 2Mc + 2 r M c + 2c^2 + 8c,
+                                         r = 2 (bf16 residual / output) for c < 512, 4 (fp32) above
+  config 3 (patch DFT, fp32, fused fwd 64->80 / filter / inv 80->64) per patch-channel:
+    F = 2*64*80 + 6*40 + 2*80*64, B = 4*64 (in) + 4*64 (out)
+  config 4 (Restormer MDTA, level l: C = 48 * 2^l, heads 2^l, HW = 921600 / 4^l), e = element size
+    Gram + norms : F = heads (2 * 48^2 HW + 4 * 48 HW), B = 2 C HW e + heads * 48^2 * 4
+    attn . V     : F = heads * 2 * 48^2 HW,          B = 2 C HW e
+  config 5 (RRDBNet 3x3, bf16, M output pixels): F = 2 M 9 Cin Cout,
+    B = 2 M_in Cin + 2 M Cout (+ 2 M 64 residual) + 18 Cin Cout
+Peaks (MI355X datasheet): bf16 MFMA 2.5 PFLOP/s, fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable
+
+import torch
+
+PEAK_FLOPS = {"bf16": 2.5e15, "fp32": 157.3e12}
+PEAK_HBM = 8.0e12
+
+
+@dataclass
+class OpCase:
+    name: str
+    config: int
+    dtype: str            # arithmetic type of the products: "bf16" or "fp32"
+    flops: float
+    nbytes: float
+    run: Callable[[], object]
+    cpu: dict = field(default_factory=dict)  # inputs for a CPU baseline of the same op
+
+    def t_bound(self) -> tuple[float, str]:
+        tm = self.flops / PEAK_FLOPS[self.dtype]
+        tb = self.nbytes / PEAK_HBM
+        return (tm, "mfma") if tm >= tb else (tb, "hbm")
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _kaiming_uniform_kn(g, cin, cout):
+    """nn.Conv2d default 1x1 init (kaiming_uniform, a = sqrt(5): bound 1/sqrt(fan_in)) as [K, N]."""
+    return ((torch.rand(cout, cin, generator=g) * 2 - 1) / math.sqrt(cin)).t().contiguous()
+
+
+CONFIG2_LEVELS = [(64, 720, 1280), (128, 360, 640), (256, 180, 320), (512, 90, 160), (1024, 45, 80)]
+
+
+def config2_cases(hip, device, seed: int = 0) -> list[OpCase]:
+    """Per level: u = linear(x, We, be, gate=True); y = linear(u, Wc, bc, scale=beta, residual=r)."""
+    cases = []
+    for c, h, w in CONFIG2_LEVELS:
+        g = _gen(seed + c)
+        m = h * w
+        x = torch.randn(1, h, w, c, generator=g).bfloat16()
+        we = _kaiming_uniform_kn(g, c, 2 * c).bfloat16()
+        be = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+        wc = _kaiming_uniform_kn(g, c, c).bfloat16()
+        bc = torch.rand(c, generator=g) * 0.2 - 0.1
+        beta = torch.randn(c, generator=g) * 0.1
+        rdt = torch.float32 if c >= 512 else torch.bfloat16
+        r = torch.randn(1, h, w, c, generator=g).to(rdt)
+        cpu = dict(x=x, we=we, be=be, wc=wc, bc=bc, beta=beta, r=r, rdt=rdt)
+        d = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in cpu.items()}
+        u = hip.linear(d["x"], d["we"], d["be"], gate=True)  # also the c->c input
+
+        def expand(d=d):
+            return hip.linear(d["x"], d["we"], d["be"], gate=True)
+
+        def cc(d=d, u=u):
+            return hip.linear(u, d["wc"], d["bc"], scale=d["beta"], residual=d["r"], out_dtype=d["rdt"])
+        rb = 2 if c < 512 else 4
+        cases.append(OpCase(f"c{c} expand+gate", 2, "bf16", 4.0 * m * c * c,
+                            2.0 * m * c + 2.0 * m * c + 4.0 * c * c + 8.0 * c, expand, cpu))
+        cases.append(OpCase(f"c{c} c->c+scale+res", 2, "bf16", 2.0 * m * c * c,
+                            2.0 * m * c + 2.0 * rb * m * c + 2.0 * c * c + 8.0 * c, cc, cpu))
+    return cases
+
+
+def config1_cases(hip32, device, seed: int = 0) -> list[OpCase]:
+    """fp32 pointwise chain on x [1, 256, 256, 32] (gate op, then scale + residual op)."""
+    g = _gen(seed)
+    x = torch.randn(1, 256, 256, 32, generator=g)
+    w1 = _kaiming_uniform_kn(g, 32, 64)
+    b1 = torch.rand(64, generator=g) * 0.2 - 0.1
+    w2 = _kaiming_uniform_kn(g, 32, 32)
+    b2 = torch.rand(32, generator=g) * 0.2 - 0.1
+    beta = torch.randn(32, generator=g) * 0.1
+    d = [t.to(device) for t in (x, w1, b1, w2, b2, beta)]
+    u = hip32.linear(d[0], d[1], d[2], gate=True)
+    m = 256 * 256
+
+    def chain():
+        uu = hip32.linear(d[0], d[1], d[2], gate=True)
+        return hip32.linear(uu, d[3], d[4], scale=d[5], residual=d[0])
+    del u
+    return [OpCase("config1 fp32 chain (gate, scale+res)", 1, "fp32", 2.0 * m * 32 * 64 + 2.0 * m * 32 * 32,
+                   4.0 * m * 32 * 2 + 4.0 * m * 32 * 2 + 4.0 * (32 * 64 + 32 * 32) + 4.0 * (64 + 64), chain)]
+
+
+def config3_cases(hip32, device, seed: int = 0) -> list[OpCase]:
+    cases = []
+    for c, h, w in [(48, 720, 1280), (96, 360, 640), (192, 180, 320)]:
+        g = _gen(seed + c)
+        x = torch.randn(1, h, w, c, generator=g).to(device)
+        f = torch.randn(c, 8, 5, generator=g).to(device)
+        units = (h // 8) * (w // 8) * c
+        cases.append(OpCase(f"patch_filter fused C{c} {h}x{w}", 3, "fp32",
+                            units * (2.0 * 64 * 80 + 6 * 40 + 2.0 * 80 * 64), units * 4.0 * 128,
+                            lambda x=x, f=f: hip32.patch_filter(x, f)))
+    return cases
+
+
+def config4_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
+    cases = []
+    for dt, hip in ((torch.float32, hip32), (torch.bfloat16, hip_bf16)):
+        e = 4 if dt == torch.float32 else 2
+        tag = "fp32" if dt == torch.float32 else "bf16"
+        for lvl, h, w in [(0, 720, 1280), (1, 360, 640), (2, 180, 320), (3, 90, 160)]:
+            g = _gen(seed + lvl)
+            c, heads = 48 * 2 ** lvl, 2 ** lvl
+            hw = h * w
+            qkv = torch.randn(1, h, w, 3 * c, generator=g).to(dt).to(device)
+            t = (torch.rand(heads, generator=g) * 1.5 + 0.5).to(device)
+            cases.append(OpCase(f"mdta gram+norms+softmax l{lvl} {tag}", 4, tag,
+                                heads * (2.0 * 48 * 48 * hw + 4.0 * 48 * hw), 2.0 * c * hw * e + heads * 48 * 48 * 4,
+                                lambda hip=hip, qkv=qkv, t=t, heads=heads: hip.channel_attention(qkv, heads, t)))
+            a = hip.channel_attention(qkv, heads, t)
+            wa = a[0].transpose(1, 2).contiguous().to(dt)  # per head A^T [heads, 48, 48]
+            cases.append(OpCase(f"mdta attn.V l{lvl} {tag}", 4, tag, heads * 2.0 * 48 * 48 * hw, 2.0 * c * hw * e,
+                                lambda hip=hip, qkv=qkv, wa=wa: hip.attention_apply(qkv, wa)))
+    return cases
+
+
+def config5_cases(hip, device, seed: int = 0) -> list[OpCase]:
+    g = _gen(seed)
+    h, w = 256, 384
+    m = h * w
+    buf = torch.randn(1, h, w, 192, generator=g).bfloat16().to(device)
+    out = torch.empty(1, h, w, 192, dtype=torch.bfloat16, device=device)
+    cases = []
+
+    def kn(cout, cin):
+        return ((torch.randn(cout, cin, 3, 3, generator=g) * math.sqrt(2.0 / (cin * 9))) * 0.1).bfloat16().to(device)
+    for cin in (64, 96, 128, 160):
+        wt, b = kn(32, cin), torch.zeros(32, device=device)
+        cases.append(OpCase(f"conv3x3 {cin}->32 +lrelu (slice)", 5, "bf16", 2.0 * m * 9 * cin * 32,
+                            2.0 * m * (cin + 32) + 18.0 * cin * 32,
+                            lambda cin=cin, wt=wt, b=b: hip.conv3x3(buf[..., :cin], wt, b, act="lrelu",
+                                                                    out=buf[..., cin:cin + 32])))
+    w5, b5 = kn(64, 192), torch.zeros(64, device=device)
+    cases.append(OpCase("conv3x3 192->64 *0.2 +res", 5, "bf16", 2.0 * m * 9 * 192 * 64,
+                        2.0 * m * (192 + 64) + 2.0 * m * 64 + 18.0 * 192 * 64,
+                        lambda: hip.conv3x3(buf, w5, b5, out_scale=0.2, residual=buf[..., :64], out=out[..., :64])))
+    for hh, ww in [(256, 384), (512, 768)]:
+        x = torch.randn(1, hh, ww, 64, generator=g).bfloat16().to(device)
+        wt, b = kn(64, 64), torch.zeros(64, device=device)
+        mo = 4 * hh * ww
+        cases.append(OpCase(f"up2 + conv3x3 64->64 +lrelu out {2 * hh}x{2 * ww}", 5, "bf16", 2.0 * mo * 9 * 64 * 64,
+                            2.0 * hh * ww * 64 + 2.0 * mo * 64 + 18.0 * 64 * 64,
+                            lambda x=x, wt=wt, b=b: hip.conv3x3(x, wt, b, act="lrelu", up2=True)))
+    return cases
