@@ -1,0 +1,237 @@
+"""CPU: the host side of the HIP backend.
+
+  * the dispatch contract (clarus_amd.dispatch, restating python/clarus/ops/__init__.py):
+    fallback on Unsupported, the last backend re-raises, overrides, served counters, report(),
+    BackendUnavailable skips, registration by decorator and by path, Backend.cached;
+  * HipOps refuses to construct off-GPU (BackendUnavailable, never a silent CPU path);
+  * the DFT matrices the patch kernels use, against numpy.fft and torch.fft;
+  * the NAFNet harness (weight folding + forward wiring) against an unfolded float64 NAFNet
+    written from the upstream block definition, and the TLC windows known answer
+    (tools/test_model_contracts.py:149-163).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from clarus_amd import dispatch
+from clarus_amd.dft import dft_matrices, filter_gains
+from clarus_amd.dispatch import Backend, BackendUnavailable, Ops, Unsupported, register_backend
+from oracle.torch_ref import TorchRef
+
+
+# ------------------------------------------------------------------ dispatch
+class _Declines(Backend):
+    name = "declines"
+
+    def linear(self, x, *a, **k):
+        if x.shape[-1] != 4:
+            raise Unsupported("only K = 4")
+        return "fast"
+
+    def only_here(self, x):
+        raise Unsupported("never")
+
+
+class _All(Backend):
+    name = "all"
+
+    def linear(self, x, *a, **k):
+        return "slow"
+
+    def dwconv(self, x):
+        return "dw"
+
+
+class _Unavailable(Backend):
+    name = "unavailable"
+
+    def __init__(self, dtype, device):
+        raise BackendUnavailable("not on this device")
+
+
+@pytest.fixture(autouse=True)
+def _registered():
+    register_backend("declines")(_Declines)
+    register_backend("all")(_All)
+    register_backend("unavailable")(_Unavailable)
+    register_backend("oracle_by_path", "tests.test_host:_OracleBackend")
+    yield
+
+
+def test_fallback_and_counters():
+    logs = []
+    ops = Ops(["unavailable", "declines", "all"], torch.float32, torch.device("cpu"), log=logs.append)
+    assert [b.name for b in ops.backends] == ["declines", "all"]
+    assert "unavailable" in ops.skipped and logs
+    assert ops.linear(torch.zeros(1, 1, 1, 4)) == "fast"
+    assert ops.linear(torch.zeros(1, 1, 1, 8)) == "slow"
+    assert ops.dwconv(None) == "dw"
+    rep = ops.report()
+    assert rep["ops"]["linear"] == {"all": 1, "declines": 1} and rep["ops"]["dwconv"] == {"all": 1}
+    with pytest.raises(Unsupported):  # the last backend's Unsupported propagates
+        ops.only_here(None)
+    with pytest.raises(AttributeError):
+        ops.not_an_op
+
+
+def test_overrides():
+    ops = Ops(["declines", "all"], torch.float32, torch.device("cpu"), overrides={"linear": "all"},
+              log=lambda *a: None)
+    assert ops.linear(torch.zeros(1, 1, 1, 4)) == "slow"
+    with pytest.raises(ValueError):
+        Ops(["all"], torch.float32, torch.device("cpu"), overrides={"linear": "declines"}, log=lambda *a: None)
+    with pytest.raises(RuntimeError):
+        Ops(["unavailable"], torch.float32, torch.device("cpu"), log=lambda *a: None)
+    with pytest.raises(ValueError):
+        Ops(["no_such_backend"], torch.float32, torch.device("cpu"), log=lambda *a: None)
+
+
+def test_cached_relayout_once():
+    b = _All(torch.float32, torch.device("cpu"))
+    w = torch.randn(4, 3)
+    calls = []
+    f = lambda t: calls.append(1) or t.t().contiguous()  # noqa: E731
+    assert torch.equal(b.cached(w, "t", f), w.t())
+    b.cached(w, "t", f)
+    assert len(calls) == 1
+
+
+def test_hip_backend_unavailable_on_cpu():
+    """Off a gfx950 device the hip backend refuses to exist (Ops logs and skips it); it never
+    runs a CPU path in its place."""
+    from clarus_amd.hip_ops import HipOps
+    with pytest.raises(BackendUnavailable):
+        HipOps(torch.bfloat16, torch.device("cpu"))
+    ops = Ops(["hip", "oracle_by_path"], torch.bfloat16, torch.device("cpu"), log=lambda *a: None)
+    assert "hip" in ops.skipped and [b.name for b in ops.backends] == ["oracle"]
+
+
+def test_host_clarus_absent():
+    assert dispatch._host is None and dispatch.Unsupported is dispatch._Unsupported
+
+
+# ------------------------------------------------------------------ DFT matrices
+def test_dft_matrices_vs_numpy_and_torch():
+    fwd, inv = dft_matrices(8)
+    assert fwd.shape == (80, 64) and inv.shape == (64, 80)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, 8, 8))
+    spec = np.fft.rfft2(x)                                # [5, 8, 5]
+    got = x.reshape(5, 64) @ fwd.T                       # [5, 80]
+    assert np.allclose(got[:, 0::2], spec.real.reshape(5, 40), atol=1e-12)
+    assert np.allclose(got[:, 1::2], spec.imag.reshape(5, 40), atol=1e-12)
+    # inverse of arbitrary (non-Hermitian) coefficients: numpy and torch agree with Inv
+    c = rng.standard_normal((5, 80))
+    z = c[:, 0::2] + 1j * c[:, 1::2]
+    ref_np = np.fft.irfft2(z.reshape(5, 8, 5), s=(8, 8)).reshape(5, 64)
+    ref_t = torch.fft.irfft2(torch.from_numpy(z.reshape(5, 8, 5)), s=(8, 8)).reshape(5, 64).numpy()
+    assert np.allclose(c @ inv.T, ref_np, atol=1e-12)
+    assert np.allclose(c @ inv.T, ref_t, atol=1e-12)
+    # round trip on real patches
+    assert np.allclose((x.reshape(5, 64) @ fwd.T) @ inv.T, x.reshape(5, 64), atol=1e-12)
+
+
+def test_filter_gains_match_the_oracle_patch_filter():
+    """y = Inv (g * (Fwd x)) reproduces irfft2(rfft2(x) * f) (the oracle) for a random,
+    non-symmetric real filter."""
+    g = torch.Generator().manual_seed(0)
+    x, f = torch.randn(1, 8, 8, 3, generator=g), torch.randn(3, 8, 5, generator=g)
+    fwd, inv = dft_matrices(8)
+    gains = filter_gains(f.numpy())                       # [3, 80]
+    xs = x[0].double().numpy().reshape(64, 3)             # pixel-major
+    y = np.stack([inv @ (gains[c] * (fwd @ xs[:, c])) for c in range(3)], axis=1).reshape(8, 8, 3)
+    ref = TorchRef().patch_filter(x, f)[0].double().numpy()
+    assert np.abs(y - ref).max() < 1e-5
+
+
+# ------------------------------------------------------------------ NAFNet harness
+class _OracleBackend(Backend):
+    """The oracle behind the dispatch contract (test use)."""
+    name = "oracle"
+
+    def __init__(self, dtype, device):
+        super().__init__(dtype, device)
+        self._r = TorchRef(dtype, device)
+
+    def __getattr__(self, op):
+        if op.startswith("_"):
+            raise AttributeError(op)
+        return getattr(self._r, op)
+
+
+def _layernorm2d(x, w, b, eps=1e-6):
+    mu = x.mean(1, keepdim=True)
+    var = (x - mu).pow(2).mean(1, keepdim=True)
+    return (x - mu) / (var + eps).sqrt() * w.view(1, -1, 1, 1) + b.view(1, -1, 1, 1)
+
+
+def _upstream_nafnet64(sd, enc, mid, dec, x, tlc_kernel):
+    """Unfolded NAFNetLocal in float64, written from the upstream block definition (NCHW,
+    LayerNorm2d, depthwise conv, SimpleGate, local-average-pool SCA, beta / gamma residuals)."""
+    sd = {k: v.double() for k, v in sd.items()}
+
+    def local_mean(t, k):
+        kh, kw = min(t.shape[2], k[0]), min(t.shape[3], k[1])
+        m = F.avg_pool2d(t, (kh, kw), stride=1)
+        ph, pw = t.shape[2] - m.shape[2], t.shape[3] - m.shape[3]
+        return F.pad(m, (pw // 2, pw - pw // 2, ph // 2, ph - ph // 2), mode="replicate")
+
+    def block(t, p, level):
+        y = _layernorm2d(t, sd[f"{p}.norm1.weight"], sd[f"{p}.norm1.bias"])
+        y = F.conv2d(y, sd[f"{p}.conv1.weight"], sd[f"{p}.conv1.bias"])
+        y = F.conv2d(y, sd[f"{p}.conv2.weight"], sd[f"{p}.conv2.bias"], padding=1, groups=y.shape[1])
+        a, b = y.chunk(2, 1)
+        y = a * b
+        y = y * F.conv2d(local_mean(y, tlc_kernel(level)), sd[f"{p}.sca.1.weight"], sd[f"{p}.sca.1.bias"])
+        y = F.conv2d(y, sd[f"{p}.conv3.weight"], sd[f"{p}.conv3.bias"])
+        t2 = t + y * sd[f"{p}.beta"]
+        y = _layernorm2d(t2, sd[f"{p}.norm2.weight"], sd[f"{p}.norm2.bias"])
+        y = F.conv2d(y, sd[f"{p}.conv4.weight"], sd[f"{p}.conv4.bias"])
+        a, b = y.chunk(2, 1)
+        y = F.conv2d(a * b, sd[f"{p}.conv5.weight"], sd[f"{p}.conv5.bias"])
+        return t2 + y * sd[f"{p}.gamma"]
+
+    inp = x.double()
+    t = F.conv2d(inp, sd["intro.weight"], sd["intro.bias"], padding=1)
+    skips = []
+    for i, n in enumerate(enc):
+        for j in range(n):
+            t = block(t, f"encoders.{i}.{j}", i)
+        skips.append(t)
+        t = F.conv2d(t, sd[f"downs.{i}.weight"], sd[f"downs.{i}.bias"], stride=2)
+    for j in range(mid):
+        t = block(t, f"middle_blks.{j}", len(enc))
+    for i, n in enumerate(dec):
+        t = F.pixel_shuffle(F.conv2d(t, sd[f"ups.{i}.0.weight"]), 2)
+        t = t + skips[len(enc) - 1 - i]
+        for j in range(n):
+            t = block(t, f"decoders.{i}.{j}", len(enc) - 1 - i)
+    return F.conv2d(t, sd["ending.weight"], sd["ending.bias"], padding=1) + inp
+
+
+def test_nafnet_harness_vs_unfolded_float64():
+    from clarus_amd.nafnet import NAFNet, random_state_dict
+    enc, mid, dec = [1, 1], 1, [1, 1]
+    sd = random_state_dict(8, enc, mid, dec, seed=3)
+    ops = Ops(["oracle_by_path"], torch.float32, torch.device("cpu"), log=lambda *a: None)
+    model = NAFNet(ops, width=8, enc=enc, mid=mid, dec=dec, tlc=(33, 33), state_dict=sd)
+    x = torch.rand(1, 3, 32, 48, generator=torch.Generator().manual_seed(1))
+    got = model.forward(x)
+    ref = _upstream_nafnet64(sd, enc, mid, dec, x, model.tlc_kernel)
+    err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
+    assert err < 1e-5, err
+
+
+def test_nafnet_tlc_windows_known_answer():
+    """train 33 with two levels: windows (53, 53), (26, 26), (13, 13)
+    (tools/test_model_contracts.py:159-160)."""
+    from clarus_amd.nafnet import NAFNet
+    ops = Ops(["oracle_by_path"], torch.float32, torch.device("cpu"), log=lambda *a: None)
+    m = NAFNet(ops, width=4, enc=[1, 1], mid=1, dec=[1, 1], tlc=(33, 33))
+    assert {m.tlc_kernel(level) for level in range(3)} == {(53, 53), (26, 26), (13, 13)}
+    # NAFNet-GoPro-w64 at train 256: 384 / 192 / 96 / 48 / 24 per level
+    m64 = NAFNet(ops, width=4, enc=[1, 1, 1, 1], mid=1, dec=[1, 1, 1, 1])
+    assert [m64.tlc_kernel(level)[0] for level in range(5)] == [384, 192, 96, 48, 24]
