@@ -67,6 +67,8 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _i64, _vp]),
     "clarus_hip_patch_corr": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
                                      _i64, _i64, _vp]),
+    "clarus_hip_dwconv3x3": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
+                                    _vp]),
     "clarus_hip_abi_version": (_i32, []),
     "clarus_hip_sizeof_gemm_args": (ctypes.c_size_t, []),
     "clarus_hip_sizeof_conv_args": (ctypes.c_size_t, []),

@@ -2,22 +2,26 @@
 //   A[n, hd] = softmax( (q / |q|) (k / |k|)^T * t[hd] ),  q, k: [HW, c_h] head slices of qkv.
 //
 // Stage 1 (gram_partial_kernel), grid (nsplit, batch * heads): each workgroup reduces a
-// contiguous pixel range. Per 128-pixel chunk the q and k head slices are read with 16-byte
-// loads (8 channels of one pixel per lane, coalesced), written transposed into LDS
-// ([channel][pixel]), and each wave contracts its 32 pixels with MFMA:
+// contiguous pixel range in chunks of 128 pixels. A chunk's q and k head slices are read with
+// 16-byte loads (8 channels of one pixel per lane, coalesced) one chunk AHEAD into registers,
+// written transposed into LDS ([channel][pixel]), and each wave contracts its 32 pixels with
+// MFMA:
 //   cross blocks  Q^T K  (NB x NB blocks of 16 x 16)
 //   diagonal blocks of Q^T Q and K^T K, whose diagonals are the squared norms.
 // bf16 inputs use bf16 MFMA (products exact in fp32), fp32 inputs fp32 MFMA. The 4 waves'
-// partials are summed in LDS in fixed order and written to scratch[split].
-// Stage 2 (gram_finish_kernel), one workgroup per (image, head): sums the split partials in
-// split order (deterministic for a given split count), scales by rsqrt(max(|.|^2, 1e-24)) and
-// the temperature, and applies a row softmax.
+// partials are summed in LDS (the transpose tile's memory, reused) in a fixed order and
+// written to scratch as one record per split.
+// Stage 2 (gram_reduce_kernel): RS slices of the splits summed per element, in split order.
+// Stage 3 (gram_finish_kernel), one workgroup per (image, head): sums the RS slices in order,
+// scales by rsqrt(max(|.|^2, 1e-24)) and the temperature, and applies a row softmax.
+// The result is deterministic (fixed summation order for a given shape).
 #include "capi.hpp"
 #include "common.hpp"
 
 namespace clarus {
 
 constexpr int GP_CHUNK = 128;  // pixels per chunk (32 per wave)
+constexpr int GP_RS = 16;      // reduce slices
 
 // partial record per (image*head, split): [NB*16][NB*16] cross, [NB*16] |q|^2, [NB*16] |k|^2
 __host__ __device__ inline int64_t gram_rec_floats(int nb) {
@@ -26,15 +30,26 @@ __host__ __device__ inline int64_t gram_rec_floats(int nb) {
 }
 
 template <int NB, int DT>
+__host__ __device__ constexpr int gram_lds_bytes() {
+  // max(transpose tile, 4-wave reduction buffer)
+  return (2 * NB * 16 * (GP_CHUNK + (DT == DT_BF16 ? 8 : 4)) * (DT == DT_BF16 ? 2 : 4)) >
+                 (4 * (NB * 16 * NB * 16 + 2 * NB * 16) * 4)
+             ? (2 * NB * 16 * (GP_CHUNK + (DT == DT_BF16 ? 8 : 4)) * (DT == DT_BF16 ? 2 : 4))
+             : (4 * (NB * 16 * NB * 16 + 2 * NB * 16) * 4);
+}
+
+template <int NB, int DT>
 __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restrict__ qkv, float* __restrict__ part,
                                                            int64_t hw, int c, int ch, int heads,
                                                            int64_t split_len, int nsplit) {
-  constexpr int CP = NB * 16;                          // padded head channels
+  constexpr int CP = NB * 16;                               // padded head channels
   constexpr int ES = (DT == DT_BF16) ? 2 : 4;
   constexpr int TROW = GP_CHUNK + (DT == DT_BF16 ? 8 : 4);  // LDS row (elements), +16 B
-  // transposed tiles: rows [0, CP) = q channels, [CP, 2 CP) = k channels
-  __shared__ __attribute__((aligned(16))) unsigned char tl[2 * CP * TROW * ES];
-  __shared__ float red[4][CP * CP + 2 * CP];
+  constexpr int REC = CP * CP + 2 * CP;
+  constexpr int UPT = (GP_CHUNK * 2 * 8 + 255) / 256;       // 16-byte units per thread (<= 8 groups)
+  __shared__ __attribute__((aligned(16))) unsigned char smem[gram_lds_bytes<NB, DT>()];
+  unsigned char* tl = smem;                                 // rows [0, CP) q, [CP, 2 CP) k
+  float* red = reinterpret_cast<float*>(smem);              // reused after the pixel loop
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 15, lg = lane >> 4;
@@ -46,6 +61,17 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
   const int64_t row_stride = 3LL * c;  // elements per pixel
   const unsigned char* base = (const unsigned char*)qkv + (int64_t)img * hw * row_stride * ES;
   const int qoff = hd * ch, koff = c + hd * ch;
+  const int groups = ch / 8;           // 8-channel groups per head slice
+  const int units = GP_CHUNK * 2 * groups;
+
+  // zero the padded channel rows once (they are never written by the loads)
+  for (int u = tid; u < 2 * (CP - ch) * TROW; u += 256) {
+    const int r = u / TROW, px = u - r * TROW;
+    const int which = r / (CP - ch), rr = r - which * (CP - ch);
+    const int row = which * CP + ch + rr;
+    if constexpr (DT == DT_BF16) reinterpret_cast<unsigned short*>(tl)[row * TROW + px] = 0;
+    else reinterpret_cast<float*>(tl)[row * TROW + px] = 0.f;
+  }
 
   f32x4 cross[NB][NB], dq[NB], dk[NB];
 #pragma unroll
@@ -55,77 +81,94 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
     for (int j = 0; j < NB; ++j) cross[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int groups = ch / 8;  // 8-channel groups per head slice
-  for (int64_t p0 = p_begin; p0 < p_end; p0 += GP_CHUNK) {
-    __syncthreads();
-    // ---- load q / k head slices of GP_CHUNK pixels, store transposed
-    const int units = GP_CHUNK * 2 * groups;
-    for (int u = tid; u < units; u += 256) {
-      const int px = u / (2 * groups);
-      const int r = u - px * 2 * groups;
-      const int which = r / groups;  // 0 q, 1 k
-      const int g = r - which * groups;
-      const int64_t p = p0 + px;
-      f32x8 v = zero8();
-      if (p < p_end) v = load8<DT>(base + (p * row_stride + (which ? koff : qoff) + g * 8) * ES);
-      const int row0 = which * CP + g * 8;
+  u32x4 rq[UPT], rq2[DT == DT_F32 ? UPT : 1];
+  auto fetch = [&](int64_t p0) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (DT == DT_BF16)
-          reinterpret_cast<unsigned short*>(tl)[(row0 + i) * TROW + px] = f32_to_bf16_bits(v.v[i]);
-        else
-          reinterpret_cast<float*>(tl)[(row0 + i) * TROW + px] = v.v[i];
+    for (int j = 0; j < UPT; ++j) {
+      const int u = tid + j * 256;
+      rq[j] = u32x4{0u, 0u, 0u, 0u};
+      if constexpr (DT == DT_F32) rq2[j] = u32x4{0u, 0u, 0u, 0u};
+      if (u < units) {
+        const int px = u / (2 * groups);
+        const int r = u - px * 2 * groups;
+        const int which = r / groups;
+        const int g = r - which * groups;
+        const int64_t p = p0 + px;
+        if (p < p_end) {
+          const unsigned char* src = base + (p * row_stride + (which ? koff : qoff) + g * 8) * ES;
+          rq[j] = *reinterpret_cast<const u32x4*>(src);
+          if constexpr (DT == DT_F32) rq2[j] = *reinterpret_cast<const u32x4*>(src + 16);
+        }
       }
     }
-    // zero the padded channel rows (ch < CP) once per chunk
-    for (int u = tid; u < 2 * (CP - ch) * GP_CHUNK; u += 256) {
-      const int r = u / GP_CHUNK, px = u - r * GP_CHUNK;
-      const int which = r / (CP - ch), rr = r - which * (CP - ch);
-      const int row = which * CP + ch + rr;
-      if constexpr (DT == DT_BF16)
-        reinterpret_cast<unsigned short*>(tl)[row * TROW + px] = 0;
-      else
-        reinterpret_cast<float*>(tl)[row * TROW + px] = 0.f;
+  };
+  auto store_t = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      const int u = tid + j * 256;
+      if (u < units) {
+        const int px = u / (2 * groups);
+        const int r = u - px * 2 * groups;
+        const int which = r / groups;
+        const int g = r - which * groups;
+        const int row0 = which * CP + g * 8;
+        if constexpr (DT == DT_BF16) {
+          unsigned short* t = reinterpret_cast<unsigned short*>(tl);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            t[(row0 + 2 * i) * TROW + px] = (unsigned short)(rq[j][i] & 0xffffu);
+            t[(row0 + 2 * i + 1) * TROW + px] = (unsigned short)(rq[j][i] >> 16);
+          }
+        } else {
+          float* t = reinterpret_cast<float*>(tl);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            t[(row0 + i) * TROW + px] = __uint_as_float(rq[j][i]);
+            t[(row0 + 4 + i) * TROW + px] = __uint_as_float(rq2[j][i]);
+          }
+        }
+      }
     }
+  };
+
+  if (p_begin < p_end) fetch(p_begin);
+  for (int64_t p0 = p_begin; p0 < p_end; p0 += GP_CHUNK) {
+    __syncthreads();  // previous chunk's MFMA reads are done
+    store_t();
     __syncthreads();
+    if (p0 + GP_CHUNK < p_end) fetch(p0 + GP_CHUNK);  // next chunk streams in during the products
     // ---- this wave's 32 pixels: k = wave * 32 + 8 * lg + s
     const int kcol = wave * 32 + lg * 8;
-    f32x8 qf[NB], kf[NB];
+    if constexpr (DT == DT_BF16) {
+      bf16x8 qf[NB], kf[NB];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      if constexpr (DT == DT_BF16) {
-        u32x4 a = *reinterpret_cast<const u32x4*>(tl + ((size_t)(i * 16 + lc) * TROW + kcol) * 2);
-        u32x4 b = *reinterpret_cast<const u32x4*>(tl + ((size_t)(CP + i * 16 + lc) * TROW + kcol) * 2);
-        // keep the raw bf16 pairs; unpacked only by the fp32 path
-        qf[i].v[0] = __uint_as_float(a[0]); qf[i].v[1] = __uint_as_float(a[1]);
-        qf[i].v[2] = __uint_as_float(a[2]); qf[i].v[3] = __uint_as_float(a[3]);
-        kf[i].v[0] = __uint_as_float(b[0]); kf[i].v[1] = __uint_as_float(b[1]);
-        kf[i].v[2] = __uint_as_float(b[2]); kf[i].v[3] = __uint_as_float(b[3]);
-      } else {
+      for (int i = 0; i < NB; ++i) {
+        qf[i] = *reinterpret_cast<const bf16x8*>(tl + ((size_t)(i * 16 + lc) * TROW + kcol) * 2);
+        kf[i] = *reinterpret_cast<const bf16x8*>(tl + ((size_t)(CP + i * 16 + lc) * TROW + kcol) * 2);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        dq[i] = mfma_bf16(qf[i], qf[i], dq[i]);
+        dk[i] = mfma_bf16(kf[i], kf[i], dk[i]);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) cross[i][j] = mfma_bf16(qf[i], kf[j], cross[i][j]);
+      }
+    } else {
+      f32x8 qf[NB], kf[NB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
         const float* ra = reinterpret_cast<const float*>(tl) + (i * 16 + lc) * TROW + kcol;
         const float* rb = reinterpret_cast<const float*>(tl) + (CP + i * 16 + lc) * TROW + kcol;
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(ra), a1 = *reinterpret_cast<const f32x4*>(ra + 4);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(rb), b1 = *reinterpret_cast<const f32x4*>(rb + 4);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) { qf[i].v[s] = ra[s]; kf[i].v[s] = rb[s]; }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      if constexpr (DT == DT_BF16) {
-        u32x4 qa = {__float_as_uint(qf[i].v[0]), __float_as_uint(qf[i].v[1]), __float_as_uint(qf[i].v[2]),
-                    __float_as_uint(qf[i].v[3])};
-        u32x4 ka = {__float_as_uint(kf[i].v[0]), __float_as_uint(kf[i].v[1]), __float_as_uint(kf[i].v[2]),
-                    __float_as_uint(kf[i].v[3])};
-        const bf16x8 qb = __builtin_bit_cast(bf16x8, qa);
-        const bf16x8 kb = __builtin_bit_cast(bf16x8, ka);
-        dq[i] = mfma_bf16(qb, qb, dq[i]);
-        dk[i] = mfma_bf16(kb, kb, dk[i]);
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          u32x4 kj = {__float_as_uint(kf[j].v[0]), __float_as_uint(kf[j].v[1]), __float_as_uint(kf[j].v[2]),
-                      __float_as_uint(kf[j].v[3])};
-          cross[i][j] = mfma_bf16(qb, __builtin_bit_cast(bf16x8, kj), cross[i][j]);
+        for (int s = 0; s < 4; ++s) {
+          qf[i].v[s] = a0[s]; qf[i].v[4 + s] = a1[s];
+          kf[i].v[s] = b0[s]; kf[i].v[4 + s] = b1[s];
         }
-      } else {
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           dq[i] = mfma_f32(qf[i].v[s], qf[i].v[s], dq[i]);
@@ -139,7 +182,8 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
 
   // ---- reduce the 4 waves (fixed order) and write this split's record
   // D layout: lane holds rows 4*lg + r (q channel within block i), column lc (k channel)
-  float* my = red[wave];
+  __syncthreads();  // the transpose tile is free: reuse it as the reduction buffer
+  float* my = red + wave * REC;
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
 #pragma unroll
@@ -154,23 +198,40 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
     }
   }
   __syncthreads();
-  float* out = part + ((int64_t)nh * nsplit + blockIdx.x) * gram_rec_floats(NB);
-  for (int e = tid; e < CP * CP + 2 * CP; e += 256) out[e] = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
+  float* out = part + ((int64_t)nh * nsplit + blockIdx.x) * REC;
+  for (int e = tid; e < REC; e += 256)
+    out[e] = ((red[e] + red[REC + e]) + red[2 * REC + e]) + red[3 * REC + e];
+}
+
+// part [nh][nsplit][rec] -> part2 [nh][RS][rec]: slice s sums splits [s * per, (s + 1) * per)
+__global__ void __launch_bounds__(256) gram_reduce_kernel(const float* __restrict__ part, float* __restrict__ part2,
+                                                          int64_t rec, int nsplit) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nh = blockIdx.y, sl = blockIdx.z;
+  if (e >= rec) return;
+  const int per = (nsplit + GP_RS - 1) / GP_RS;
+  const int s0 = sl * per;
+  const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
+  const float* src = part + ((int64_t)nh * nsplit) * rec + e;
+  float s = 0.f;
+  for (int sp = s0; sp < s1; ++sp) s += src[(int64_t)sp * rec];
+  part2[((int64_t)nh * GP_RS + sl) * rec + e] = s;
 }
 
 template <int NB>
-__global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restrict__ part, const float* __restrict__ temp,
-                                                          float* __restrict__ out, int ch, int heads, int nsplit) {
+__global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restrict__ part2, const float* __restrict__ temp,
+                                                          float* __restrict__ out, int ch, int heads) {
   constexpr int CP = NB * 16;
+  constexpr int REC = CP * CP + 2 * CP;
   __shared__ float g[CP * CP];
   __shared__ float nq[CP], nk[CP];
   const int nh = blockIdx.x;
   const int hd = nh % heads;
-  const int64_t rec = gram_rec_floats(NB);
-  const float* src = part + (int64_t)nh * nsplit * rec;
-  for (int e = threadIdx.x; e < CP * CP + 2 * CP; e += 256) {
+  const float* src = part2 + (int64_t)nh * GP_RS * REC;
+  for (int e = threadIdx.x; e < REC; e += 256) {
     float s = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) s += src[sp * rec + e];
+#pragma unroll
+    for (int sl = 0; sl < GP_RS; ++sl) s += src[sl * REC + e];
     if (e < CP * CP) g[e] = s;
     else if (e < CP * CP + CP) nq[e - CP * CP] = rsqrtf(fmaxf(s, 1e-24f));
     else nk[e - CP * CP - CP] = rsqrtf(fmaxf(s, 1e-24f));
@@ -210,7 +271,7 @@ extern "C" size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t 
   if (batch <= 0 || hw <= 0 || c <= 0 || heads <= 0 || c % heads) return 0;
   const int64_t ch = c / heads;
   const int64_t nsplit = cdiv(hw, split_len_for(batch, heads, hw));
-  return (size_t)(batch * heads * nsplit * gram_rec_floats(pick_nb(ch)) * sizeof(float));
+  return (size_t)(batch * heads * (nsplit + GP_RS) * gram_rec_floats(pick_nb(ch)) * sizeof(float));
 }
 
 extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,
@@ -230,9 +291,12 @@ extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, 
   const int64_t len = split_len_for(batch, heads, hw);
   const int nsplit = (int)cdiv(hw, len);
   const int nb = pick_nb(ch);
+  const int64_t rec = gram_rec_floats(nb);
   hipStream_t s = (hipStream_t)stream;
   dim3 g1((unsigned)nsplit, (unsigned)(batch * heads));
+  dim3 g2((unsigned)cdiv(rec, 256), (unsigned)(batch * heads), GP_RS);
   float* part = (float*)scratch;
+  float* part2 = part + batch * heads * nsplit * rec;
 #define CLARUS_GRAM(NB)                                                                                       \
   do {                                                                                                        \
     if (qkv_dtype == DT_BF16)                                                                                 \
@@ -241,8 +305,9 @@ extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, 
     else                                                                                                      \
       hipLaunchKernelGGL((gram_partial_kernel<NB, DT_F32>), g1, dim3(256), 0, s, qkv, part, hw, (int)c,       \
                          (int)ch, (int)heads, len, nsplit);                                                   \
-    hipLaunchKernelGGL((gram_finish_kernel<NB>), dim3((unsigned)(batch * heads)), dim3(256), 0, s, part,      \
-                       temperature, out, (int)ch, (int)heads, nsplit);                                        \
+    hipLaunchKernelGGL(gram_reduce_kernel, g2, dim3(256), 0, s, part, part2, rec, nsplit);                     \
+    hipLaunchKernelGGL((gram_finish_kernel<NB>), dim3((unsigned)(batch * heads)), dim3(256), 0, s, part2,     \
+                       temperature, out, (int)ch, (int)heads);                                                \
   } while (0)
   switch (nb) {
     case 1: CLARUS_GRAM(1); break;

@@ -23,6 +23,7 @@ typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 
 enum : int { DT_F32 = 0, DT_BF16 = 1 };
+enum : int { ACT_NONE = 0, ACT_GELU = 1, ACT_LRELU = 2 };
 
 struct f32x8 {
   float v[8];

@@ -31,7 +31,6 @@ namespace clarus {
 enum : int { PRO_NONE = 0, PRO_LN = 1, PRO_MUL = 2, PRO_RMS = 3, PRO_LNMUL = 5 };
 enum : int { AM_ROWS = 0, AM_S2D = 1, AM_CONV3 = 2 };
 enum : int { CM_ROWS = 0, CM_SHUFFLE = 1, CM_NCHW = 2 };
-enum : int { ACT_NONE = 0, ACT_GELU = 1, ACT_LRELU = 2 };
 enum : int { OPM_BF16 = 0, OPM_SPLIT = 1, OPM_F32 = 2 };
 
 struct GemmP {

@@ -1,0 +1,149 @@
+// Depthwise 3x3 convolution with fused gates on gfx950 (NHWC, HBM-bound streaming kernel).
+//
+//   y[p, c] = b[c] + sum_{ky, kx} w[c, ky, kx] * x[p + dil * (ky - 1, kx - 1), c]   ('same' zero padding)
+//   gate 0: out = act(y)                          (C channels)
+//   gate 1: out = y[:, :C/2] * y[:, C/2:]         (SimpleGate)
+//   gate 2: out = gelu(y[:, :C/2]) * y[:, C/2:]   (GELU gate, Restormer / FFTformer GDFN)
+//   act 1 (gate 0 only): out = gelu(y)
+// Semantics of the reference backend's dwconv (python/clarus/ops/torch_ref.py:143-155): fp32
+// math, one cast to the output dtype at the end.
+//
+// A thread computes 8 consecutive output channels of one pixel: per tap one 16-byte load of
+// each input half (bf16) or two (fp32), fp32 FMAs with the tap weights read from LDS, then
+// the gate and a 16-byte store. Lanes are channel-group-minor, so a wave reads whole pixel
+// rows; the 3x3 neighbourhood is re-read from L1 / L2.
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace clarus {
+
+struct DwP {
+  const void* x;
+  const float* w;   // [C_in][9] fp32 taps (row-major ky, kx)
+  const float* b;   // [C_in] fp32 or null
+  void* out;
+  int64_t n, h, w_, cin, cout;  // cout = cin / 2 with a gate
+  int dil, gate, act, x_dt, o_dt;
+};
+
+template <int XDT, int GATE>
+__global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
+  extern __shared__ __attribute__((aligned(16))) float wsh[];  // [9][cin] taps, then [cin] bias
+  const int64_t cin = p.cin;
+  for (int64_t i = threadIdx.x; i < 9 * cin; i += 256) {
+    const int64_t c = i % cin, t = i / cin;
+    wsh[i] = p.w[c * 9 + t];
+  }
+  for (int64_t i = threadIdx.x; i < cin; i += 256) wsh[9 * cin + i] = p.b ? p.b[i] : 0.f;
+  __syncthreads();
+
+  constexpr int XES = (XDT == DT_BF16) ? 2 : 4;
+  const int64_t groups = p.cout / 8;  // output channel groups of 8
+  const int64_t total = p.n * p.h * p.w_ * groups;
+  const int64_t half = GATE ? p.cout : 0;  // channel offset of the second half
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    const int64_t pix = t / groups;
+    const int64_t g = t - pix * groups;
+    const int64_t c0 = g * 8;
+    const int64_t hw = p.h * p.w_;
+    const int64_t img = pix / hw;
+    const int64_t r = pix - img * hw;
+    const int y = (int)(r / p.w_), x = (int)(r - (r / p.w_) * p.w_);
+    float a1[8], a2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a1[i] = wsh[9 * cin + c0 + i];
+      a2[i] = GATE ? wsh[9 * cin + half + c0 + i] : 0.f;
+    }
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+      const int yy = y + (ky - 1) * p.dil;
+      if (yy < 0 || yy >= p.h) continue;
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const int xx = x + (kx - 1) * p.dil;
+        if (xx < 0 || xx >= p.w_) continue;
+        const int tap = ky * 3 + kx;
+        const unsigned char* src = (const unsigned char*)p.x + (((img * p.h + yy) * p.w_ + xx) * cin + c0) * XES;
+        const f32x8 v1 = load8<XDT>(src);
+        const float* wt = wsh + tap * cin + c0;
+        const f32x4 w1a = *reinterpret_cast<const f32x4*>(wt), w1b = *reinterpret_cast<const f32x4*>(wt + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a1[i] = fmaf(w1a[i], v1.v[i], a1[i]);
+          a1[4 + i] = fmaf(w1b[i], v1.v[4 + i], a1[4 + i]);
+        }
+        if constexpr (GATE != 0) {
+          const f32x8 v2 = load8<XDT>(src + half * XES);
+          const f32x4 w2a = *reinterpret_cast<const f32x4*>(wt + half);
+          const f32x4 w2b = *reinterpret_cast<const f32x4*>(wt + half + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            a2[i] = fmaf(w2a[i], v2.v[i], a2[i]);
+            a2[4 + i] = fmaf(w2b[i], v2.v[4 + i], a2[4 + i]);
+          }
+        }
+      }
+    }
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (GATE == 1) o[i] = a1[i] * a2[i];
+      else if constexpr (GATE == 2) o[i] = gelu_erf(a1[i]) * a2[i];
+      else o[i] = p.act == ACT_GELU ? gelu_erf(a1[i]) : a1[i];
+    }
+    const int64_t oo = pix * p.cout + c0;
+    if (p.o_dt == DT_BF16) {
+      u32x4 q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        q[i] = (unsigned)f32_to_bf16_bits(o[2 * i]) | ((unsigned)f32_to_bf16_bits(o[2 * i + 1]) << 16);
+      *reinterpret_cast<u32x4*>((unsigned short*)p.out + oo) = q;
+    } else {
+      float* op = (float*)p.out + oo;
+      *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<f32x4*>(op + 4) = f32x4{o[4], o[5], o[6], o[7]};
+    }
+  }
+}
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float* w, const float* bias, void* out,
+                                    int32_t o_dtype, int64_t n, int64_t h, int64_t wd, int64_t c, int32_t dil,
+                                    int32_t gate, int32_t act, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(x && w && out, "dwconv3x3: null operand");
+  CLARUS_REQUIRE(n > 0 && h > 0 && wd > 0 && c > 0, "dwconv3x3: empty problem");
+  CLARUS_REQUIRE((x_dtype == DT_BF16 || x_dtype == DT_F32) && (o_dtype == DT_BF16 || o_dtype == DT_F32),
+                 "dwconv3x3: bad dtype");
+  CLARUS_REQUIRE(gate >= 0 && gate <= 2 && (act == 0 || (act == ACT_GELU && gate == 0)) && dil >= 1,
+                 "dwconv3x3: bad gate / act / dilation");
+  const int64_t cout = gate ? c / 2 : c;
+  CLARUS_REQUIRE((gate == 0 || c % 2 == 0) && cout % 8 == 0, "dwconv3x3: output channels must be a multiple of 8");
+  CLARUS_REQUIRE(aligned(x, 16) && aligned(out, 16) && aligned(w, 16), "dwconv3x3: 16-byte alignment");
+  const size_t lds = (size_t)10 * c * sizeof(float);
+  CLARUS_REQUIRE(lds <= 160 * 1024, "dwconv3x3: %lld channels exceed the LDS tap table", (long long)c);
+  DwP p{x, w, bias, out, n, h, wd, c, cout, dil, gate, act, x_dtype, o_dtype};
+  const int64_t total = n * h * wd * (cout / 8);
+  int64_t blocks = cdiv(total, 256);
+  if (blocks > 8192) blocks = 8192;
+  hipStream_t s = (hipStream_t)stream;
+#define DW_LAUNCH(XDT, G)                                                                                  \
+  do {                                                                                                     \
+    static const bool attr = (hipFuncSetAttribute(reinterpret_cast<const void*>(&dwconv3x3_kernel<XDT, G>), \
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024), \
+                              true);                                                                       \
+    (void)attr;                                                                                            \
+    hipLaunchKernelGGL((dwconv3x3_kernel<XDT, G>), dim3((unsigned)blocks), dim3(256), lds, s, p);          \
+  } while (0)
+  if (x_dtype == DT_BF16) {
+    if (gate == 1) DW_LAUNCH(DT_BF16, 1); else if (gate == 2) DW_LAUNCH(DT_BF16, 2); else DW_LAUNCH(DT_BF16, 0);
+  } else {
+    if (gate == 1) DW_LAUNCH(DT_F32, 1); else if (gate == 2) DW_LAUNCH(DT_F32, 2); else DW_LAUNCH(DT_F32, 0);
+  }
+#undef DW_LAUNCH
+  return check_launch("dwconv3x3");
+}

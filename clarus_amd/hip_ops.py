@@ -8,7 +8,8 @@ adapter (python/clarus/ops/triton_cuda.py): arguments the kernels do not handle 
 `Unsupported` BEFORE anything is launched; a failure inside the library raises RuntimeError.
 
 Ops served: linear, down, up, intro, ending, conv3x3, channel_attention, linear_per_image,
-patch_filter, linear_patch_filter, patch_corr, ln_mul_linear.
+patch_filter, linear_patch_filter, patch_corr, ln_mul_linear (the GEMM family), plus dwconv
+(depthwise 3x3 + gates, the next op on the NAFNet forward) and attention_apply (MDTA attn . V).
 
 Capture safety: kernels launch on torch's current stream, scratch comes from torch's
 allocator, weight re-layouts are computed once through `Backend.cached` (in the eager warm-up
@@ -267,6 +268,26 @@ class HipOps(Backend):
             raise Unsupported("conv3x3: bf16 / fp32, cin % 8 == 0, 16-byte pixel rows")
         return self._conv(x, w, b, odt=odt, act=act, residual=residual, out_scale=out_scale, up2=up2, out=out,
                           slope=slope)
+
+    def dwconv(self, x, w, b, dil=1, gate=False, act=None):
+        """Depthwise 3x3 conv with fused SimpleGate / GELU gate / GELU (not GEMM-shaped; the
+        reference serves it from its torch or Triton backend, ops/torch_ref.py:143-155)."""
+        kh, kw = w.shape[-2:]
+        n, h, wd, c = x.shape
+        gcode = {False: 0, None: 0, True: 1, "mul": 1, "gelu": 2}.get(gate, -1)
+        cout = c // 2 if gcode else c
+        if ((kh, kw) != (3, 3) or tuple(w.shape[:2]) != (c, 1) or gcode < 0 or act not in (None, "gelu")
+                or (act == "gelu" and gcode) or dil < 1 or not _dense(x, b)):
+            raise Unsupported("dwconv: contiguous 3x3 depthwise, gate none / mul / gelu, act none / gelu")
+        if not (_kdt(x) and (gcode == 0 or c % 2 == 0) and cout % 8 == 0 and _vec16(x) and 10 * c * 4 <= 160 * 1024):
+            raise Unsupported("dwconv: bf16 / fp32, output channels % 8 == 0")
+        taps = self.cached(w, "dw9", lambda t: t.float().reshape(t.shape[0], 9).contiguous())
+        out = torch.empty((n, h, wd, cout), device=x.device, dtype=self.dtype)
+        _lib.check(self.lib.clarus_hip_dwconv3x3(
+            x.data_ptr(), _lib.dtype_code(x.dtype), taps.data_ptr(), _lib.ptr(self._bias(b)), out.data_ptr(),
+            _lib.dtype_code(self.dtype), n, h, wd, c, int(dil), gcode, _lib.ACT_GELU if act == "gelu" else 0,
+            self._stream(x)), "dwconv")
+        return out
 
     # ------------------------------------------------------------------ attention
     def channel_attention(self, qkv, heads, temperature):

@@ -176,6 +176,19 @@ int clarus_hip_patch_corr(const void* x, int32_t x_dtype, int64_t sn, int64_t sh
                           const float* fwd, const float* inv, float* out, int64_t batch,
                           int64_t h, int64_t w, int64_t c, void* stream);
 
+/*
+ * Depthwise 3x3 convolution, 'same' zero padding, dilation dil, fused gate (NHWC):
+ *   y = conv_dw(x) + bias;  gate 0: out = act(y) (act CLARUS_ACT_NONE / CLARUS_ACT_GELU),
+ *   gate 1: out = y[:, :c/2] * y[:, c/2:],  gate 2: out = gelu(y[:, :c/2]) * y[:, c/2:].
+ * x [n, h, w, c] contiguous (x_dtype); w [c][9] fp32 taps (ky, kx); bias [c] fp32 or NULL;
+ * out [n, h, w, c or c/2] contiguous (o_dtype). Output channels must be a multiple of 8.
+ * Not a GEMM: the reference runs it on its torch backend (ops/torch_ref.py:143-155) or its
+ * Triton dwconv (kernels/spatial.py:95-214); replaces the latter.
+ */
+int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float* w, const float* bias, void* out,
+                         int32_t o_dtype, int64_t n, int64_t h, int64_t w_, int64_t c, int32_t dil,
+                         int32_t gate, int32_t act, void* stream);
+
 /* ABI version (CLARUS_HIP_ABI_VERSION) and struct sizes, for binding checks. */
 int clarus_hip_abi_version(void);
 size_t clarus_hip_sizeof_gemm_args(void);

@@ -141,3 +141,27 @@ def test_config5_upconv(h, w, hip_bf16):
     b = torch.zeros(64)
     got = hip_bf16.conv3x3(x.cuda(), wt.cuda(), b.cuda(), act="lrelu", up2=True)
     check(got.cpu(), REF.conv3x3(x, wt, b, act="lrelu", up2=True, out_dtype=torch.float32), f"upconv {h}x{w}")
+
+
+# ------------------------------------------------------------------ depthwise 3x3 (next op on the NAFNet path)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gate,act,dil", [(True, None, 1), ("gelu", None, 1), (False, None, 1),
+                                          (False, "gelu", 1), (False, None, 2)])
+def test_dwconv(dt, gate, act, dil, hip_bf16, hip_f32):
+    """Depthwise 3x3 + SimpleGate / GELU gate / GELU / dilation 2 (tools/test_kernels.py:110-121,
+    193-199), odd sizes."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(8)
+    c = 96
+    x, w, b = rnd(g, 2, 37, 53, c, dtype=dt), rnd(g, c, 1, 3, 3), rnd(g, c)
+    got = hip.dwconv(x.cuda(), w.cuda(), b.cuda(), dil=dil, gate=gate, act=act)
+    ref = TorchRef(torch.float32, "cpu").dwconv(x, w, b, dil=dil, gate=gate, act=act)
+    check(got.cpu(), ref, f"dwconv gate={gate} act={act} dil={dil} {dt}")
+
+
+def test_dwconv_nafnet_720p(hip_bf16):
+    """NAFNet level 0: 1x720x1280x128 -> SimpleGate -> 64 channels."""
+    g = gen(9)
+    x, w, b = rnd(g, 1, 720, 1280, 128, dtype=torch.bfloat16), rnd(g, 128, 1, 3, 3), rnd(g, 128)
+    got = hip_bf16.dwconv(x.cuda(), w.cuda(), b.cuda(), gate=True)
+    check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, w, b, gate=True), "dwconv 720p gate")
