@@ -19,6 +19,12 @@ Extra fields of the JSON line:
 
   python bench.py --summarize-trace DIR   per-(kernel, grid) durations from a rocprofv3
                                           kernel trace written under DIR
+
+HBM traffic of the step's kernels (roofline.traffic), from two rocprofv3 counter passes of
+`python bench.py --pmc-pass` (FETCH_SIZE, then WRITE_SIZE): that mode ends with one plain copy
+kernel of known size (256 MiB read + 256 MiB written) followed by each step op once, and
+`python bench.py --summarize-pmc FETCH_DIR WRITE_DIR` scales each op's counters by the copy's
+(bytes per counted KiB) and writes profiles/pmc_traffic.json.
 """
 from __future__ import annotations
 
@@ -62,6 +68,52 @@ def summarize_trace(directory: str) -> None:
         short = name if len(name) < 110 else name[:107] + "..."
         print(f"{len(d):6d} {statistics.mean(d):9.2f} {statistics.median(d):9.2f} {sum(d) / 1e3:9.3f}  "
               f"{'x'.join(g for g in grid if g)}  {short}")
+
+
+COPY_BYTES = 256 * 1024 * 1024  # the pmc pass's calibration copy: this many bytes read and written
+
+
+def _pmc_dispatches(directory: str, counter: str) -> list:
+    """(dispatch id, kernel name, counter value) of every dispatch in a rocprofv3 --pmc run."""
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {directory}")
+    vals: dict = {}
+    for f in files:
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = int(row["Dispatch_Id"])
+                name, v = row.get("Kernel_Name", "?"), float(row["Counter_Value"])
+                prev = vals.get(key)
+                vals[key] = (name, v + (prev[1] if prev else 0.0))
+    return [(k, vals[k][0], vals[k][1]) for k in sorted(vals)]
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
+    """Per-op HBM bytes of the step from the two counter passes of `--pmc-pass` (see above)."""
+    from clarus_amd.workloads import config2_names
+    names = config2_names()
+    out = {"ops": {}, "copy_bytes": COPY_BYTES}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        d = _pmc_dispatches(directory, counter)
+        tail = d[-(len(names) + 1):]
+        copy, ops = tail[0], tail[1:]
+        if "clarus" in copy[1] or not all("clarus" in o[1] for o in ops):
+            raise SystemExit(f"{counter}: the last dispatches are not the copy + step ops: {[t[1][:40] for t in tail]}")
+        factor = COPY_BYTES / (copy[2] * 1024.0)  # bytes per counted KiB, from the known copy
+        out[f"{counter.lower()}_copy_kib"] = copy[2]
+        out[f"{counter.lower()}_factor"] = round(factor, 4)
+        for nm, o in zip(names, ops):
+            out["ops"].setdefault(nm, {})[counter.lower() + "_bytes"] = round(o[2] * 1024.0 * factor)
+            out["ops"][nm]["kernel"] = o[1][:120]
+    for nm, v in out["ops"].items():
+        v["bytes_per_launch"] = v.get("fetch_size_bytes", 0) + v.get("write_size_bytes", 0)
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def cpu_baseline_config2(steps_cpu: int = 3) -> dict:
@@ -119,9 +171,14 @@ def main() -> None:
     ap.add_argument("--no-ops", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--summarize-trace", default=None)
+    ap.add_argument("--pmc-pass", action="store_true", help="one copy + each step op once (counter runs)")
+    ap.add_argument("--summarize-pmc", nargs=2, default=None, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path shards "
@@ -145,6 +202,19 @@ def main() -> None:
     step = wl.config2_cases(hip, dev)
     flops_step = sum(c.flops for c in step)
     log(f"[bench] config-2 step: {len(step)} GEMMs, {flops_step / 1e9:.2f} GFLOP")
+    if args.pmc_pass:  # the last dispatches of the process: the calibration copy, then each op once
+        for c in step:
+            c.run()
+        src = torch.randn(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        keep = []
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)
+        for c in step:
+            keep.append(c.run())
+        torch.cuda.synchronize()
+        log(f"[bench] pmc pass: copy of {COPY_BYTES} B, then {[c.name for c in step]}")
+        return
     for _ in range(args.warmup):
         for c in step:
             c.run()
@@ -188,8 +258,7 @@ def main() -> None:
     if os.path.exists(tfile):
         with open(tfile) as fh:
             t = json.load(fh)
-        if t.get("op") == dc.name:
-            traffic = t.get("bytes_per_launch")
+        traffic = t.get("ops", {}).get(dc.name, {}).get("bytes_per_launch")
     roofline = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": unit, "frac": round(ach / peak, 3),
                 "traffic": traffic, "kernel": f"gemm_kernel ({dc.name})", "avg_us": round(dus, 2),
                 "algorithmic_bytes": int(dc.nbytes), "algorithmic_flops": int(dc.flops)}

@@ -57,6 +57,11 @@ def _kaiming_uniform_kn(g, cin, cout):
 CONFIG2_LEVELS = [(64, 720, 1280), (128, 360, 640), (256, 180, 320), (512, 90, 160), (1024, 45, 80)]
 
 
+def config2_names() -> list[str]:
+    """Names of the config-2 step ops, in the order config2_cases builds them."""
+    return [n for c, _, _ in CONFIG2_LEVELS for n in (f"c{c} expand+gate", f"c{c} c->c+scale+res")]
+
+
 def config2_cases(hip, device, seed: int = 0) -> list[OpCase]:
     """Per level: u = linear(x, We, be, gate=True); y = linear(u, Wc, bc, scale=beta, residual=r)."""
     cases = []
