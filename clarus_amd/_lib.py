@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the kernel library
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libclarus_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "clarus_hip.h")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 OK, EINVAL, ELAUNCH = 0, 1, 2
 F32, BF16 = 0, 1
 PRO_NONE, PRO_LN, PRO_MUL, PRO_RMS, PRO_LNMUL = 0, 1, 2, 3, 5
@@ -29,7 +29,7 @@ _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.
 class GemmArgs(ctypes.Structure):
     _fields_ = [
         ("a", _vp), ("wt", _vp), ("c", _vp), ("bias", _vp), ("scale", _vp), ("res", _vp),
-        ("small", _vp), ("m2", _vp), ("lnw", _vp), ("lnb", _vp),
+        ("small", _vp), ("m2", _vp), ("lnw", _vp), ("lnb", _vp), ("stats", _vp),
         ("m", _i64), ("n", _i64), ("k", _i64), ("batch", _i64),
         ("lda", _i64), ("ldc", _i64), ("ldr", _i64), ("ldm2", _i64),
         ("a_bstride", _i64), ("w_bstride", _i64), ("c_bstride", _i64), ("r_bstride", _i64),

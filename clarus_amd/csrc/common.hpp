@@ -21,6 +21,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
 
 enum : int { DT_F32 = 0, DT_BF16 = 1 };
 enum : int { ACT_NONE = 0, ACT_GELU = 1, ACT_LRELU = 2 };

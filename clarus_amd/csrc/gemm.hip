@@ -1,7 +1,10 @@
 // C entry points of the fused GEMM family: clarus_hip_gemm, clarus_hip_conv3x3,
 // clarus_hip_intro3x3. Argument checks happen here, before any launch.
+#include <algorithm>
+
 #include "capi.hpp"
 #include "gemm_dispatch.hpp"
+#include "gemm_lds_dispatch.hpp"
 #include "gemm_stream_dispatch.hpp"
 
 namespace clarus {
@@ -60,6 +63,70 @@ static dim3 grid_for(int64_t ptiles, int64_t ntiles, int64_t batch, int64_t k, i
   return dim3((unsigned)gx, (unsigned)ntiles, (unsigned)batch);
 }
 
+// ------------------------------------------------------------------- LayerNorm / RMS statistics
+// One wave per row (persistent over rows): the row is read once into registers (up to 2048
+// elements; longer rows are re-read for the second pass), exact two-pass mean and variance,
+// wave-wide butterfly sums (fixed order, deterministic). stats[2 r] = mean (0 for RMS),
+// stats[2 r + 1] = rsqrt(var + eps) (rsqrt(mean(x^2) + eps) for RMS).
+// Semantics of kernels/gemm.py:289-313 row_stats / ops/torch_ref.py:94-100.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int TA>
+__global__ void __launch_bounds__(256) row_stats_kernel(const void* a, int64_t lda, int64_t m, int64_t k, int rms,
+                                                        float eps, float* stats) {
+  constexpr int ES = TA == DT_BF16 ? 2 : 4;
+  constexpr int CACHED = 4;  // fragments of 8 per lane kept in registers (K <= 2048)
+  const int lane = threadIdx.x & 63;
+  const float invk = 1.0f / (float)k;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < m; row += (int64_t)gridDim.x * 4) {
+    const unsigned char* base = (const unsigned char*)a + row * lda * ES;
+    f32x8 x[CACHED];
+#pragma unroll
+    for (int j = 0; j < CACHED; ++j) {
+      const int64_t kk = (int64_t)(j * 64 + lane) * 8;
+      x[j] = kk < k ? load8<TA>(base + kk * ES) : zero8();
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < CACHED; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += x[j].v[i];
+    for (int64_t kk = (int64_t)(CACHED * 64 + lane) * 8; kk < k; kk += 512) {
+      const f32x8 t = load8<TA>(base + kk * ES);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += t.v[i];
+    }
+    const float mean = rms ? 0.f : wave_sum(s) * invk;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < CACHED; ++j) {
+      if ((int64_t)(j * 64 + lane) * 8 >= k) continue;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { const float d = x[j].v[i] - mean; ss += d * d; }
+    }
+    for (int64_t kk = (int64_t)(CACHED * 64 + lane) * 8; kk < k; kk += 512) {
+      const f32x8 t = load8<TA>(base + kk * ES);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { const float d = t.v[i] - mean; ss += d * d; }
+    }
+    const float rstd = rsqrtf(wave_sum(ss) * invk + eps);
+    if (lane == 0) *reinterpret_cast<f32x2*>(stats + 2 * row) = f32x2{mean, rstd};
+  }
+}
+
+static void launch_row_stats(const void* a, int a_dt, int64_t lda, int64_t m, int64_t k, bool rms, float eps,
+                             float* stats, hipStream_t s) {
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(m, 4), 2048);
+  if (a_dt == DT_BF16)
+    hipLaunchKernelGGL(row_stats_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, a, lda, m, k, (int)rms, eps, stats);
+  else
+    hipLaunchKernelGGL(row_stats_kernel<DT_F32>, dim3(blocks), dim3(256), 0, s, a, lda, m, k, (int)rms, eps, stats);
+}
+
 static int launch(GemmP& p, int am, bool gate, int opm, int ta, int tile, int64_t batch,
                   hipStream_t s, const char* what) {
   if (tile < 0 || tile >= kNumTiles) {
@@ -111,6 +178,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   p.a = a->a; p.wt = a->wt; p.c = a->c;
   p.bias = a->bias; p.scale = a->scale; p.res = a->res;
   p.small = a->small; p.m2 = a->m2; p.lnw = a->lnw; p.lnb = a->lnb;
+  p.stats = nullptr;
   p.m = a->m; p.n = a->n; p.k = a->k;
   p.lda = a->lda; p.ldc = a->ldc; p.ldr = a->ldr; p.ldm2 = a->ldm2;
   p.a_bs = a->a_bstride; p.w_bs = a->w_bstride; p.c_bs = a->c_bstride; p.r_bs = a->r_bstride;
@@ -174,6 +242,34 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     }
     CLARUS_REQUIRE(a->tile == 0, "gemm: no streaming kernel for K=%lld nb=%d", (long long)a->k, nb);
   }
+  // pipelined LDS-tiled kernel for long-K row operands (tile 0 = auto for K > 128, 10 = force);
+  // LN-type prologues need the statistics scratch there
+  const bool ln_like = a->pro == PRO_LN || a->pro == PRO_RMS || a->pro == PRO_LNMUL;
+  const bool lds_shape = a->a_mode == CLARUS_A_ROWS && opm != OPM_F32 && a->batch == 1 &&
+                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
+  const bool use_lds = lds_shape && (a->tile == 10 || (a->tile == 0 && a->k > 128)) && (!ln_like || a->stats);
+  CLARUS_REQUIRE(a->tile != 10 || use_lds, "gemm: the pipelined tile kernel does not take this problem");
+  const bool needs_stats = a->a_mode == CLARUS_A_ROWS && ln_like && (use_lds || a->k > kc_for(opm));
+  if (needs_stats && a->stats && a->batch == 1) {  // one pass over A instead of one per column tile
+    CLARUS_REQUIRE(aligned(a->stats, 8), "gemm: stats scratch must be 8-byte aligned");
+    launch_row_stats(a->a, a->a_dtype, a->lda, a->m, a->k, a->pro == PRO_RMS, a->ln_eps, a->stats,
+                     (hipStream_t)stream);
+    p.stats = a->stats;
+  }
+  // bf16 operands without prologue: the multi-stage DMA pipeline (tile 11 forces it)
+  const bool dma_ok = lds_shape && opm == OPM_BF16 && a->pro == PRO_NONE && a->k % 32 == 0 &&
+                      (a->lda * 2) % 16 == 0;
+  CLARUS_REQUIRE(a->tile != 11 || dma_ok, "gemm: the DMA-pipelined kernel does not take this problem");
+  if (dma_ok && (a->tile == 11 || (use_lds && a->tile == 0))) {
+    launch_gemm_dma(p, a->gate != 0, (hipStream_t)stream);
+    return check_launch("gemm");
+  }
+  if (use_lds) {
+    const bool x2 = a->pro == PRO_MUL || a->pro == PRO_LNMUL;
+    CLARUS_REQUIRE(launch_gemm_lds(p, a->gate != 0, opm, a->a_dtype, x2, (hipStream_t)stream),
+                   "gemm: no pipelined tile kernel for operand mode %d A dtype %d", opm, a->a_dtype);
+    return check_launch("gemm");
+  }
   const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(a->m, a->n, a->k, a->batch, a->gate != 0, opm, run_div);
   CLARUS_REQUIRE(tile >= 0 && tile < kNumTiles && (!run_div || run_div % (4 * kTileNB[tile]) == 0),
                  "gemm: tile %d does not fit the pixel-shuffle quadrant width", tile + 1);
@@ -222,33 +318,65 @@ extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
 }
 
 // ------------------------------------------------------------------- intro 3 -> C conv
-// One thread per (pixel, 4-channel group): 27 loads of the 3x3x3 window, 27 x 4 FMAs.
+// One thread per (pixel, 8 output channels), lanes channel-group-minor so a wave stores whole
+// pixel rows: 27 input loads (shared through L1 by the threads of a pixel), 27 x 8 fp32 FMAs
+// with the taps read from LDS as 16-byte vectors, one 16-byte bf16 store (two for fp32).
+// Persistent grid; all index math in 32 bits (the host checks the sizes).
+template <int ODT>
 __global__ void __launch_bounds__(256) intro_kernel(const float* __restrict__ inp, const float* __restrict__ wt,
-                                                    const float* __restrict__ bias, void* out, int out_dt,
-                                                    int64_t m, int h, int w, int cout) {
-  const int groups = (cout + 3) / 4;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= m * groups) return;
-  const int64_t q = t / groups;
-  const int c0 = (int)(t - q * groups) * 4;
-  const int64_t hw = (int64_t)h * w;
-  const int64_t img = q / hw;
-  const int rr = (int)(q - img * hw);
-  const int y = rr / w, x = rr - (rr / w) * w;
-  float acc[4];
-  for (int i = 0; i < 4; ++i) acc[i] = (c0 + i < cout) ? bias[c0 + i] : 0.f;
-  for (int tap = 0; tap < 9; ++tap) {
-    const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
-    if (yy < 0 || yy >= h || xx < 0 || xx >= w) continue;
-    for (int c = 0; c < 3; ++c) {
-      const float v = inp[(img * 3 + c) * hw + (int64_t)yy * w + xx];
-      const float* wr = wt + (tap * 3 + c) * cout + c0;
-      for (int i = 0; i < 4; ++i)
-        if (c0 + i < cout) acc[i] = fmaf(v, wr[i], acc[i]);
+                                                    const float* __restrict__ bias, void* out, int m, int h,
+                                                    int w, int cout) {
+  extern __shared__ __attribute__((aligned(16))) float wsh[];  // [27][cout] taps, then [cout] bias
+  for (int i = threadIdx.x; i < 28 * cout; i += 256) wsh[i] = i < 27 * cout ? wt[i] : bias[i - 27 * cout];
+  __syncthreads();
+  const int groups = cout >> 3;
+  const int total = m * groups;
+  const int hw = h * w;
+  for (int t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
+    const int q = t / groups;
+    const int c0 = (t - q * groups) * 8;
+    const int img = q / hw;
+    const int rr = q - img * hw;
+    const int y = rr / w, x = rr - (rr / w) * w;
+    const float* plane = inp + (int64_t)img * 3 * hw;
+    f32x4 a0 = *reinterpret_cast<const f32x4*>(wsh + 27 * cout + c0);
+    f32x4 a1 = *reinterpret_cast<const f32x4*>(wsh + 27 * cout + c0 + 4);
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+      const int yy = y + ky - 1;
+      if (yy < 0 || yy >= h) continue;
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const int xx = x + kx - 1;
+        if (xx < 0 || xx >= w) continue;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          const float v = plane[c * hw + yy * w + xx];
+          const float* wr = wsh + ((ky * 3 + kx) * 3 + c) * cout + c0;
+          const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr);
+          const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            a0[i] = fmaf(v, w0[i], a0[i]);
+            a1[i] = fmaf(v, w1[i], a1[i]);
+          }
+        }
+      }
+    }
+    const int64_t oo = (int64_t)q * cout + c0;
+    if constexpr (ODT == DT_BF16) {
+      u32x4 r;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        r[i] = (unsigned)f32_to_bf16_bits(a0[2 * i]) | ((unsigned)f32_to_bf16_bits(a0[2 * i + 1]) << 16);
+        r[2 + i] = (unsigned)f32_to_bf16_bits(a1[2 * i]) | ((unsigned)f32_to_bf16_bits(a1[2 * i + 1]) << 16);
+      }
+      *reinterpret_cast<u32x4*>((unsigned short*)out + oo) = r;
+    } else {
+      *reinterpret_cast<f32x4*>((float*)out + oo) = a0;
+      *reinterpret_cast<f32x4*>((float*)out + oo + 4) = a1;
     }
   }
-  for (int i = 0; i < 4; ++i)
-    if (c0 + i < cout) store1(out, out_dt, q * cout + c0 + i, acc[i]);
 }
 
 extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, void* out,
@@ -258,9 +386,18 @@ extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const floa
   CLARUS_REQUIRE(inp && wt && bias && out, "intro3x3: null operand");
   CLARUS_REQUIRE(batch > 0 && h > 0 && w > 0 && cout > 0, "intro3x3: empty problem");
   CLARUS_REQUIRE(dt_ok(out_dtype), "intro3x3: bad dtype");
+  CLARUS_REQUIRE(cout % 8 == 0 && cout <= 512, "intro3x3: cout must be a multiple of 8, at most 512");
+  CLARUS_REQUIRE(batch * h * w * (cout / 8) < ((int64_t)1 << 31), "intro3x3: problem too large for 32-bit indexing");
+  CLARUS_REQUIRE(aligned(out, 16) && aligned(wt, 16) && aligned(bias, 16), "intro3x3: 16-byte alignment");
   const int64_t m = batch * h * w;
-  const int64_t work = m * ((cout + 3) / 4);
-  hipLaunchKernelGGL(intro_kernel, dim3((unsigned)cdiv(work, 256)), dim3(256), 0, (hipStream_t)stream, inp, wt,
-                     bias, out, out_dtype, m, (int)h, (int)w, (int)cout);
+  const int64_t work = m * (cout / 8);
+  const size_t lds = (size_t)28 * cout * sizeof(float);
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(work, 256), 2048);
+  if (out_dtype == DT_BF16)
+    hipLaunchKernelGGL(intro_kernel<DT_BF16>, dim3(blocks), dim3(256), lds, (hipStream_t)stream, inp, wt, bias, out,
+                       (int)m, (int)h, (int)w, (int)cout);
+  else
+    hipLaunchKernelGGL(intro_kernel<DT_F32>, dim3(blocks), dim3(256), lds, (hipStream_t)stream, inp, wt, bias, out,
+                       (int)m, (int)h, (int)w, (int)cout);
   return check_launch("intro3x3");
 }

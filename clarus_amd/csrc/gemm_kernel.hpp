@@ -44,6 +44,7 @@ struct GemmP {
   const void* m2;
   const float* lnw;
   const float* lnb;
+  const float* stats;  // per-row (mean, rstd) from the statistics pass, or null
   int64_t m, n, k;
   int64_t lda, ldc, ldr, ldm2;
   int64_t a_bs, w_bs, c_bs, r_bs;
@@ -269,7 +270,14 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmP p) {
     float mean[PB], rstd[PB];
 #pragma unroll
     for (int b = 0; b < PB; ++b) { mean[b] = 0.f; rstd[b] = 1.f; }
-    if (stats && nchunks > 1) {
+    if (stats && nchunks > 1 && p.stats) {  // precomputed by the statistics pass
+#pragma unroll
+      for (int b = 0; b < PB; ++b) {
+        const f32x2 st = pval[b] ? *reinterpret_cast<const f32x2*>(p.stats + 2 * pix[b]) : f32x2{0.f, 1.f};
+        mean[b] = st[0];
+        rstd[b] = st[1];
+      }
+    } else if (stats && nchunks > 1) {
       const float invk = 1.0f / (float)K;
 #pragma unroll
       for (int b = 0; b < PB; ++b) {

@@ -1,0 +1,84 @@
+// gemm_lds_kernel instantiations and launcher.
+#include "capi.hpp"
+#include "gemm_dma.hpp"
+#include "gemm_lds.hpp"
+#include "gemm_lds_dispatch.hpp"
+
+namespace clarus {
+
+namespace {
+
+constexpr int kLdsKC = 32;
+
+template <int OPM, int TA, bool GATE, bool X2>
+void launch_one(GemmP& p, hipStream_t s) {
+  constexpr int lds = lt_lds_bytes(kLdsKC, OPM);
+  auto fn = &gemm_lds_kernel<OPM, TA, GATE, X2, kLdsKC>;
+  static const int per_cu = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), 256, lds) != hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  p.ptiles = cdiv(p.m, LT_P);
+  const int64_t tiles = p.ptiles * cdiv(p.n, LT_R / (GATE ? 2 : 1));
+  // persistent: every workgroup resident, a multiple of 8 so each XCD gets the same number
+  int64_t gx = 256LL * per_cu;
+  const int64_t need = cdiv(tiles, 8) * 8;
+  if (gx > need) gx = need;
+  hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), lds, s, p);
+}
+
+template <bool GATE>
+void launch_dma(GemmP& p, hipStream_t s) {
+  constexpr int lds = dma_lds_bytes();
+  auto fn = &gemm_dma_kernel<GATE>;
+  static const int per_cu = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), 256, lds) != hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  p.ptiles = cdiv(p.m, DMA_P);
+  const int64_t tiles = p.ptiles * cdiv(p.n, DMA_R / (GATE ? 2 : 1));
+  int64_t gx = 256LL * per_cu;
+  const int64_t need = cdiv(tiles, 8) * 8;
+  if (gx > need) gx = need;
+  hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), lds, s, p);
+}
+
+}  // namespace
+
+void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s) {
+  if (gate) launch_dma<true>(p, s);
+  else launch_dma<false>(p, s);
+}
+
+bool launch_gemm_lds(GemmP& p, bool gate, int opm, int ta, bool x2, hipStream_t s) {
+  if (opm == OPM_BF16) {
+    if (ta != DT_BF16 || x2) return false;
+    if (gate) launch_one<OPM_BF16, DT_BF16, true, false>(p, s);
+    else launch_one<OPM_BF16, DT_BF16, false, false>(p, s);
+    return true;
+  }
+  if (opm != OPM_SPLIT) return false;
+#define LDS_SPLIT(TA)                                                  \
+  if (gate) {                                                          \
+    if (x2) launch_one<OPM_SPLIT, TA, true, true>(p, s);               \
+    else launch_one<OPM_SPLIT, TA, true, false>(p, s);                 \
+  } else {                                                             \
+    if (x2) launch_one<OPM_SPLIT, TA, false, true>(p, s);              \
+    else launch_one<OPM_SPLIT, TA, false, false>(p, s);                \
+  }
+  if (ta == DT_BF16) { LDS_SPLIT(DT_BF16) } else { LDS_SPLIT(DT_F32) }
+#undef LDS_SPLIT
+  return true;
+}
+
+}  // namespace clarus

@@ -1,0 +1,18 @@
+// Launcher of gemm_lds_kernel (pipelined LDS-tiled GEMM for long-K row operands).
+#pragma once
+
+#include "gemm_kernel.hpp"
+
+namespace clarus {
+
+// Launches the kernel for p (AM_ROWS, batch 1, p.ptiles unset). Returns false when no
+// instantiation matches (operand mode, A dtype, gate, second prologue operand).
+bool launch_gemm_lds(GemmP& p, bool gate, int opm, int ta, bool x2, hipStream_t s);
+
+// Launches gemm_dma_kernel for p (AM_ROWS, batch 1, bf16 A and W, no prologue, K % 32 == 0).
+void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s);
+
+// output channels per tile (the lane run must divide a pixel-shuffle quadrant)
+constexpr int gemm_lds_run(bool gate) { return gate ? 8 : 16; }
+
+}  // namespace clarus

@@ -11,7 +11,8 @@
 // A thread computes 8 consecutive output channels of one pixel: per tap one 16-byte load of
 // each input half (bf16) or two (fp32), fp32 FMAs with the tap weights read from LDS, then
 // the gate and a 16-byte store. Lanes are channel-group-minor, so a wave reads whole pixel
-// rows; the 3x3 neighbourhood is re-read from L1 / L2.
+// rows; the 3x3 neighbourhood is re-read from L1 / L2. The grid is persistent so the tap
+// table ([9][C] fp32, copied as 16-byte vectors) is staged once per block.
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -19,7 +20,7 @@ namespace clarus {
 
 struct DwP {
   const void* x;
-  const float* w;   // [C_in][9] fp32 taps (row-major ky, kx)
+  const float* w;   // [9][C_in] fp32 taps, tap = 3 ky + kx
   const float* b;   // [C_in] fp32 or null
   void* out;
   int64_t n, h, w_, cin, cout;  // cout = cin / 2 with a gate
@@ -29,26 +30,27 @@ struct DwP {
 template <int XDT, int GATE>
 __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
   extern __shared__ __attribute__((aligned(16))) float wsh[];  // [9][cin] taps, then [cin] bias
-  const int64_t cin = p.cin;
-  for (int64_t i = threadIdx.x; i < 9 * cin; i += 256) {
-    const int64_t c = i % cin, t = i / cin;
-    wsh[i] = p.w[c * 9 + t];
+  const int cin = (int)p.cin;
+  {
+    const f32x4* src = reinterpret_cast<const f32x4*>(p.w);  // [9][cin], cin % 8 == 0
+    for (int i = threadIdx.x; i < 9 * cin / 4; i += 256) reinterpret_cast<f32x4*>(wsh)[i] = src[i];
+    for (int i = threadIdx.x; i < cin; i += 256) wsh[9 * cin + i] = p.b ? p.b[i] : 0.f;
   }
-  for (int64_t i = threadIdx.x; i < cin; i += 256) wsh[9 * cin + i] = p.b ? p.b[i] : 0.f;
   __syncthreads();
 
   constexpr int XES = (XDT == DT_BF16) ? 2 : 4;
-  const int64_t groups = p.cout / 8;  // output channel groups of 8
-  const int64_t total = p.n * p.h * p.w_ * groups;
-  const int64_t half = GATE ? p.cout : 0;  // channel offset of the second half
-  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
-    const int64_t pix = t / groups;
-    const int64_t g = t - pix * groups;
-    const int64_t c0 = g * 8;
-    const int64_t hw = p.h * p.w_;
-    const int64_t img = pix / hw;
-    const int64_t r = pix - img * hw;
-    const int y = (int)(r / p.w_), x = (int)(r - (r / p.w_) * p.w_);
+  const int cout = (int)p.cout;
+  const int groups = cout / 8;  // output channel groups of 8
+  const int H = (int)p.h, W = (int)p.w_, hw = H * W;
+  const int total = (int)(p.n * hw) * groups;  // the host checks that this fits 31 bits
+  const int half = GATE ? cout : 0;            // channel offset of the second half
+  const unsigned char* X = (const unsigned char*)p.x;
+  for (int t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
+    const int pix = t / groups;
+    const int c0 = (t - pix * groups) * 8;
+    const int img = pix / hw;
+    const int r = pix - img * hw;
+    const int y = r / W, x = r - (r / W) * W;
     float a1[8], a2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -58,14 +60,16 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
 #pragma unroll
     for (int ky = 0; ky < 3; ++ky) {
       const int yy = y + (ky - 1) * p.dil;
-      if (yy < 0 || yy >= p.h) continue;
+      if (yy < 0 || yy >= H) continue;
 #pragma unroll
       for (int kx = 0; kx < 3; ++kx) {
         const int xx = x + (kx - 1) * p.dil;
-        if (xx < 0 || xx >= p.w_) continue;
+        if (xx < 0 || xx >= W) continue;
         const int tap = ky * 3 + kx;
-        const unsigned char* src = (const unsigned char*)p.x + (((img * p.h + yy) * p.w_ + xx) * cin + c0) * XES;
+        const unsigned char* src = X + ((int64_t)((img * H + yy) * W + xx) * cin + c0) * XES;
         const f32x8 v1 = load8<XDT>(src);
+        f32x8 v2;
+        if constexpr (GATE != 0) v2 = load8<XDT>(src + (int64_t)half * XES);
         const float* wt = wsh + tap * cin + c0;
         const f32x4 w1a = *reinterpret_cast<const f32x4*>(wt), w1b = *reinterpret_cast<const f32x4*>(wt + 4);
 #pragma unroll
@@ -74,7 +78,6 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
           a1[4 + i] = fmaf(w1b[i], v1.v[4 + i], a1[4 + i]);
         }
         if constexpr (GATE != 0) {
-          const f32x8 v2 = load8<XDT>(src + half * XES);
           const f32x4 w2a = *reinterpret_cast<const f32x4*>(wt + half);
           const f32x4 w2b = *reinterpret_cast<const f32x4*>(wt + half + 4);
 #pragma unroll
@@ -92,7 +95,7 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
       else if constexpr (GATE == 2) o[i] = gelu_erf(a1[i]) * a2[i];
       else o[i] = p.act == ACT_GELU ? gelu_erf(a1[i]) : a1[i];
     }
-    const int64_t oo = pix * p.cout + c0;
+    const int64_t oo = (int64_t)pix * cout + c0;
     if (p.o_dt == DT_BF16) {
       u32x4 q;
 #pragma unroll
@@ -123,13 +126,18 @@ extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float*
                  "dwconv3x3: bad gate / act / dilation");
   const int64_t cout = gate ? c / 2 : c;
   CLARUS_REQUIRE((gate == 0 || c % 2 == 0) && cout % 8 == 0, "dwconv3x3: output channels must be a multiple of 8");
+  CLARUS_REQUIRE(n * h * wd * (cout / 8) < ((int64_t)1 << 31) && n * h * wd * c < ((int64_t)1 << 40),
+                 "dwconv3x3: problem too large for 32-bit pixel indexing");
   CLARUS_REQUIRE(aligned(x, 16) && aligned(out, 16) && aligned(w, 16), "dwconv3x3: 16-byte alignment");
   const size_t lds = (size_t)10 * c * sizeof(float);
   CLARUS_REQUIRE(lds <= 160 * 1024, "dwconv3x3: %lld channels exceed the LDS tap table", (long long)c);
   DwP p{x, w, bias, out, n, h, wd, c, cout, dil, gate, act, x_dtype, o_dtype};
   const int64_t total = n * h * wd * (cout / 8);
+  // persistent grid: as many blocks as fit the LDS tap table (at most 8 per CU on 256 CUs)
+  int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)(lds + 1024);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 8 ? 8 : per_cu);
   int64_t blocks = cdiv(total, 256);
-  if (blocks > 8192) blocks = 8192;
+  if (blocks > 256 * per_cu) blocks = 256 * per_cu;
   hipStream_t s = (hipStream_t)stream;
 #define DW_LAUNCH(XDT, G)                                                                                  \
   do {                                                                                                     \

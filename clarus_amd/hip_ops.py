@@ -129,9 +129,13 @@ class HipOps(Backend):
               small=None, geom=(0, 0, 0, 0, 0, 0), m2=None, ldm2=0, lnw=None, lnb=None, m2_act=0,
               ln_eps=1e-6, out_scale=1.0, tile=0):
         h, w, oh, ow, pt, pl = geom
+        stats = None
+        if pro in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1:
+            stats = torch.empty(2 * m, device=a.device, dtype=torch.float32)  # row statistics scratch
         args = _lib.GemmArgs(
             a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
             res=_lib.ptr(res), small=_lib.ptr(small), m2=_lib.ptr(m2), lnw=_lib.ptr(lnw), lnb=_lib.ptr(lnb),
+            stats=_lib.ptr(stats),
             m=m, n=n, k=k, batch=batch, lda=lda, ldc=ldc, ldr=ldr, ldm2=ldm2,
             a_bstride=a_bs, w_bstride=w_bs, c_bstride=c_bs, r_bstride=r_bs,
             a_dtype=_lib.dtype_code(a.dtype), w_dtype=_lib.dtype_code(wt.dtype), c_dtype=_lib.dtype_code(c.dtype),
@@ -214,8 +218,8 @@ class HipOps(Backend):
         if tuple(w.shape[1:]) != (3, 3, 3) or b is None or inp.dim() != 4 or inp.shape[1] != 3:
             raise Unsupported("intro: 3-channel input, 3x3, bias")
         odt = out_dtype or self.dtype
-        if odt not in _KDT:
-            raise Unsupported("intro: bf16 / fp32 output")
+        if odt not in _KDT or w.shape[0] % 8 or w.shape[0] > 512:
+            raise Unsupported("intro: bf16 / fp32 output, cout a multiple of 8 and at most 512")
         n, _, h, wd = inp.shape
         cout = w.shape[0]
         x = inp if (inp.dtype == torch.float32 and inp.is_contiguous()) else inp.float().contiguous()
@@ -279,9 +283,10 @@ class HipOps(Backend):
         if ((kh, kw) != (3, 3) or tuple(w.shape[:2]) != (c, 1) or gcode < 0 or act not in (None, "gelu")
                 or (act == "gelu" and gcode) or dil < 1 or not _dense(x, b)):
             raise Unsupported("dwconv: contiguous 3x3 depthwise, gate none / mul / gelu, act none / gelu")
-        if not (_kdt(x) and (gcode == 0 or c % 2 == 0) and cout % 8 == 0 and _vec16(x) and 10 * c * 4 <= 160 * 1024):
+        if not (_kdt(x) and (gcode == 0 or c % 2 == 0) and cout % 8 == 0 and c % 8 == 0 and _vec16(x)
+                and 10 * c * 4 <= 160 * 1024):
             raise Unsupported("dwconv: bf16 / fp32, output channels % 8 == 0")
-        taps = self.cached(w, "dw9", lambda t: t.float().reshape(t.shape[0], 9).contiguous())
+        taps = self.cached(w, "dw9", lambda t: t.float().reshape(t.shape[0], 9).t().contiguous())
         out = torch.empty((n, h, wd, cout), device=x.device, dtype=self.dtype)
         _lib.check(self.lib.clarus_hip_dwconv3x3(
             x.data_ptr(), _lib.dtype_code(x.dtype), taps.data_ptr(), _lib.ptr(self._bias(b)), out.data_ptr(),

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define CLARUS_HIP_ABI_VERSION 1
+#define CLARUS_HIP_ABI_VERSION 2
 
 /* return codes */
 #define CLARUS_OK 0
@@ -85,6 +85,9 @@ typedef struct ClarusGemmArgs {
   const void* m2;     /* PRO_LNMUL multiplier rows, pixel stride ldm2 */
   const float* lnw;   /* PRO_LNMUL LayerNorm affine [k]              */
   const float* lnb;
+  float* stats;       /* optional scratch, 2 * m floats (batch 1): with PRO_LN / PRO_RMS /
+                         PRO_LNMUL and K > 128 the row statistics are computed into it by a
+                         separate pass (one read of A) instead of inside every column tile */
   int64_t m;          /* rows (output pixels) per batch entry         */
   int64_t n;          /* output channels                              */
   int64_t k;          /* reduction length                             */
@@ -96,7 +99,9 @@ typedef struct ClarusGemmArgs {
   int32_t oh, ow, pt, pl; /* PRO_MUL map geometry (torch_ref.py:18-41)                  */
   int32_t pro, a_mode, c_mode, gate, act, m2_act;
   float ln_eps, out_scale, slope;
-  int32_t tile;       /* 0 = library's choice; else a tile id for sweeps */
+  int32_t tile;       /* 0 = library's choice; else a kernel / tile id for sweeps: 1-7 tiled
+                         shapes, 8 / 9 W-resident streaming (4 / 8 channel blocks), 10 pipelined
+                         LDS tile, 11 DMA-pipelined tile (bf16 A, no prologue, K % 32 == 0) */
 } ClarusGemmArgs;
 
 /* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */
@@ -129,7 +134,8 @@ int clarus_hip_conv3x3(const ClarusConvArgs* args, void* stream);
 
 /*
  * 3 -> cout 3x3 conv (padding 1) from an NCHW fp32 image [batch, 3, h, w] to NHWC
- * [batch, h, w, cout]; wt [27][cout] fp32 ordered (ky, kx, c); bias [cout] fp32.
+ * [batch, h, w, cout]; wt [27][cout] fp32 ordered (ky, kx, c); bias [cout] fp32. cout is a
+ * multiple of 8, at most 512; out, wt and bias 16-byte aligned.
  * replaces kernels/conv3x3.py:196-204 intro3x3
  */
 int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, void* out,
@@ -180,7 +186,7 @@ int clarus_hip_patch_corr(const void* x, int32_t x_dtype, int64_t sn, int64_t sh
  * Depthwise 3x3 convolution, 'same' zero padding, dilation dil, fused gate (NHWC):
  *   y = conv_dw(x) + bias;  gate 0: out = act(y) (act CLARUS_ACT_NONE / CLARUS_ACT_GELU),
  *   gate 1: out = y[:, :c/2] * y[:, c/2:],  gate 2: out = gelu(y[:, :c/2]) * y[:, c/2:].
- * x [n, h, w, c] contiguous (x_dtype); w [c][9] fp32 taps (ky, kx); bias [c] fp32 or NULL;
+ * x [n, h, w, c] contiguous (x_dtype); w [9][c] fp32 taps (tap = 3 ky + kx); bias [c] fp32 or NULL;
  * out [n, h, w, c or c/2] contiguous (o_dtype). Output channels must be a multiple of 8.
  * Not a GEMM: the reference runs it on its torch backend (ops/torch_ref.py:143-155) or its
  * Triton dwconv (kernels/spatial.py:95-214); replaces the latter.

@@ -90,6 +90,83 @@ def test_linear_layernorm(k, mode, hip_bf16):
         assert_fp32(got.cpu(), ref, rel=1e-4, what=f"linear ln={mode} k{k} eps{eps}")
 
 
+@pytest.mark.parametrize("k", [256, 512, 1024])
+@pytest.mark.parametrize("mode", [True, "rms"])
+def test_linear_layernorm_fp32_rows(k, mode, hip_bf16):
+    """fp32 residual rows (NAFNet levels 3-4) with K > 128: the statistics come from the separate
+    row-statistics pass. Rows with a common offset (mean 50, std 2) and one outlier channel."""
+    g = gen(31)
+    x = 50 + 2 * rnd(g, 1, 13, 17, k)
+    x[..., 5] += 40.0
+    wt, b = rnd(g, k, 96, scale=k ** -0.5, dtype=torch.bfloat16), rnd(g, 96)
+    for gate in (False, True):
+        got = hip_bf16.linear(*dev(x, wt, b), ln=mode, gate=gate, out_dtype=torch.float32)
+        ref = REF.linear(x, wt, b, ln=mode, gate=gate)
+        assert_fp32(got.cpu(), ref, rel=1e-5, what=f"linear fp32 rows ln={mode} k{k} gate={gate}")
+
+
+@pytest.mark.parametrize("k,nout,gate", [(288, 40, False), (512, 200, True), (1024, 72, False), (576, 64, True)])
+def test_linear_long_k(k, nout, gate, hip_bf16):
+    """bf16 rows with K > 256 (the pipelined tile kernels): odd pixel count, output channels not a
+    multiple of the tile, bias + GELU / gate + scale + residual."""
+    g = gen(33)
+    x = rnd(g, 1, 13, 17, k, dtype=torch.bfloat16)
+    wt = rnd(g, k, 2 * nout if gate else nout, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc = rnd(g, 2 * nout if gate else nout), rnd(g, nout)
+    res = rnd(g, 1, 13, 17, nout, dtype=torch.bfloat16)
+    act = None if gate else "gelu"
+    got = hip_bf16.linear(*dev(x, wt, b), gate=gate, act=act, scale=sc.cuda(), residual=res.cuda())
+    check(got.cpu(), REF.linear(x, wt, b, gate=gate, act=act, scale=sc, residual=res), f"linear K{k} N{nout} gate={gate}")
+
+
+@pytest.mark.parametrize("tile", [0, 10, 11])
+def test_long_k_kernels_agree(tile, hip_bf16):
+    """Through the C ABI, the pipelined LDS tile kernel (10), the DMA-pipelined kernel (11) and
+    the library's choice (0) on one long-K problem with a gate, against the oracle."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(34)
+    m, k, n = 1000, 512, 96
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    wt = rnd(g, 2 * n, k, scale=k ** -0.5, dtype=torch.bfloat16)  # W^T of the gated product [2n][k]
+    b = rnd(g, 2 * n)
+    ref = REF.linear(x, wt.t().contiguous(), b, gate=True)
+    xd, wd, bd = x.cuda(), wt.cuda(), b.cuda()
+    out = torch.empty(m, n, device="cuda")
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=wd.data_ptr(), c=out.data_ptr(), bias=bd.data_ptr(),
+                         m=m, n=n, k=k, batch=1, lda=k, ldc=n, a_dtype=_lib.BF16, w_dtype=_lib.BF16,
+                         c_dtype=_lib.F32, gate=1, out_scale=1.0, tile=tile)
+    _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "gemm")
+    assert_fp32(out.cpu(), ref, rel=1e-5, what=f"long-K gated GEMM tile {tile}")
+
+
+def test_stats_scratch_is_optional(hip_bf16):
+    """Through the C ABI: the same LN GEMM with and without the statistics scratch (in-kernel
+    pre-pass) both match the oracle."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(32)
+    m, k, n = 700, 512, 64
+    x = 3 + rnd(g, m, k)
+    wt = rnd(g, n, k, scale=k ** -0.5, dtype=torch.bfloat16)  # W^T [n][k]
+    ref = REF.linear(x, wt.t().contiguous(), None, ln=True)
+    xd, wd = x.cuda(), wt.cuda()
+    for use_stats in (True, False):
+        out = torch.empty(m, n, device="cuda")
+        stats = torch.empty(2 * m, device="cuda") if use_stats else None
+        args = _lib.GemmArgs(a=xd.data_ptr(), wt=wd.data_ptr(), c=out.data_ptr(), stats=_lib.ptr(stats),
+                             m=m, n=n, k=k, batch=1, lda=k, ldc=n, a_dtype=_lib.F32, w_dtype=_lib.BF16,
+                             c_dtype=_lib.F32, pro=_lib.PRO_LN, ln_eps=1e-6, out_scale=1.0)
+        rc = lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        _lib.check(rc, "gemm")
+        assert_fp32(out.cpu(), ref, rel=1e-5, what=f"LN GEMM stats scratch={use_stats}")
+
+
 @pytest.mark.parametrize("k", [64, 256])
 def test_linear_mul_prologue(k, hip_bf16):
     """TLC local-mean multiply fused into the prologue (tools/test_kernels.py:72-77) and the
@@ -212,6 +289,18 @@ def test_ln_mul_linear(hip_bf16):
                                  out_dtype=torch.float32)
     assert_fp32(got.cpu(), REF.ln_mul_linear(x * 1e4, lw, lb, xb, wb, m_act="gelu"), rel=1e-4,
                 what="ln_mul_linear gelu fp32 x")
+
+
+def test_ln_mul_linear_long_rows(hip_bf16):
+    """K = 384 > 128 with fp32 x: LN statistics from the row-statistics pass."""
+    g = gen(11)
+    x, hid = 7 + rnd(g, 1, 24, 40, 384), rnd(g, 1, 24, 40, 384)
+    lw, lb, wl, b = rnd(g, 384), rnd(g, 384), rnd(g, 384, 64, scale=0.05), rnd(g, 64)
+    hb, wb = hid.bfloat16(), wl.bfloat16()
+    got = hip_bf16.ln_mul_linear(x.cuda(), lw.cuda(), lb.cuda(), hb.cuda(), wb.cuda(), b.cuda(), m_act="gelu",
+                                 out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.ln_mul_linear(x, lw, lb, hb, wb, b, m_act="gelu"), rel=1e-5,
+                what="ln_mul_linear K384 fp32 x")
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
