@@ -69,6 +69,9 @@ SIGNATURES = {
                                      _i64, _i64, _vp]),
     "clarus_hip_dwconv3x3": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
                                     _vp]),
+    "clarus_hip_boxmean_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "clarus_hip_boxmean": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t,
+                                  _vp]),
     "clarus_hip_abi_version": (_i32, []),
     "clarus_hip_sizeof_gemm_args": (ctypes.c_size_t, []),
     "clarus_hip_sizeof_conv_args": (ctypes.c_size_t, []),

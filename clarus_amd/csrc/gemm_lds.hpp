@@ -30,10 +30,7 @@ constexpr int LT_R = 128;  // W^T rows per tile
 __host__ __device__ constexpr int lt_rowb(int kc) { return (kc + 8) * 2; }  // bf16 row + 16 B pad
 __host__ __device__ constexpr int lt_wbuf(int kc) { return LT_R * lt_rowb(kc); }
 __host__ __device__ constexpr int lt_abuf(int kc, int opm) { return (opm == OPM_SPLIT ? 2 : 1) * LT_P * lt_rowb(kc); }
-__host__ __device__ constexpr int lt_epi_floats() { return 3 * LT_R / 2 * 2; }  // per tile: up to 2 x 64 bias + 128 scale
-__host__ __device__ constexpr int lt_lds_bytes(int kc, int opm) {
-  return 2 * lt_epi_floats() * 4 + 2 * (lt_wbuf(kc) + lt_abuf(kc, opm));
-}
+__host__ __device__ constexpr int lt_lds_bytes(int kc, int opm) { return 2 * (lt_wbuf(kc) + lt_abuf(kc, opm)); }
 
 // residual add + store of one lane's run of RUN output channels (v in fp32, channel run0 ..)
 template <int RUN>
@@ -97,7 +94,7 @@ __device__ __forceinline__ void store_run(const GemmP& p, float (&v)[RUN], int64
 }
 
 template <int OPM, int TA, bool GATE, bool X2, int KC>
-__global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_lds_kernel(const GemmP p) {
   static_assert(OPM == OPM_BF16 || OPM == OPM_SPLIT, "bf16 weights only");
   static_assert(KC % 32 == 0 && (LT_P * KC / 8) % 256 == 0, "chunk shape");
   constexpr int G = GATE ? 2 : 1;
@@ -110,49 +107,76 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
   constexpr int STAGE = WBUF + ABUF;
   constexpr int NKS = KC / 32;
   constexpr int FQ = KC / 8;                 // 8-k fragments per pixel row of a chunk
-  constexpr int FPT = LT_P * FQ / 256;       // A fragments staged per thread per chunk
-  constexpr int EPI = lt_epi_floats();
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  float* epi_base = reinterpret_cast<float*>(lds);  // [2][EPI]: per tile parity, bias [G * TNO] then scale [TNO]
-  unsigned char* stages = lds + 2 * EPI * 4;
+  constexpr int FPT = LT_P * FQ / 256;       // A fragments (and W^T units) staged per thread per chunk
+  extern __shared__ __attribute__((aligned(16))) unsigned char stages[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 15, lg = lane >> 4;
   const int wp = wave & 1, wn = wave >> 1;
   const int64_t K = p.k;
   const int nch = (int)cdiv(K, KC);
-  const int64_t ntn = cdiv(p.n, TNO);
-  const int64_t T = p.ptiles * ntn;
+  const int ntn = (int)cdiv(p.n, TNO);
+  const int T = (int)p.ptiles * ntn;  // the host checks that this fits 31 bits
   const unsigned char* A = (const unsigned char*)p.a;
   const unsigned char* Wt = (const unsigned char*)p.wt;
 
   // XCD-aware deal: workgroup b runs on XCD b % 8 and takes tiles xcd * span + b / 8 + j * per
   const int xcd = blockIdx.x & 7;
-  const int64_t per = gridDim.x >> 3;
-  const int64_t span = cdiv(T, 8);
-  const int64_t t0 = xcd * span + (blockIdx.x >> 3);
-  const int64_t t_end = (xcd + 1) * span < T ? (xcd + 1) * span : T;
-  const int64_t ntiles = t0 < t_end ? cdiv(t_end - t0, per) : 0;
-  const int64_t nsteps = ntiles * nch;
+  const int per = gridDim.x >> 3;
+  const int span = (T + 7) >> 3;
+  const int t0 = xcd * span + (blockIdx.x >> 3);
+  const int t_end = (xcd + 1) * span < T ? (xcd + 1) * span : T;
+  const int ntiles = t0 < t_end ? (t_end - t0 + per - 1) / per : 0;
+  const int nsteps = ntiles * nch;
 
-  // ---- staging of step s: A fragments and W^T units in registers
+  // ---- staging: this thread's A fragments f = tid + 256 i (pixel f / FQ, k = k0 + 8 (f % FQ))
+  // and W^T units u = tid + 256 i (tile row u / FQ, same k), loaded into registers one step
+  // ahead, transformed and written to LDS after the current step's products.
   RawFrag<TA> ra[FPT];
-  u32x4 rw[FPT];  // W^T units (LT_R rows x KC has as many 16-byte units as the A tile has fragments)
+  u32x4 rw[FPT];
   RawFrag<DT_F32> rx[X2 ? FPT : 1];
+  const unsigned char* a_src[FPT];  // per tile: row + unit offset at k = 0
+  const unsigned char* w_src[FPT];
+  const unsigned char* x_src[X2 ? FPT : 1];
   f32x2 rst[FPT];
-  auto tile_of = [&](int64_t s) { return t0 + (s / nch) * per; };
+  bool pv[FPT];
+  int is_tile = 0, is_chunk = 0;
+  int64_t is_k0 = 0;
 
-  auto issue = [&](int64_t s) __attribute__((always_inline)) {
-    const int64_t t = tile_of(s);
-    const int64_t k0 = (int64_t)(s % nch) * KC;
-    const int64_t pt = t / ntn, nt = t - pt * ntn;
-    // W^T: unit u = tid + 256 i is 8 k of tile row u / FQ; tile row r holds the channel that
-    // makes a lane's accumulators a contiguous run. Sources past the last channel / K are
-    // clamped into the tensor (finite values that meet zero A or feed unstored channels).
+  auto set_issue_tile = [&]() __attribute__((always_inline)) {
+    const int t = t0 + is_tile * per;
+    const int pt = t / ntn, nt = t - pt * ntn;
 #pragma unroll
     for (int i = 0; i < FPT; ++i) {
-      const int u = tid + 256 * i;
-      const int r = u / FQ;
+      const int f = tid + 256 * i;
+      const int64_t q = (int64_t)pt * LT_P + f / FQ;
+      pv[i] = q < p.m;
+      const int64_t qc = pv[i] ? q : p.m - 1;
+      a_src[i] = A + (qc * p.lda + (f % FQ) * 8) * esz<TA>();
+      rst[i] = f32x2{0.f, 1.f};
+      if constexpr (OPM == OPM_SPLIT)
+        if (p.stats) rst[i] = *reinterpret_cast<const f32x2*>(p.stats + 2 * qc);
+      if constexpr (X2) {
+        int64_t xo;
+        if (p.pro == PRO_MUL) {
+          const int hwi = p.h * p.w;
+          const int64_t im = qc / hwi;
+          const int rr = (int)(qc - im * hwi);
+          const int yq = rr / p.w;
+          int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
+          sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
+          sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
+          xo = ((im * p.oh + sy) * p.ow + sx) * K;
+        } else {
+          xo = qc * p.ldm2;
+        }
+        const int dt = (p.pro == PRO_MUL) ? p.s_dt : p.m2_dt;
+        const unsigned char* b = (const unsigned char*)((p.pro == PRO_MUL) ? p.small : p.m2);
+        x_src[i] = b + (xo + (f % FQ) * 8) * (dt == DT_BF16 ? 2 : 4);
+      }
+      // W^T: tile row r holds the channel that makes a lane's accumulators a contiguous run;
+      // rows past the last channel are clamped into the tensor (their outputs are not stored)
+      const int r = f / FQ;
       int half, ch;
       if constexpr (GATE) {
         half = r >> 6;
@@ -163,44 +187,28 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
         const int w2 = r >> 6, r2 = r & 63;
         ch = w2 * 64 + ((r2 & 15) >> 2) * 16 + (r2 >> 4) * 4 + (r2 & 3);
       }
-      int64_t c = nt * TNO + ch;
+      int64_t c = (int64_t)nt * TNO + ch;
       if (c > p.n - 1) c = p.n - 1;
-      int64_t kk = k0 + (u % FQ) * 8;
-      if (kk > K - 8) kk = K - 8;
-      rw[i] = *reinterpret_cast<const u32x4*>(Wt + ((half * p.n + c) * K + kk) * 2);
+      w_src[i] = Wt + ((half * p.n + c) * K + (f % FQ) * 8) * 2;
     }
-    // A: fragment f = tid + 256 i covers pixel f / FQ of the tile, k = k0 + 8 (f % FQ)
+  };
+
+  auto issue = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < FPT; ++i) {
       const int f = tid + 256 * i;
-      const int64_t q = pt * LT_P + f / FQ;
-      const int64_t k = k0 + (f % FQ) * 8;
-      const bool ok = q < p.m && k < K;
-      ra[i] = ok ? raw_load<TA>(A + (q * p.lda + k) * esz<TA>()) : raw_zero<TA>();
-      if constexpr (OPM == OPM_SPLIT) {
-        rst[i] = f32x2{0.f, 1.f};
-        if (p.stats && q < p.m) rst[i] = *reinterpret_cast<const f32x2*>(p.stats + 2 * q);
-      }
+      const int64_t k = is_k0 + (f % FQ) * 8;
+      const bool kok = k < K;
+      // W^T past K: clamped to the last 8 k (they meet zero A)
+      const int64_t wk = kok ? is_k0 : (K - 8 - (f % FQ) * 8);
+      rw[i] = *reinterpret_cast<const u32x4*>(w_src[i] + wk * 2);
+      ra[i] = (pv[i] && kok) ? raw_load<TA>(a_src[i] + is_k0 * esz<TA>()) : raw_zero<TA>();
       if constexpr (X2) {
         RawFrag<DT_F32> v;
         v.a = v.b = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (ok) {
-          int64_t xo;
-          if (p.pro == PRO_MUL) {
-            const int hwi = p.h * p.w;
-            const int64_t im = q / hwi;
-            const int rr = (int)(q - im * hwi);
-            const int yq = rr / p.w;
-            int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
-            sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
-            sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
-            xo = ((im * p.oh + sy) * p.ow + sx) * K;
-          } else {
-            xo = q * p.ldm2;
-          }
+        if (pv[i] && kok) {
           const int dt = (p.pro == PRO_MUL) ? p.s_dt : p.m2_dt;
-          const unsigned char* b = (const unsigned char*)((p.pro == PRO_MUL) ? p.small : p.m2);
-          const f32x8 t8 = dt == DT_BF16 ? load8<DT_BF16>(b + (xo + k) * 2) : load8<DT_F32>(b + (xo + k) * 4);
+          const f32x8 t8 = dt == DT_BF16 ? load8<DT_BF16>(x_src[i] + is_k0 * 2) : load8<DT_F32>(x_src[i] + is_k0 * 4);
           v.a = f32x4{t8.v[0], t8.v[1], t8.v[2], t8.v[3]};
           v.b = f32x4{t8.v[4], t8.v[5], t8.v[6], t8.v[7]};
         }
@@ -208,22 +216,26 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
       }
     }
   };
-
-  // prologue + split of the staged fragments into LDS stage s; the tile's epilogue vectors
-  // (bias, scale) with its first chunk
-  auto commit = [&](int64_t s) __attribute__((always_inline)) {
-    unsigned char* wbuf = stages + (s & 1) * STAGE;
-    unsigned char* abuf = wbuf + WBUF;
-    const int64_t k0 = (int64_t)(s % nch) * KC;
-#pragma unroll
-    for (int i = 0; i < FPT; ++i) {
-      const int u = tid + 256 * i;
-      *reinterpret_cast<u32x4*>(wbuf + (u / FQ) * ROWB + (u % FQ) * 16) = rw[i];
+  auto advance_issue = [&]() __attribute__((always_inline)) {
+    if (++is_chunk == nch) {
+      is_chunk = 0;
+      is_k0 = 0;
+      ++is_tile;
+      if (is_tile < ntiles) set_issue_tile();
+    } else {
+      is_k0 += KC;
     }
+  };
+
+  // prologue + split of the staged registers into LDS stage sb (k0 of the staged chunk)
+  auto commit = [&](int sb, int64_t k0) __attribute__((always_inline)) {
+    unsigned char* wbuf = stages + sb * STAGE;
+    unsigned char* abuf = wbuf + WBUF;
 #pragma unroll
     for (int i = 0; i < FPT; ++i) {
       const int f = tid + 256 * i;
       const int off = (f / FQ) * ROWB + (f % FQ) * 16;
+      *reinterpret_cast<u32x4*>(wbuf + off) = rw[i];
       if constexpr (OPM == OPM_BF16) {
         *reinterpret_cast<u32x4*>(abuf + off) = ra[i].q;
       } else {
@@ -253,25 +265,11 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
             }
           }
         }
-        const int64_t q = (tile_of(s) / ntn) * LT_P + f / FQ;
-        if (!(q < p.m && k < K)) a = zero8();
+        if (!(pv[i] && k < K)) a = zero8();
         bf16x8 hi, lo;
         split_bf16(a, hi, lo);
         *reinterpret_cast<bf16x8*>(abuf + off) = hi;
         *reinterpret_cast<bf16x8*>(abuf + LT_P * ROWB + off) = lo;
-      }
-    }
-    if (s % nch == 0) {
-      const int64_t t = tile_of(s);
-      const int64_t n0 = (t - (t / ntn) * ntn) * TNO;
-      float* epi = epi_base + ((s / nch) & 1) * EPI;
-      for (int i = tid; i < (G + 1) * TNO; i += 256) {
-        const int part = i / TNO;
-        const int64_t c = n0 + (i - part * TNO);
-        float v;
-        if (part < G) v = (p.bias && c < p.n) ? p.bias[part * p.n + c] : 0.f;
-        else v = ((p.scale && c < p.n) ? p.scale[c] : 1.f) * p.out_scale;
-        epi[i] = v;
       }
     }
   };
@@ -281,22 +279,22 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   // W^T row of the wave's MFMA row block rb (gate: blocks 0, 1 first half, 2, 3 second half)
   auto wrow = [&](int rb) { return GATE ? ((rb >> 1) * 64 + wn * 32 + (rb & 1) * 16) : (wn * 64 + rb * 16); };
 
-  if (nsteps > 0) {
-    issue(0);
-    commit(0);
-    __syncthreads();
-  }
-  for (int64_t s = 0; s < nsteps; ++s) {
-    const bool more = s + 1 < nsteps;
-    if (more) issue(s + 1);
+  if (nsteps == 0) return;
+  set_issue_tile();
+  issue();
+  commit(0, 0);
+  advance_issue();
+  __syncthreads();
+  int s = 0;
 
-    // ---- products of chunk s
-    {
-      asm volatile("" ::: "memory");
+  for (int tl = 0; tl < ntiles; ++tl) {
+    for (int kc = 0; kc < nch; ++kc, ++s) {
+      const bool more = s + 1 < nsteps;
+      const int64_t next_k0 = is_k0;
+      if (more) issue();
       const unsigned char* wb = stages + (s & 1) * STAGE;
       const unsigned char* ab = wb + WBUF;
 #pragma unroll
@@ -318,35 +316,43 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
           }
         }
       }
+      if (kc + 1 < nch && more) {  // the tile continues: stage the next chunk now
+        commit((s + 1) & 1, next_k0);
+        advance_issue();
+        __syncthreads();
+      }
     }
 
-    // ---- epilogue after the tile's last chunk
-    if (s % nch == nch - 1) {
-      const int64_t t = tile_of(s);
-      const int64_t pt = t / ntn, nt = t - pt * ntn;
-      const float* epi = epi_base + ((s / nch) & 1) * EPI;
-      const int e0 = wn * WCH + lg * RUN;  // this lane's run within the tile's channels
-      const int64_t run0 = nt * TNO + e0;
+    // ---- epilogue of the tile (the next tile's first chunk is in registers)
+    {
+      const int t = t0 + tl * per;
+      const int pt = t / ntn, nt = t - pt * ntn;
+      const int e0 = wn * WCH + lg * RUN;
+      const int64_t run0 = (int64_t)nt * TNO + e0;
       const bool full_n = run0 + RUN <= p.n;
+      float b1[RUN], b2[GATE ? RUN : 1], sc[RUN];
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) {
+        const bool ok = run0 + i < p.n;
+        b1[i] = (p.bias && ok) ? p.bias[run0 + i] : 0.f;
+        if constexpr (GATE) b2[i] = (p.bias && ok) ? p.bias[p.n + run0 + i] : 0.f;
+        sc[i] = ((p.scale && ok) ? p.scale[run0 + i] : 1.f) * p.out_scale;
+      }
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
-        const int64_t q = pt * LT_P + wp * 64 + pb * 16 + lc;
+        const int64_t q = (int64_t)pt * LT_P + wp * 64 + pb * 16 + lc;
         float v[RUN];
         if constexpr (GATE) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const f32x4 b1 = *reinterpret_cast<const f32x4*>(epi + e0 + j * 4);
-            const f32x4 b2 = *reinterpret_cast<const f32x4*>(epi + TNO + e0 + j * 4);
+          for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[j * 4 + i] = (acc[pb][j][i] + b1[i]) * (acc[pb][2 + j][i] + b2[i]);
-          }
+            for (int i = 0; i < 4; ++i)
+              v[j * 4 + i] = (acc[pb][j][i] + b1[j * 4 + i]) * (acc[pb][2 + j][i] + b2[j * 4 + i]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x4 b1 = *reinterpret_cast<const f32x4*>(epi + e0 + j * 4);
+          for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[j * 4 + i] = acc[pb][j][i] + b1[i];
-          }
+            for (int i = 0; i < 4; ++i) v[j * 4 + i] = acc[pb][j][i] + b1[j * 4 + i];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[pb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -359,11 +365,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
           for (int i = 0; i < RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
         }
 #pragma unroll
-        for (int j = 0; j < RUN / 4; ++j) {
-          const f32x4 sc = *reinterpret_cast<const f32x4*>(epi + G * TNO + e0 + j * 4);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[j * 4 + i] *= sc[i];
-        }
+        for (int i = 0; i < RUN; ++i) v[i] *= sc[i];
         int64_t oo, ro;
         if (p.c_mode == CM_SHUFFLE) {
           const int64_t hwi = (int64_t)p.h * p.w;
@@ -381,9 +383,11 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(const GemmP p) {
         store_run<RUN>(p, v, oo, ro, run0, full_n);
       }
     }
-
-    if (more) commit(s + 1);
-    __syncthreads();
+    if (s < nsteps) {  // stage the next tile's first chunk (loaded during the last products)
+      commit(s & 1, 0);
+      advance_issue();
+      __syncthreads();
+    }
   }
 }
 

@@ -27,6 +27,17 @@ class Small:
         return Small(data, self.pt, self.pl, self.H, self.W)
 
 
+try:  # inside a clarus installation, return clarus's own Small (its torch backend checks the type)
+    from clarus.ops.torch_ref import Small as _HostSmall  # type: ignore
+except ImportError:
+    _HostSmall = None
+
+
+def make_small(data, pt: int, pl: int, H: int, W: int):
+    """A local-mean map of the host's Small type when clarus is installed, else the local one."""
+    return (_HostSmall or Small)(data, pt, pl, H, W)
+
+
 def is_small(x) -> bool:
     return all(hasattr(x, a) for a in ("data", "pt", "pl", "H", "W", "with_data")) and not torch.is_tensor(x)
 

@@ -24,7 +24,7 @@ import torch
 from . import _lib
 from .dft import dft_matrices
 from .dispatch import Backend, BackendUnavailable, Unsupported, register_backend
-from .geometry import is_small
+from .geometry import box_geometry, is_small, make_small
 
 _KDT = (torch.bfloat16, torch.float32)
 
@@ -272,6 +272,21 @@ class HipOps(Backend):
             raise Unsupported("conv3x3: bf16 / fp32, cin % 8 == 0, 16-byte pixel rows")
         return self._conv(x, w, b, odt=odt, act=act, residual=residual, out_scale=out_scale, up2=up2, out=out,
                           slope=slope)
+
+    def boxmean(self, x, k):
+        """TLC local mean over the valid (kh, kw) windows, returned as the un-padded map (not
+        GEMM-shaped; the reference's boxmean, ops/torch_ref.py:133-141)."""
+        if x.dim() != 4 or not x.is_contiguous() or x.dtype not in _KDT or x.shape[-1] % 8 or not _vec16(x):
+            raise Unsupported("boxmean: contiguous NHWC bf16 / fp32 with channels % 8 == 0")
+        n, h, wd, c = x.shape
+        k1, k2, oh, ow, pt, pl = box_geometry(h, wd, k)
+        out = torch.empty((n, oh, ow, c), device=x.device, dtype=self.dtype)
+        nbytes = self.lib.clarus_hip_boxmean_workspace(n, h, wd, c, k1, k2)
+        scratch = torch.empty((nbytes + 3) // 4, device=x.device, dtype=torch.float32)
+        _lib.check(self.lib.clarus_hip_boxmean(x.data_ptr(), _lib.dtype_code(x.dtype), out.data_ptr(),
+                                               _lib.dtype_code(self.dtype), n, h, wd, c, k1, k2, scratch.data_ptr(),
+                                               nbytes, self._stream(x)), "boxmean")
+        return make_small(out, pt, pl, h, wd)
 
     def dwconv(self, x, w, b, dil=1, gate=False, act=None):
         """Depthwise 3x3 conv with fused SimpleGate / GELU gate / GELU (not GEMM-shaped; the

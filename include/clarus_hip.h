@@ -195,6 +195,18 @@ int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float* w, const f
                          int32_t o_dtype, int64_t n, int64_t h, int64_t w_, int64_t c, int32_t dil,
                          int32_t gate, int32_t act, void* stream);
 
+/*
+ * TLC local mean (valid windows, NHWC): out[b, i, j, c] = mean of x[b, i .. i + k1 - 1,
+ * j .. j + k2 - 1, c], i < h - k1 + 1, j < w - k2 + 1. x contiguous [n, h, w, c] (x_dtype),
+ * out contiguous [n, h - k1 + 1, w - k2 + 1, c] (o_dtype); c a multiple of 8; scratch holds
+ * clarus_hip_boxmean_workspace(...) bytes (the fp32 column sums). Sums are accumulated in fp64.
+ * Not a GEMM: replaces the reference's boxmean (ops/torch_ref.py:133-141, ops/triton_cuda.py:132-137).
+ */
+size_t clarus_hip_boxmean_workspace(int64_t n, int64_t h, int64_t w, int64_t c, int64_t k1, int64_t k2);
+int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int32_t o_dtype, int64_t n, int64_t h,
+                       int64_t w, int64_t c, int64_t k1, int64_t k2, void* scratch, size_t scratch_bytes,
+                       void* stream);
+
 /* ABI version (CLARUS_HIP_ABI_VERSION) and struct sizes, for binding checks. */
 int clarus_hip_abi_version(void);
 size_t clarus_hip_sizeof_gemm_args(void);

@@ -165,3 +165,43 @@ def test_dwconv_nafnet_720p(hip_bf16):
     x, w, b = rnd(g, 1, 720, 1280, 128, dtype=torch.bfloat16), rnd(g, 128, 1, 3, 3), rnd(g, 128)
     got = hip_bf16.dwconv(x.cuda(), w.cuda(), b.cuda(), gate=True)
     check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, w, b, gate=True), "dwconv 720p gate")
+
+
+# ------------------------------------------------------------------ TLC local mean (NAFNet SCA input)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("h,w,k", [(37, 53, 13), (37, 53, (26, 53)), (20, 30, 64), (33, 33, 33), (9, 150, 5)])
+def test_boxmean(dt, h, w, k, hip_bf16, hip_f32):
+    """Valid-window local mean vs the oracle's prefix-sum form (tools/test_model_contracts.py:
+    149-163 windows), odd sizes, windows clamped to the map, a 1 x W output row."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(10)
+    x = (1.5 + rnd(g, 2, h, w, 24)).to(dt)
+    got = hip.boxmean(x.cuda(), k)
+    ref = TorchRef(torch.float32, "cpu").boxmean(x, k)
+    assert (got.pt, got.pl, got.H, got.W) == (ref.pt, ref.pl, ref.H, ref.W)
+    assert got.data.shape == ref.data.shape
+    check(got.data.cpu(), ref.data.float(), f"boxmean {h}x{w} k={k} {dt}")
+
+
+def test_boxmean_exact_float64():
+    """fp32 input: every window sum against a float64 brute force (the HIP kernel accumulates in
+    fp64, so it is held to 2e-7 relative, tighter than the prefix-sum oracle itself)."""
+    from clarus_amd.hip_ops import HipOps
+    hip = HipOps(torch.float32, torch.device("cuda", 0))
+    g = gen(11)
+    x = 100 + rnd(g, 1, 40, 60, 16)
+    got = hip.boxmean(x.cuda(), (17, 23)).data.cpu().double()
+    xd = x.double()
+    s = torch.nn.functional.pad(xd.cumsum(2).cumsum(1), (0, 0, 1, 0, 1, 0))
+    ref = (s[:, 17:, 23:] + s[:, :-17, :-23] - s[:, :-17, 23:] - s[:, 17:, :-23]) / (17 * 23)
+    assert ((got - ref).abs() / ref.abs()).max().item() < 2e-7
+
+
+def test_boxmean_nafnet_level0(hip_bf16):
+    """NAFNet-w64 level 0: 1 x 720 x 1280 x 64 bf16, window 384 (map 337 x 897)."""
+    g = gen(12)
+    x = rnd(g, 1, 720, 1280, 64, dtype=torch.bfloat16)
+    got = hip_bf16.boxmean(x.cuda(), 384)
+    ref = TorchRef(torch.float32, "cpu").boxmean(x, 384)
+    assert got.data.shape == (1, 337, 897, 64)
+    check(got.data.cpu(), ref.data.float(), "boxmean level 0")
