@@ -313,6 +313,15 @@ extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
     p.vec_res = 0;
   }
   const int opm = operand_mode(a->x_dtype, a->w_dtype, false);
+  // output tiles with an LDS halo and resident weights (tile 0 = auto, 12 = force); the
+  // implicit GEMM otherwise (tiles 1..7)
+  const bool halo_ok = opm == OPM_BF16 && a->c_mode == CLARUS_C_ROWS && a->cin % 32 == 0 &&
+                       a->batch * H * W < ((int64_t)1 << 31);
+  CLARUS_REQUIRE(a->tile != 12 || halo_ok, "conv3x3: the halo-tile kernel does not take this problem");
+  if (halo_ok && (a->tile == 0 || a->tile == 12)) {
+    if (launch_conv_halo(p, (hipStream_t)stream)) return check_launch("conv3x3");
+    CLARUS_REQUIRE(a->tile == 0, "conv3x3: the halo-tile kernel's weights do not fit in LDS");
+  }
   const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(p.m, p.n, p.k, 1, false, opm, 0);
   return launch(p, AM_CONV3, false, opm, a->x_dtype, tile, 1, (hipStream_t)stream, "conv3x3");
 }

@@ -12,6 +12,10 @@ bool launch_gemm_lds(GemmP& p, bool gate, int opm, int ta, bool x2, hipStream_t 
 // Launches gemm_dma_kernel for p (AM_ROWS, batch 1, bf16 A and W, no prologue, K % 32 == 0).
 void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s);
 
+// Launches conv_halo_kernel for p (bf16 x and weights, cin % 32 == 0, row output). Returns
+// false when the resident weights of even a 32-channel tile do not fit in LDS.
+bool launch_conv_halo(GemmP& p, hipStream_t s);
+
 // output channels per tile (the lane run must divide a pixel-shuffle quadrant)
 constexpr int gemm_lds_run(bool gate) { return gate ? 8 : 16; }
 

@@ -78,6 +78,50 @@ def test_conv3x3_up2(dt, hip_bf16, hip_f32):
     check(got.cpu(), REF.conv3x3(x, w, b, up2=True, act="lrelu"), f"conv3x3 up2 {dt}")
 
 
+@pytest.mark.parametrize("cin,cout,up2,h,w,n", [(64, 32, False, 13, 45, 2), (96, 64, False, 8, 32, 1),
+                                                 (64, 64, True, 11, 19, 2), (192, 64, False, 9, 40, 1),
+                                                 (32, 48, True, 5, 7, 1), (128, 40, False, 17, 33, 1)])
+def test_conv3x3_halo_shapes(cin, cout, up2, h, w, n, hip_bf16):
+    """bf16 convs with cin % 32 == 0 (the halo-tile kernel): ragged 8 x 32 tiles, batch 2, x2
+    upsample, output channels that are not a multiple of the 32 / 64-channel tile, LeakyReLU,
+    out_scale and a residual."""
+    g = gen(13)
+    x = rnd(g, n, h, w, cin, dtype=torch.bfloat16)
+    wt = rnd(g, cout, cin, 3, 3, scale=(cin * 9) ** -0.5, dtype=torch.bfloat16)
+    b = rnd(g, cout)
+    H, W = (2 * h, 2 * w) if up2 else (h, w)
+    res = rnd(g, n, H, W, cout, dtype=torch.bfloat16)
+    got = hip_bf16.conv3x3(x.cuda(), wt.cuda(), b.cuda(), act="lrelu", out_scale=0.5, residual=res.cuda(), up2=up2)
+    ref = REF.conv3x3(x, wt, b, act="lrelu", out_scale=0.5, residual=res, up2=up2, out_dtype=torch.float32)
+    check(got.cpu(), ref, f"conv3x3 halo cin{cin} cout{cout} up2={up2} {n}x{h}x{w}")
+
+
+@pytest.mark.parametrize("tile", [12, 4])
+def test_conv3x3_kernels_agree(tile, hip_bf16):
+    """Through the C ABI: the halo-tile kernel (12) and an implicit-GEMM tile (4) on one problem
+    with channel slices, fp32 output, against the oracle."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(14)
+    n, h, w, cin, cout = 1, 21, 37, 96, 32
+    buf = rnd(g, n, h, w, 128, dtype=torch.bfloat16)
+    wt = rnd(g, cout, cin, 3, 3, scale=(cin * 9) ** -0.5, dtype=torch.bfloat16)
+    b = rnd(g, cout)
+    ref = REF.conv3x3(buf[..., :cin], wt, b, act="lrelu", out_dtype=torch.float32)
+    wtk = wt.permute(0, 2, 3, 1).reshape(cout, 9 * cin).contiguous().cuda()  # W^T [cout][(ky, kx, cin)]
+    bd, bias = buf.cuda(), b.cuda()
+    out = torch.empty(n, h, w, cout, device="cuda")
+    args = _lib.ConvArgs(x=bd.data_ptr(), wt=wtk.data_ptr(), out=out.data_ptr(), bias=bias.data_ptr(),
+                         batch=n, h=h, w=w, cin=cin, cout=cout, ldx=128, ldo=cout, ldr=0,
+                         x_dtype=_lib.BF16, w_dtype=_lib.BF16, o_dtype=_lib.F32, act=_lib.ACT_LRELU,
+                         out_scale=1.0, slope=0.2, tile=tile)
+    _lib.check(lib.clarus_hip_conv3x3(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "conv3x3")
+    assert_fp32(out.cpu(), ref, rel=1e-5, what=f"conv3x3 tile {tile}")
+
+
 def test_ending_and_intro(hip_bf16):
     """ending: fp32 input at |x| ~ 300, NCHW fp32 output + global residual; intro 3 -> 64 / 48."""
     g = gen(4)
