@@ -228,9 +228,12 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const int64_t run_div = a->c_mode == CLARUS_C_SHUFFLE ? a->n / 4 : 0;
   // W-resident streaming kernel for row operands with K <= 256 (bf16 A) / 128 (fp32 A) (tile 0 = auto, 8 / 9 = force
   // NB 4 / 8); the tiled kernel otherwise (tiles 1..7 force one of its tile shapes)
-  if (a->a_mode == CLARUS_A_ROWS && opm != OPM_F32 && (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
+  // fp32 weights stream with fp32 A and K <= 128, no second prologue operand (LDS holds fp32 rows)
+  const bool stream_opm = opm != OPM_F32 || (a->a_dtype == DT_F32 && a->pro != PRO_MUL && a->pro != PRO_LNMUL);
+  if (a->a_mode == CLARUS_A_ROWS && stream_opm && (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
     const int ks = stream_ks_for(a->k, a->a_dtype);
     int nb = a->tile == 8 ? 4 : a->tile == 9 ? 8 : ((a->n <= 64 || a->gate) ? 4 : 8);
+    if (opm == OPM_F32 && a->gate) nb = 4;  // fp32 gate rows of NB 8 exceed the LDS budget
     if (run_div && run_div % (4 * nb)) nb = 4;
     const bool x2 = a->pro == PRO_MUL || a->pro == PRO_LNMUL;
     GemmLaunch fn = (ks && (!run_div || run_div % (4 * nb) == 0)) ? pick_gemm_stream(nb, a->gate != 0, opm, a->a_dtype, ks, x2)

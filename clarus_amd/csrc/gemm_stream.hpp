@@ -17,9 +17,11 @@
 
 namespace clarus {
 
-__host__ __device__ constexpr int stream_wrow_elems(int ks) { return ks * 32 + 8; }  // bf16 row + 16 B pad
-__host__ __device__ constexpr int stream_lds_bytes(int nb, bool gate, int ks) {
-  return gemm_epi_bytes(nb) + (gate ? 2 : 1) * nb * 16 * stream_wrow_elems(ks) * 2;
+// W^T row in LDS: KS * 32 elements + a 16-byte pad (bf16, or fp32 with OPM_F32)
+__host__ __device__ constexpr int stream_wes(int opm) { return opm == 2 ? 4 : 2; }
+__host__ __device__ constexpr int stream_wrow_elems(int ks, int opm) { return ks * 32 + 16 / stream_wes(opm); }
+__host__ __device__ constexpr int stream_lds_bytes(int nb, bool gate, int ks, int opm) {
+  return gemm_epi_bytes(nb) + (gate ? 2 : 1) * nb * 16 * stream_wrow_elems(ks, opm) * stream_wes(opm);
 }
 
 // register budget per lane: accumulators + D blocks of A (+ second operand) + epilogue;
@@ -32,12 +34,12 @@ __host__ __device__ constexpr int stream_waves_per_eu(int nb, bool gate, int ks,
 template <int NB, bool GATE, int OPM, int TA, int KS, bool X2>
 __global__ void __launch_bounds__(256)
 gemm_stream_kernel(const GemmP p) {
-  static_assert(OPM == OPM_BF16 || OPM == OPM_SPLIT, "bf16 weights only");
   constexpr int G = GATE ? 2 : 1;
   constexpr int TN = NB * 16;
   constexpr int RUN = 4 * NB;
-  constexpr int ROWE = stream_wrow_elems(KS);
-  constexpr int ROWB = ROWE * 2;
+  constexpr int WES = stream_wes(OPM);
+  constexpr int ROWE = stream_wrow_elems(KS, OPM);
+  constexpr int ROWB = ROWE * WES;
   constexpr int WB = G * TN * ROWB;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   float* epi = reinterpret_cast<float*>(lds);
@@ -50,7 +52,7 @@ gemm_stream_kernel(const GemmP p) {
   const int64_t run0 = n0 + lg * RUN;
   const int64_t K = p.k;
   const unsigned char* A = (const unsigned char*)p.a + bz * p.a_bs * esz<TA>();
-  const unsigned char* Wt = (const unsigned char*)p.wt + bz * p.w_bs * 2;
+  const unsigned char* Wt = (const unsigned char*)p.wt + bz * p.w_bs * WES;
 
   // ---- epilogue vectors and W^T rows (all of K) -> LDS, once
   for (int i = tid; i < (G + 1) * TN; i += 256) {
@@ -66,14 +68,14 @@ gemm_stream_kernel(const GemmP p) {
     if (pos < WB) {
       const int r = pos / ROWB;
       int cb = pos - r * ROWB;
-      if (cb >= KS * 64) cb = 0;
+      if (cb >= KS * 32 * WES) cb = 0;
       const int half = r / TN;
       const int rr = r - half * TN;
       int64_t ch = n0 + ((rr & 15) >> 2) * RUN + (rr >> 4) * 4 + (rr & 3);
       if (ch > p.n - 1) ch = p.n - 1;
-      int64_t kk = cb / 2;
-      if (kk > K - 8) kk = K - 8;
-      const unsigned char* src = Wt + ((half * p.n + ch) * K + kk) * 2;
+      int64_t kk = cb / WES;
+      if (kk > K - 16 / WES) kk = K - 16 / WES;
+      const unsigned char* src = Wt + ((half * p.n + ch) * K + kk) * WES;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(wlds + base), 16, 0, 0);
     }
@@ -81,11 +83,11 @@ gemm_stream_kernel(const GemmP p) {
   wait_vmem_all();
   __syncthreads();
 
-  const bool full_n = (n0 + TN) <= p.n;
+  const bool lane_full = run0 + RUN <= p.n;  // this lane's whole channel run exists
   const int64_t nblk = cdiv(p.m, 16);
   const int64_t stride = (int64_t)gridDim.x * 4;
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
-  const bool stats = OPM == OPM_SPLIT && (p.pro == PRO_LN || p.pro == PRO_LNMUL || p.pro == PRO_RMS);
+  const bool stats = OPM != OPM_BF16 && (p.pro == PRO_LN || p.pro == PRO_LNMUL || p.pro == PRO_RMS);
   const float invk = 1.0f / (float)K;
 
   // per-pixel offset (elements) of the second prologue operand row: local-mean map / LN*m rows
@@ -131,7 +133,7 @@ gemm_stream_kernel(const GemmP p) {
       ro = bz * p.r_bs + q * p.ldr + run0;
     }
   };
-  const bool fast = full_n && p.vec_out && (!p.has_res || p.vec_res);
+  const bool fast = lane_full && p.vec_out && (!p.has_res || p.vec_res);
 
   auto load_block = [&](int sl, int64_t blk) __attribute__((always_inline)) {
     const int64_t q = blk * 16 + lc;
@@ -240,10 +242,11 @@ gemm_stream_kernel(const GemmP p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       bf16x8 hi, lo;
+      f32x8 a;
       if constexpr (OPM == OPM_BF16) {
         hi = __builtin_bit_cast(bf16x8, raw[sl][ks].q);
       } else {
-        f32x8 a = raw_f32<TA>(raw[sl][ks]);
+        a = raw_f32<TA>(raw[sl][ks]);
         const int64_t k = ks * 32 + lg * 8;
         if (p.pro == PRO_LN) {
 #pragma unroll
@@ -269,17 +272,26 @@ gemm_stream_kernel(const GemmP p) {
           }
         }
         if (!(pv && k < K)) a = zero8();
-        split_bf16(a, hi, lo);
+        if constexpr (OPM == OPM_SPLIT) split_bf16(a, hi, lo);
       }
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
 #pragma unroll
         for (int hf = 0; hf < G; ++hf) {
-          const bf16x8 wv = *reinterpret_cast<const bf16x8*>(
-              wlds + (size_t)(hf * TN + j * 16 + lc) * ROWB + (ks * 32 + lg * 8) * 2);
+          const unsigned char* wp = wlds + (size_t)(hf * TN + j * 16 + lc) * ROWB + (ks * 32 + lg * 8) * WES;
           f32x4 t = hf ? acc2[GATE ? j : 0] : acc[j];
-          t = mfma_bf16(wv, hi, t);
-          if constexpr (OPM == OPM_SPLIT) t = mfma_bf16(wv, lo, t);
+          if constexpr (OPM == OPM_F32) {  // fp32 products: mfma i contracts k = ks * 32 + 8 lg + i over lg
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(wp);
+            const f32x4 w1 = *reinterpret_cast<const f32x4*>(wp + 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = mfma_f32(w0[i], a.v[i], t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = mfma_f32(w1[i], a.v[4 + i], t);
+          } else {
+            const bf16x8 wv = *reinterpret_cast<const bf16x8*>(wp);
+            t = mfma_bf16(wv, hi, t);
+            if constexpr (OPM == OPM_SPLIT) t = mfma_bf16(wv, lo, t);
+          }
           if (hf) acc2[GATE ? j : 0] = t; else acc[j] = t;
         }
       }

@@ -12,7 +12,7 @@ constexpr int stream_ks_for(int64_t k, int ta) {
 }
 template <int NB, bool GATE, int OPM, int TA, int KS, bool X2>
 void launch_stream_one(const GemmP& p, dim3 grid_max, hipStream_t s, int) {
-  constexpr int lds = stream_lds_bytes(NB, GATE, KS);
+  constexpr int lds = stream_lds_bytes(NB, GATE, KS, OPM);
   auto fn = &gemm_stream_kernel<NB, GATE, OPM, TA, KS, X2>;
   static const int per_cu = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,

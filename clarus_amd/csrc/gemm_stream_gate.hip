@@ -21,6 +21,9 @@ namespace clarus {
     if (x2) { S_KS(NB, OPM_SPLIT, DT_F32, true) }                     \
     S_KS(NB, OPM_SPLIT, DT_F32, false)                               \
   }                                                                  \
+  if (opm == OPM_F32 && ta == DT_F32 && ks <= 4 && !x2) {             \
+    S_KS(NB, OPM_F32, DT_F32, false)                                 \
+  }                                                                  \
   return nullptr;
 
 GemmLaunch pick_gemm_stream_gate(int nb, int opm, int ta, int ks, bool x2) {
