@@ -14,7 +14,9 @@ Extra fields of the JSON line:
   cpu_baseline  the oracle (CPU restatement of the reference PyTorch backend) running the
                 same config-2 step on this host's cores (fp32 math, bf16 storage)
   per_op        every config 1-5 op: time, TFLOP/s, GB/s, bound and fraction of the bound.
-                Ops outside the step are timed cold: the L2 / MALL is flushed before each rep.
+                Ops outside the step are timed cold: before each rep a read-only pass over
+                512 MB (larger than the 256 MB MALL) evicts the caches without leaving dirty
+                lines whose write-back would overlap the timed op.
   nafnet_e2e    NAFNet-w64 720p bf16 forward (HIP GEMMs, non-GEMM ops on torch) in ms
 
   python bench.py --summarize-trace DIR   per-(kernel, grid) durations from a rocprofv3
@@ -265,7 +267,8 @@ def main() -> None:
 
     # ------------------------------------------------------------ other configs, cold per op
     if not args.no_ops:
-        flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)  # > MALL (256 MB)
+        flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)  # > MALL (256 MB)
+        sink = torch.empty((), dtype=torch.float32, device=dev)
         others = (wl.config1_cases(hip32, dev) + wl.config3_cases(hip32, dev) + wl.config4_cases(hip, hip32, dev)
                   + wl.config5_cases(hip, dev))
         for c in others:
@@ -273,7 +276,7 @@ def main() -> None:
                 c.run()
             ts = []
             for _ in range(args.reps):
-                flush.zero_()
+                torch.sum(flush, dim=0, out=sink)  # reads 512 MB, writes 4 bytes
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record(stream)
                 c.run()
@@ -282,7 +285,7 @@ def main() -> None:
             torch.cuda.synchronize()
             us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in ts)
             rows.append(op_row(c, us))
-        del flush
+        del flush, sink
     for r in rows:
         log(f"[op] cfg{r['config']} {r['op']:<44} {r['dtype']:>4} {r['us']:9.2f} us {r['tflops']:8.1f} TF/s "
             f"{r['gbs']:8.0f} GB/s  {r['bound']:>4} bound {r['t_bound_us']:8.2f} us  frac {r['frac']:.3f}")
