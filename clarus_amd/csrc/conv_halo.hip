@@ -18,7 +18,7 @@ void launch_one(GemmP& p, hipStream_t s) {
                             true);
   (void)attr;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 256, lds) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 512, lds) !=
           hipSuccess ||
       per_cu < 1)
     per_cu = 1;
@@ -28,7 +28,7 @@ void launch_one(GemmP& p, hipStream_t s) {
   int64_t per_col = 256LL * per_cu / ncol;  // persistent: every workgroup resident
   if (per_col < 1) per_col = 1;
   if (per_col > ptiles) per_col = ptiles;
-  hipLaunchKernelGGL(fn, dim3((unsigned)(per_col * ncol)), dim3(256), lds, s, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)(per_col * ncol)), dim3(512), lds, s, p);
 }
 
 template <int TR, bool UP2>

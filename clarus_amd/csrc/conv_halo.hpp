@@ -9,9 +9,9 @@
 //     ((8 + 2) x (32 + 2) pixels, or 6 x 18 at input resolution with the x2 upsample) arrives by
 //     direct global->LDS copies into a ring of STAGES buffers; taps outside the image read a
 //     zero page, so the padding costs no branches,
-//   * and computes all nine taps from the halo: each wave owns two output rows (4 blocks of 16
-//     pixels) and all TR channels, one bf16 MFMA (16 x 16 x 32) per (tap, pixel block, 16
-//     channels).
+//   * and computes all nine taps from the halo: each of the 8 waves owns one output row (2
+//     blocks of 16 pixels) and all TR channels, one bf16 MFMA (16 x 16 x 32) per (tap, pixel
+//     block, 16 channels); two waves per SIMD hide each other's LDS latency.
 // The K loop of a tile is one chunk per step with a single barrier; the epilogue (bias,
 // LeakyReLU, out_scale, residual, 16-byte stores into a channel slice of the output) runs once
 // per tile outside it, and the next tile's first halo is already in flight by then.
@@ -32,7 +32,7 @@ struct HaloGeom {
   static constexpr int px = rows * cols;                          // 108 / 340
   static constexpr int px_pad = UP2 ? 128 : 384;                  // a whole number of 16-pixel copies per wave
   static constexpr int bytes = px_pad * 64;                       // 32 bf16 channels per pixel
-  static constexpr int copies = px_pad / 64;                      // 16-byte copies per lane per stage (4 waves)
+  static constexpr int copies = px_pad / 128;                     // 16-byte copies per lane per stage (8 waves)
 };
 
 // LDS bytes of the resident weights (rounded up to whole 1 KiB copies) and of the kernel
@@ -53,8 +53,10 @@ __device__ __forceinline__ void wait_copies(int stages_later) {
   else __builtin_amdgcn_s_waitcnt(0x0F70 | COPIES);
 }
 
+constexpr int CH_WAVES = 8;  // one output row of the tile per wave
+
 template <int TR, bool UP2, int STAGES>
-__global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
+__global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
   using HG = HaloGeom<UP2>;
   constexpr int NRB = TR / 16;  // MFMA row blocks (16 output channels each)
   constexpr int RUN = 4 * NRB;  // contiguous output channels per lane
@@ -87,7 +89,7 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
 
   // ---- resident weights: unit v of the LDS region is row v / upr, 8 k at (v % upr) * 8; the
   // pad unit of a row and the units past the last row take any valid source
-  for (int v0 = wave * 64; v0 < wunits; v0 += 256) {
+  for (int v0 = wave * 64; v0 < wunits; v0 += 64 * CH_WAVES) {
     const int v = v0 + lane;
     const int r = v / upr, j = v - r * upr;
     const bool real = r < TR && j < upr - 1;
@@ -99,12 +101,12 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
                                      (__attribute__((address_space(3))) void*)(wl + v0 * 16), 16, 0, 0);
   }
 
-  // ---- halo copies: copy j of a wave moves the 16 halo pixels (wave + 4 j) * 16 .. + 15; lane
-  // i fills pixel hp = (wave + 4 j) * 16 + i / 4, slot i % 4 with source unit slot ^ ((hp / 2) % 4)
+  // ---- halo copies: copy j of a wave moves the 16 halo pixels (wave + 8 j) * 16 .. + 15; lane
+  // i fills pixel hp = (wave + 8 j) * 16 + i / 4, slot i % 4 with source unit slot ^ ((hp / 2) % 4)
   int hp_r[COPIES], hp_c[COPIES], hp_u[COPIES];
 #pragma unroll
   for (int j = 0; j < COPIES; ++j) {
-    const int hp = (wave + 4 * j) * 16 + (lane >> 2);
+    const int hp = (wave + CH_WAVES * j) * 16 + (lane >> 2);
     hp_u[j] = (lane & 3) ^ ((hp >> 1) & 3);
     hp_r[j] = hp < HG::px ? hp / HG::cols : -1000000;  // padding slots: always outside the image
     hp_c[j] = hp < HG::px ? hp - (hp / HG::cols) * HG::cols : 0;
@@ -132,8 +134,8 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
 #pragma unroll
     for (int j = 0; j < COPIES; ++j)
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(hsrc[j] + cb),
-                                       (__attribute__((address_space(3))) void*)(st + (wave + 4 * j) * 1024), 16, 0,
-                                       0);
+                                       (__attribute__((address_space(3))) void*)(st + (wave + CH_WAVES * j) * 1024), 16,
+                                       0, 0);
     is_stage = is_stage + 1 == STAGES ? 0 : is_stage + 1;
     if (++is_chunk == nch) {
       is_chunk = 0;
@@ -142,9 +144,9 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
     }
   };
 
-  f32x4 acc[4][NRB];
+  f32x4 acc[2][NRB];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < NRB; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -169,8 +171,8 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
           wf[rb] = *reinterpret_cast<const bf16x8*>(wl + (rb * 16 + lc) * wrowb +
                                                     ((tap * cin + kc * CH_KC) / 8 + lg) * 16);
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
-          const int Y = 2 * wave + (pb >> 1), Xo = (pb & 1) * 16 + lc;
+        for (int pb = 0; pb < 2; ++pb) {
+          const int Y = wave, Xo = pb * 16 + lc;
           const int hp = UP2 ? ((Y + dy + 1) >> 1) * HG::cols + ((Xo + dx + 1) >> 1) : (Y + dy) * HG::cols + Xo + dx;
           const bf16x8 af = *reinterpret_cast<const bf16x8*>(hb + hp * 64 + ((lg ^ ((hp >> 1) & 3)) * 16));
 #pragma unroll
@@ -192,9 +194,9 @@ __global__ void __launch_bounds__(256) conv_halo_kernel(const GemmP p) {
 #pragma unroll
       for (int i = 0; i < RUN; ++i) b1[i] = (p.bias && run0 + i < p.n) ? p.bias[run0 + i] : 0.f;
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        const int oy = ty * CH_TH + 2 * wave + (pb >> 1);
-        const int ox = tx * CH_TW + (pb & 1) * 16 + lc;
+      for (int pb = 0; pb < 2; ++pb) {
+        const int oy = ty * CH_TH + wave;
+        const int ox = tx * CH_TW + pb * 16 + lc;
         float v[RUN];
 #pragma unroll
         for (int j = 0; j < NRB; ++j)
