@@ -4,10 +4,13 @@
 
 A step is one pass of BASELINE config 2 (NAFNet-w64 720p pointwise GEMMs, bf16 operands, fp32
 accumulation): at each of the 5 UNet levels the expand c -> 2c + bias + SimpleGate and the
-c -> c + bias, * beta, + residual GEMM, inputs resident in HBM. `value` is the step's
-algorithmic TFLOP/s. Every op of every timed step is bracketed by HIP events on the stream it
-runs on (torch's current stream), so the per-op times and the dominant kernel's roofline come
-from the same launches a rocprofv3 kernel trace of this command sees.
+c -> c + bias, * beta, + residual GEMM, inputs resident in HBM. The step is captured in a HIP
+graph (as clarus's worker captures its static-shape forward) and `value` is its algorithmic
+TFLOP/s over K replays. Per-op times come from the same K steps launched eagerly behind a
+bounded GPU spin (the host queues every launch before the GPU gets to them), each op bracketed
+by HIP events on the stream it runs on (torch's current stream), so the per-op times and the
+dominant kernel's roofline come from launches a rocprofv3 kernel trace of this command sees,
+without host-side launch gaps.
 
 Extra fields of the JSON line:
   roofline      dominant kernel of the step (largest share of the step time) against its bound
@@ -217,27 +220,47 @@ def main() -> None:
         torch.cuda.synchronize()
         log(f"[bench] pmc pass: copy of {COPY_BYTES} B, then {[c.name for c in step]}")
         return
-    for _ in range(args.warmup):
+    # the step as one HIP graph (timed for `value`), captured on a side stream after an eager
+    # warm-up: no host-side launch overhead enters the timed region
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for _ in range(max(args.warmup, 1)):
+            for c in step:
+                c.run()
+    torch.cuda.synchronize()
+    g_step = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_step, stream=side):
         for c in step:
             c.run()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in step]
-          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        g_step.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for _ in range(args.steps):
+        g_step.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    # per-op times: the same K steps launched eagerly behind a bounded GPU spin, so the host has
+    # queued every timed launch before the GPU reaches them (kernels run back to back, no host
+    # launch gaps inside the events)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in step]
+          for _ in range(args.steps)]
+    torch.cuda._sleep(int(2.4e8))  # ~0.1 s of spinning
     for s in range(args.steps):
         for i, c in enumerate(step):
             ev[s][i][0].record(stream)
             c.run()
             ev[s][i][1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / args.steps
     per_step_op = []
     for i, c in enumerate(step):
         us = statistics.mean(ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e3 for s in range(args.steps))
         per_step_op.append(us)
     value = flops_step / (ms_step / 1e3) / 1e12
-    log(f"[bench] step {ms_step:.3f} ms -> {value:.1f} TFLOP/s")
+    log(f"[bench] step {ms_step:.3f} ms -> {value:.1f} TFLOP/s (graph replays; eager ops sum {sum(per_step_op):.1f} us)")
 
     def op_row(c, us):
         tb, bound = c.t_bound()

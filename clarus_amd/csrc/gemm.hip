@@ -228,9 +228,18 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const int64_t run_div = a->c_mode == CLARUS_C_SHUFFLE ? a->n / 4 : 0;
   // W-resident streaming kernel for row operands with K <= 256 (bf16 A) / 128 (fp32 A) (tile 0 = auto, 8 / 9 = force
   // NB 4 / 8); the tiled kernel otherwise (tiles 1..7 force one of its tile shapes)
+  // Automatic choice for bf16 rows without a prologue (measured on the config-2 shapes):
+  // K > 128 (K % 32 == 0): the DMA-pipelined tile kernel; K <= 128 with a residual: the tiled
+  // kernel with 64 x 64 tiles (the streaming kernel's residual prefetch costs it ~25 % there).
+  const bool plain_bf16 = a->a_mode == CLARUS_A_ROWS && opm == OPM_BF16 && a->pro == PRO_NONE && a->batch == 1;
+  const bool auto_dma = a->tile == 0 && plain_bf16 && a->k > 128 && a->k % 32 == 0 && (a->lda * 2) % 16 == 0 &&
+                        (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
+  int tile_override = 0;
+  if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && !run_div) tile_override = 3;
   // fp32 weights stream with fp32 A and K <= 128, no second prologue operand (LDS holds fp32 rows)
   const bool stream_opm = opm != OPM_F32 || (a->a_dtype == DT_F32 && a->pro != PRO_MUL && a->pro != PRO_LNMUL);
-  if (a->a_mode == CLARUS_A_ROWS && stream_opm && (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
+  if (a->a_mode == CLARUS_A_ROWS && stream_opm && !auto_dma && !tile_override &&
+      (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
     const int ks = stream_ks_for(a->k, a->a_dtype);
     int nb = a->tile == 8 ? 4 : a->tile == 9 ? 8 : ((a->n <= 64 || a->gate) ? 4 : 8);
     if (opm == OPM_F32 && a->gate) nb = 4;  // fp32 gate rows of NB 8 exceed the LDS budget
@@ -263,7 +272,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const bool dma_ok = lds_shape && opm == OPM_BF16 && a->pro == PRO_NONE && a->k % 32 == 0 &&
                       (a->lda * 2) % 16 == 0;
   CLARUS_REQUIRE(a->tile != 11 || dma_ok, "gemm: the DMA-pipelined kernel does not take this problem");
-  if (dma_ok && (a->tile == 11 || (use_lds && a->tile == 0))) {
+  if (dma_ok && (a->tile == 11 || auto_dma || (use_lds && a->tile == 0))) {
     launch_gemm_dma(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
   }
@@ -273,7 +282,9 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                    "gemm: no pipelined tile kernel for operand mode %d A dtype %d", opm, a->a_dtype);
     return check_launch("gemm");
   }
-  const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(a->m, a->n, a->k, a->batch, a->gate != 0, opm, run_div);
+  const int tile = a->tile > 0 ? a->tile - 1
+                   : tile_override ? tile_override - 1
+                                   : auto_tile(a->m, a->n, a->k, a->batch, a->gate != 0, opm, run_div);
   CLARUS_REQUIRE(tile >= 0 && tile < kNumTiles && (!run_div || run_div % (4 * kTileNB[tile]) == 0),
                  "gemm: tile %d does not fit the pixel-shuffle quadrant width", tile + 1);
   return launch(p, a->a_mode == CLARUS_A_ROWS ? AM_ROWS : AM_S2D, a->gate != 0, opm, a->a_dtype, tile, a->batch,

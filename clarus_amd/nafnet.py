@@ -202,7 +202,8 @@ def psnr(pred: torch.Tensor, gt: torch.Tensor, peak: float = 1.0) -> float:
 
 def bench_forward(dev, reps: int = 20, log=print) -> dict:
     """NAFNet-GoPro-w64 (NAFNetLocal, enc [1, 1, 1, 28], mid 1, dec [1, 1, 1, 1]) 720p bf16
-    forward: HIP GEMM-family ops, non-GEMM ops on torch; captured in a HIP graph after an eager
+    forward: GEMM-family ops, depthwise conv and TLC box mean on `hip`, pixel (un)shuffle and
+    elementwise adds on torch; captured in a HIP graph after an eager
     warm-up, median of `reps` event-timed replays."""
     from . import spatial_torch  # noqa: F401  (registers "torch" for the non-GEMM ops)
     from .dispatch import Ops
