@@ -108,6 +108,16 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Workgroup barrier that leaves outstanding global loads in flight. __syncthreads() is a
+// workgroup fence plus s_barrier, and the fence makes every wave wait for all of its vector
+// memory operations first (vmcnt(0)): that drains a prefetch or LDS-copy ring at each barrier.
+// Callers of this barrier order their global -> LDS copies with explicit vmcnt waits; the
+// wave's own LDS reads and writes are complete before it arrives (lgkmcnt(0)). The asm is also
+// a compiler barrier for memory operations.
+__device__ __forceinline__ void barrier_keep_vm() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // exact-erf GELU (torch.nn.functional.gelu default)
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));

@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
     for (int kc = 0; kc < nch; ++kc, ++s) {
       const int later = (nsteps - 1 - s) < (STAGES - 2) ? (nsteps - 1 - s) : (STAGES - 2);
       wait_copies<COPIES>(kc == 0 ? 0 : later);  // a tile's first chunk: everything (weights, epilogue)
-      __syncthreads();
+      barrier_keep_vm();
       if (s + STAGES - 1 < nsteps) issue();
       const unsigned char* hb = ring + c_stage * HG::bytes;
 #pragma unroll

@@ -268,10 +268,19 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                      (hipStream_t)stream);
     p.stats = a->stats;
   }
-  // bf16 operands without prologue: the multi-stage DMA pipeline (tile 11 forces it)
+  // bf16 operands without prologue: the DMA-pipelined kernels. K % 64 == 0 runs on 32x32x16
+  // MFMAs with 64-k chunks (tile 13 forces it), other K % 32 == 0 on 16x16x32 MFMAs with 32-k
+  // chunks (tile 11 forces it)
   const bool dma_ok = lds_shape && opm == OPM_BF16 && a->pro == PRO_NONE && a->k % 32 == 0 &&
-                      (a->lda * 2) % 16 == 0;
+                      (a->lda * 2) % 16 == 0 &&
+                      cdiv(a->m, 128) * cdiv(a->n, 64) < ((int64_t)1 << 31);  // tile index in 31 bits
+  const bool m32_ok = dma_ok && a->k % 64 == 0 && (!run_div || run_div % kGemmM32Run == 0);
   CLARUS_REQUIRE(a->tile != 11 || dma_ok, "gemm: the DMA-pipelined kernel does not take this problem");
+  CLARUS_REQUIRE(a->tile != 13 || m32_ok, "gemm: the 32x32 DMA-pipelined kernel does not take this problem");
+  if (a->tile == 13 || (m32_ok && a->tile == 0 && (auto_dma || use_lds))) {
+    launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
+    return check_launch("gemm");
+  }
   if (dma_ok && (a->tile == 11 || auto_dma || (use_lds && a->tile == 0))) {
     launch_gemm_dma(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");

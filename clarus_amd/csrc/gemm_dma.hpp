@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmP p) {
       // At a tile's first chunk the previous epilogue's memory ops share the counter: wait for all.
       const int later = (nsteps - 1 - s) < (DMA_STAGES - 2) ? (nsteps - 1 - s) : (DMA_STAGES - 2);
       wait_vm(kc == 0 ? 0 : later * DMA_COPIES);
-      __syncthreads();
+      barrier_keep_vm();
       if (s + DMA_STAGES - 1 < nsteps) issue();
       const unsigned char* st = ring + c_stage * DMA_STAGE;
       const unsigned char* wb = st + DMA_ABYTES;

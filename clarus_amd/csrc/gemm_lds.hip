@@ -1,6 +1,7 @@
 // gemm_lds_kernel instantiations and launcher.
 #include "capi.hpp"
 #include "gemm_dma.hpp"
+#include "gemm_mfma32.hpp"
 #include "gemm_lds.hpp"
 #include "gemm_lds_dispatch.hpp"
 
@@ -53,7 +54,33 @@ void launch_dma(GemmP& p, hipStream_t s) {
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), lds, s, p);
 }
 
+template <bool GATE>
+void launch_m32(GemmP& p, hipStream_t s) {
+  auto fn = &gemm_mfma32_kernel<GATE>;
+  static const int per_cu = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), 256, M32_LDS) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  p.ptiles = cdiv(p.m, M32_P);
+  const int64_t tiles = p.ptiles * cdiv(p.n, M32_R / (GATE ? 2 : 1));
+  int64_t gx = 256LL * per_cu;
+  const int64_t need = cdiv(tiles, 8) * 8;
+  if (gx > need) gx = need;
+  hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), M32_LDS, s, p);
+}
+
 }  // namespace
+
+void launch_gemm_m32(GemmP& p, bool gate, hipStream_t s) {
+  if (gate) launch_m32<true>(p, s);
+  else launch_m32<false>(p, s);
+}
 
 void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s) {
   if (gate) launch_dma<true>(p, s);

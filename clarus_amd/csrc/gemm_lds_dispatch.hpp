@@ -12,11 +12,16 @@ bool launch_gemm_lds(GemmP& p, bool gate, int opm, int ta, bool x2, hipStream_t 
 // Launches gemm_dma_kernel for p (AM_ROWS, batch 1, bf16 A and W, no prologue, K % 32 == 0).
 void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s);
 
+// Launches gemm_mfma32_kernel for p (AM_ROWS, batch 1, bf16 A and W, no prologue, K % 64 == 0,
+// a pixel-shuffle quadrant a multiple of 16 channels).
+void launch_gemm_m32(GemmP& p, bool gate, hipStream_t s);
+
 // Launches conv_halo_kernel for p (bf16 x and weights, cin % 32 == 0, row output). Returns
 // false when the resident weights of even a 32-channel tile do not fit in LDS.
 bool launch_conv_halo(GemmP& p, hipStream_t s);
 
-// output channels per tile (the lane run must divide a pixel-shuffle quadrant)
+// output channels per lane run (the run must divide a pixel-shuffle quadrant)
 constexpr int gemm_lds_run(bool gate) { return gate ? 8 : 16; }
+constexpr int kGemmM32Run = 16;
 
 }  // namespace clarus

@@ -1,0 +1,270 @@
+// DMA-pipelined bf16 GEMM on 32x32x16 MFMAs with 64-k chunks (MFMA-bound NHWC shapes without
+// prologue: NAFNet levels 2-4 expand and c -> c, K % 64 == 0), gfx950.
+//
+// Same math and output mapping as gemm_kernel (D[channel][pixel] = W^T . A^T on bf16 MFMA, a
+// lane accumulates a run of consecutive output channels of one pixel). Three measured facts set
+// the shape of this kernel:
+//   * a global -> LDS copy instruction moves 64 x 16 B; when those bytes are 64-byte pieces of
+//     16 rows, L2 delivers 9-17 TB/s, when they are 128-byte pieces of 8 rows it delivers
+//     ~33 TB/s. A chunk is therefore 64 k (128 bytes of every row);
+//   * 32x32x16 bf16 MFMAs issued back to back by one wave per SIMD reach ~2.3 PFLOP/s, the
+//     16x16x32 ones ~1.3 (they need two waves per SIMD);
+//   * on the NAFNet shapes two workgroups per CU with a 2-stage ring (64 KiB each) beat one
+//     workgroup with a 3- or 4-stage ring: a single wave per SIMD serializes copy issue, LDS
+//     reads and MFMAs, where two interleave them;
+//   * LDS reads run at ~128 B/clk per CU: a wave computes 64 pixels x 64 rows (2 x 2 MFMA
+//     blocks) from 4 fragment reads per 16-k step.
+// Data movement:
+//   * a workgroup computes a 128-pixel x 128-W^T-row tile (128 output channels, or 64 with
+//     SimpleGate, both halves of a channel in the same lane); its 4 waves split it 2 x 2;
+//   * A rows and W^T rows of each 64-k chunk travel global -> LDS by direct 16-byte copies into
+//     a ring of M32_STAGES stages of 32 KiB; rows are 128 bytes, their eight 16-byte units
+//     XOR-swizzled by (row / 2) % 8 so the fragment reads of 16 consecutive rows hit 16
+//     distinct 16-byte bank groups;
+//   * the (tile, chunk) steps of a workgroup form one flat pipeline across tile boundaries;
+//     tiles are dealt out XCD-aware (a contiguous tile range per XCD, the column tiles of a
+//     pixel tile adjacent).
+// Output mapping of the 32x32x16 MFMA: lane l holds D[8 (j / 4) + 4 (l / 32) + j % 4][l % 32]
+// in accumulator element j. W^T rows are permuted when staged so that element j of lane l is
+// channel 16 (l / 32) + j of its 32-row block: every lane owns 16 consecutive channels.
+// Memory waits are explicit: with two stages the chunk waited for is always the newest copy
+// group, so every wait is vmcnt(0) (it also covers an epilogue's loads and stores).
+#pragma once
+
+#include "gemm_lds.hpp"
+
+namespace clarus {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int M32_P = 128;                        // pixels per tile
+constexpr int M32_R = 128;                        // W^T rows per tile
+constexpr int M32_KC = 64;                        // k per chunk
+constexpr int M32_ROWB = 128;                     // bytes per staged row (64 bf16)
+constexpr int M32_ABYTES = M32_P * M32_ROWB;      // 16 KiB
+constexpr int M32_WBYTES = M32_R * M32_ROWB;      // 16 KiB
+constexpr int M32_STAGE = M32_ABYTES + M32_WBYTES;
+constexpr int M32_COPIES = M32_STAGE / 1024 / 4;  // 16-byte copies per lane per stage (8)
+constexpr int M32_RUN = 16;                       // consecutive output channels per lane
+constexpr int M32_STAGES = 2;                     // LDS ring depth
+constexpr int M32_LDS = M32_STAGES * M32_STAGE;   // 64 KiB: two workgroups per CU
+
+__device__ __forceinline__ int m32_swz(int row, int unit) { return unit ^ ((row >> 1) & 7); }
+
+__device__ __forceinline__ f32x16 mfma32_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// vmcnt(N) (expcnt / lgkmcnt untouched): the count's low 4 bits in [3:0], high 2 bits in [15:14]
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+
+// two workgroups per CU: registers capped at 256 per lane
+template <bool GATE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_mfma32_kernel(const GemmP p) {
+  constexpr int STAGES = M32_STAGES;
+  static_assert(STAGES == 2, "the waits below assume one chunk in flight behind the computed one");
+  constexpr int TNO = GATE ? M32_R / 2 : M32_R;  // output channels per tile
+  extern __shared__ __attribute__((aligned(16))) unsigned char ring[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int wp = wave & 1, wn = wave >> 1;
+  const int64_t K = p.k;
+  const int nch = (int)(K / M32_KC);
+  const int ntn = (int)cdiv(p.n, TNO);
+  const int T = (int)p.ptiles * ntn;  // the host checks that this fits 31 bits
+  const unsigned char* A = (const unsigned char*)p.a;
+  const unsigned char* Wt = (const unsigned char*)p.wt;
+
+  const int xcd = blockIdx.x & 7;
+  const int per = gridDim.x >> 3;
+  const int span = (T + 7) >> 3;
+  const int t0 = xcd * span + (blockIdx.x >> 3);
+  const int t_end = (xcd + 1) * span < T ? (xcd + 1) * span : T;
+  const int ntiles = t0 < t_end ? (t_end - t0 + per - 1) / per : 0;
+  const int nsteps = ntiles * nch;
+
+  // copies of one chunk into ring stage st: 32 KiB = 32 x 1 KiB; wave w takes the KiBs w + 4 j
+  // (the first 16 are A, the rest W^T). A KiB is 8 rows x 128 B: lane i fills row 8 (KiB % 16)
+  // + i / 8, slot i % 8 with source unit m32_swz(row, slot). The issue position (tile, chunk)
+  // advances incrementally.
+  int is_tile = 0, is_chunk = 0, is_stage = 0;
+  const unsigned char* src_base[M32_COPIES];  // this lane's source at k = 0 for the issue tile
+  auto set_issue_tile = [&]() __attribute__((always_inline)) {
+    const int t = t0 + is_tile * per;
+    const int pt = t / ntn;
+    const int nt = t - pt * ntn;
+#pragma unroll
+    for (int j = 0; j < M32_COPIES; ++j) {
+      const int kib = wave + 4 * j;
+      const int row = (kib & 15) * 8 + (lane >> 3);
+      const int unit = m32_swz(row, lane & 7);
+      if (kib < 16) {
+        int64_t q = (int64_t)pt * M32_P + row;
+        if (q > p.m - 1) q = p.m - 1;  // rows past M: any valid row, its outputs are not stored
+        src_base[j] = A + (q * p.lda + unit * 8) * 2;
+      } else {
+        // W^T row `row` = wave-row wr, block rb, block row rr = 8 g + 4 h + i holds channel
+        // 16 h + 4 g + i of its 32-channel run (gate: block rb is the SimpleGate half)
+        const int wr = row >> 6, rb = (row >> 5) & 1, rr = row & 31;
+        const int cw = 16 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3);
+        const int half = GATE ? rb : 0;
+        const int ch = GATE ? wr * 32 + cw : wr * 64 + rb * 32 + cw;
+        int64_t c = (int64_t)nt * TNO + ch;
+        if (c > p.n - 1) c = p.n - 1;  // channels past N: not stored
+        src_base[j] = Wt + ((half * p.n + c) * K + unit * 8) * 2;
+      }
+    }
+  };
+  auto issue = [&]() __attribute__((always_inline)) {
+    const int kb = is_chunk * (M32_KC * 2);
+    unsigned char* st = ring + is_stage * M32_STAGE;
+#pragma unroll
+    for (int j = 0; j < M32_COPIES; ++j)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src_base[j] + kb),
+                                       (__attribute__((address_space(3))) void*)(st + (wave + 4 * j) * 1024), 16, 0,
+                                       0);
+    is_stage = is_stage + 1 == STAGES ? 0 : is_stage + 1;
+    if (++is_chunk == nch) {
+      is_chunk = 0;
+      ++is_tile;
+      set_issue_tile();
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+
+  // MFMA fragments of one 16-k step, double-buffered: step ks + 1 is read while step ks computes
+  bf16x8 wf[2][2], af[2][2];
+  auto load_frags = [&](int buf, int stage, int ks) __attribute__((always_inline)) {
+    const unsigned char* st = ring + stage * M32_STAGE;
+    const int u = 2 * ks + hl;  // 16-byte unit: k = 16 ks + 8 (l / 32) .. + 8
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int r = wn * 64 + rb * 32 + l32;
+      wf[buf][rb] = *reinterpret_cast<const bf16x8*>(st + M32_ABYTES + r * M32_ROWB + m32_swz(r, u) * 16);
+    }
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      const int r = wp * 64 + pb * 32 + l32;
+      af[buf][pb] = *reinterpret_cast<const bf16x8*>(st + r * M32_ROWB + m32_swz(r, u) * 16);
+    }
+  };
+  auto products = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf[buf][rb], af[buf][pb], acc[pb][rb]);
+  };
+
+  if (nsteps == 0) return;  // nothing issued
+  set_issue_tile();
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nsteps) issue();
+  // chunk 0 landed everywhere; the ring's last stage is free
+  wait_vmcnt<0>();
+  barrier_keep_vm();
+  if (STAGES - 1 < nsteps) issue();
+  load_frags(0, 0, 0);
+  int s = 0;        // global step (chunk) index
+  int c_stage = 0;  // ring stage of step s
+
+  for (int tl = 0; tl < ntiles; ++tl) {
+    // ---- the tile's K loop: one 64-k chunk per step, 4 MFMA steps of 16 k
+    for (int kc = 0; kc < nch; ++kc, ++s) {
+#pragma unroll
+      for (int ks = 0; ks < M32_KC / 16 - 1; ++ks) {
+        load_frags((ks + 1) & 1, c_stage, ks + 1);
+        products(ks & 1);
+      }
+      // last MFMA step: chunk s + 1 must have landed (this thread's copies, then everyone's);
+      // with two stages it is the newest copy group, so the wait is for all. After the barrier
+      // every wave has finished its LDS reads of chunk s, whose stage takes chunk s + 2.
+      const int n_stage = c_stage + 1 == STAGES ? 0 : c_stage + 1;
+      if (s + 1 < nsteps) {
+        wait_vmcnt<0>();
+        barrier_keep_vm();
+        if (s + STAGES < nsteps) issue();
+        load_frags(0, n_stage, 0);
+      }
+      products(1);
+      c_stage = n_stage;
+    }
+
+    // ---- epilogue of the tile: lane l owns pixel l % 32 of each pixel block and channels
+    // 16 (l / 32) + [0, 16) of each run
+    {
+      const int t = t0 + tl * per;
+      const int pt = t / ntn, nt = t - pt * ntn;
+#pragma unroll
+      for (int ro = 0; ro < (GATE ? 1 : 2); ++ro) {
+        const int64_t run0 = (int64_t)nt * TNO + (GATE ? wn * 32 : wn * 64 + ro * 32) + 16 * hl;
+        const bool full_n = run0 + M32_RUN <= p.n;
+        float b1[M32_RUN], b2[GATE ? M32_RUN : 1], sc[M32_RUN];
+#pragma unroll
+        for (int i = 0; i < M32_RUN; ++i) {
+          const bool ok = run0 + i < p.n;
+          b1[i] = (p.bias && ok) ? p.bias[run0 + i] : 0.f;
+          if constexpr (GATE) b2[i] = (p.bias && ok) ? p.bias[p.n + run0 + i] : 0.f;
+          sc[i] = ((p.scale && ok) ? p.scale[run0 + i] : 1.f) * p.out_scale;
+        }
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+          const int64_t q = (int64_t)pt * M32_P + wp * 64 + pb * 32 + l32;
+          float v[M32_RUN];
+          if constexpr (GATE) {
+#pragma unroll
+            for (int j = 0; j < M32_RUN; ++j) v[j] = (acc[pb][0][j] + b1[j]) * (acc[pb][1][j] + b2[j]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < M32_RUN; ++j) v[j] = acc[pb][ro][j] + b1[j];
+          }
+          if (q >= p.m) continue;
+          if (p.act == ACT_GELU) {
+#pragma unroll
+            for (int i = 0; i < M32_RUN; ++i) v[i] = gelu_erf(v[i]);
+          } else if (p.act == ACT_LRELU) {
+#pragma unroll
+            for (int i = 0; i < M32_RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
+          }
+#pragma unroll
+          for (int i = 0; i < M32_RUN; ++i) v[i] *= sc[i];
+          int64_t oo, rof;
+          if (p.c_mode == CM_SHUFFLE) {
+            const int64_t hwi = (int64_t)p.h * p.w;
+            const int64_t im = q / hwi;
+            const int rr = (int)(q - im * hwi);
+            const int y = rr / p.w, x = rr - (rr / p.w) * p.w;
+            const int64_t cq = p.n >> 2;
+            const int64_t qd = run0 / cq, cc = run0 - qd * cq;
+            oo = ((im * 2 * p.h + 2 * y + (qd >> 1)) * 2 * p.w + 2 * x + (qd & 1)) * cq + cc;
+            rof = oo;
+          } else {
+            oo = q * p.ldc + run0;
+            rof = q * p.ldr + run0;
+          }
+          store_run<M32_RUN>(p, v, oo, rof, run0, full_n);
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+    }
+  }
+}
+
+}  // namespace clarus

@@ -101,7 +101,8 @@ typedef struct ClarusGemmArgs {
   float ln_eps, out_scale, slope;
   int32_t tile;       /* 0 = library's choice; else a kernel / tile id for sweeps: 1-7 tiled
                          shapes, 8 / 9 W-resident streaming (4 / 8 channel blocks), 10 pipelined
-                         LDS tile, 11 DMA-pipelined tile (bf16 A, no prologue, K % 32 == 0) */
+                         LDS tile, 11 DMA-pipelined tile (bf16 A, no prologue, K % 32 == 0),
+                         13 DMA-pipelined 32x32-MFMA tile (bf16 A, no prologue, K % 64 == 0) */
 } ClarusGemmArgs;
 
 /* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */

@@ -119,10 +119,11 @@ def test_linear_long_k(k, nout, gate, hip_bf16):
     check(got.cpu(), REF.linear(x, wt, b, gate=gate, act=act, scale=sc, residual=res), f"linear K{k} N{nout} gate={gate}")
 
 
-@pytest.mark.parametrize("tile", [0, 10, 11])
+@pytest.mark.parametrize("tile", [0, 10, 11, 13])
 def test_long_k_kernels_agree(tile, hip_bf16):
-    """Through the C ABI, the pipelined LDS tile kernel (10), the DMA-pipelined kernel (11) and
-    the library's choice (0) on one long-K problem with a gate, against the oracle."""
+    """Through the C ABI, the pipelined LDS tile kernel (10), the DMA-pipelined kernels (11:
+    16x16 MFMAs and 32-k chunks; 13: 32x32 MFMAs and 64-k chunks) and the library's choice (0)
+    on one long-K problem with a gate, against the oracle."""
     import ctypes
 
     from clarus_amd import _lib
@@ -141,6 +142,46 @@ def test_long_k_kernels_agree(tile, hip_bf16):
     _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
                "gemm")
     assert_fp32(out.cpu(), ref, rel=1e-5, what=f"long-K gated GEMM tile {tile}")
+
+
+@pytest.mark.parametrize("gate,k", [(False, 1024), (True, 192), (False, 64), (True, 2048)])
+def test_m32_kernel_epilogues(gate, k, hip_bf16):
+    """Through the C ABI, the 32x32-MFMA DMA-pipelined kernel with bf16 output: ragged pixel
+    count and channel count (a partial lane run), bias + GELU or gate, scale and a bf16 residual;
+    K from one chunk to 32 chunks."""
+    tile = 13
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(35)
+    m, n = 1000, 200
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    wt = rnd(g, 2 * n if gate else n, k, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc = rnd(g, 2 * n if gate else n), rnd(g, n)
+    res = rnd(g, m, n, dtype=torch.bfloat16)
+    act = None if gate else "gelu"
+    ref = REF.linear(x, wt.t().contiguous(), b, gate=gate, act=act, scale=sc, residual=res)
+    xd, wd, bd, sd, rd = dev(x, wt, b, sc, res)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=wd.data_ptr(), c=out.data_ptr(), bias=bd.data_ptr(),
+                         scale=sd.data_ptr(), res=rd.data_ptr(), m=m, n=n, k=k, batch=1, lda=k, ldc=n, ldr=n,
+                         a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.BF16, r_dtype=_lib.BF16,
+                         gate=int(gate), act=0 if gate else _lib.ACT_GELU, out_scale=1.0, tile=tile)
+    _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "gemm")
+    check(out.cpu(), ref, f"32x32 DMA GEMM tile {tile} gate={gate} K{k}")
+
+
+def test_up_long_k(hip_bf16):
+    """1x1 conv + PixelShuffle(2) with K = 256 (the DMA-pipelined kernels' store addressing)."""
+    g = gen(36)
+    n, hh, ww, k, co = 1, 21, 30, 256, 64
+    x = rnd(g, n, hh, ww, k, dtype=torch.bfloat16)
+    wkn = rnd(g, k, 4 * co, scale=k ** -0.5, dtype=torch.bfloat16)
+    res = rnd(g, n, 2 * hh, 2 * ww, co, dtype=torch.bfloat16)
+    got = hip_bf16.up(*dev(x, wkn), residual=res.cuda())
+    check(got.cpu(), REF.up(x, wkn, residual=res), "up K256")
 
 
 def test_stats_scratch_is_optional(hip_bf16):
