@@ -115,90 +115,131 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
 // ------------------------------------------------------------------- TLC local mean
 // out[i, j, c] = (1 / (k1 k2)) sum_{y = i}^{i + k1 - 1} sum_{x = j}^{j + k2 - 1} X[y, x, c],
 // i < OH = h - k1 + 1, j < OW = w - k2 + 1 (the valid windows; python/clarus/ops/
-// torch_ref.py:133-141 computes the same map from a 2-D prefix sum). Separable, two passes
-// of sliding-window running sums with fp64 accumulators (exact to the fp32 rounding of the
-// intermediate): box_v sums k1 rows into V [n, OH, w, c] fp32, box_h sums k2 columns of V.
-// A thread owns 8 channels of one column (box_v) or one output row (box_h) over a segment of
-// `seg` outputs; lanes are channel-group-minor so a wave touches contiguous NHWC rows.
-struct BoxP {
+// torch_ref.py:133-141 computes the same map from a 2-D prefix sum). Separable: a vertical
+// pass sums k1 rows into V [n, OH, w, c] fp32, a horizontal pass sums k2 columns of V. Both
+// are one 1-D sliding-window pass over "lines" (an (x, c) column of a plane, or a c of a V row):
+//
+//   W(i) = sum_{j = i}^{i + k - 1} X[j],  W(i + 1) = W(i) + X[i + k] - X[i]   (fp64, exact to the
+//   final rounding for ordinary data).
+//
+// Outputs are cut into blocks of k positions (van Herk / Gil-Werman): the windows starting in
+// block b cover only blocks b and b + 1. A workgroup owns one block of one plane for a range
+// of lines; its T threads per line each own R = k / T consecutive positions. A thread loads
+// its R rows of block b and of block b + 1 (16-byte loads: 8 bf16 or 4 fp32 channels), sums
+// them (A_s, B_s), exchanges the sums through LDS, and starts its recurrence at
+//   W(b k + s R) = sum_{s' >= s} A_s' + sum_{s' < s} B_s'
+// so no thread walks a k - 1 element warm-up and every row is read twice.
+struct BoxPass {
   const void* x;
-  float* v;
-  void* out;
-  int n, h, w, c, k1, k2, oh, ow, seg_v, seg_h, x_dt, o_dt;
-  double area;  // k1 * k2
+  void* y;
+  int64_t L, k, lo;   // axis length, window, outputs (L - k + 1)
+  int64_t inner;      // elements per axis step (contiguous), a multiple of the lane width
+  int64_t outer;      // planes (each L x inner)
+  int64_t y_plane;    // output elements per plane (lo x inner)
+  int T, R, QW;       // threads per line block, positions per thread, lane groups per workgroup
+  int nblk, nqg;      // output blocks per plane, lane-group ranges per plane
+  double scale;       // 1 / (k1 k2) on the final pass, 1 otherwise
 };
 
-__device__ __forceinline__ void add8(double (&s)[8], const f32x8& a, double sign) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) s[i] += sign * (double)a.v[i];
-}
+constexpr int BOX_BATCH = 8;  // rows loaded per batch and stream (loads in flight per thread)
 
-template <int XDT>
-__global__ void __launch_bounds__(256) box_v_kernel(const BoxP p) {
-  constexpr int ES = XDT == DT_BF16 ? 2 : 4;
-  const int g8 = p.c >> 3;
-  const int nseg = (p.oh + p.seg_v - 1) / p.seg_v;
-  const int64_t units = (int64_t)p.n * nseg * p.w * g8;
-  const int64_t row = (int64_t)p.w * p.c;  // elements per image row
-  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
-    const int g = (int)(u % g8);
-    int64_t r = u / g8;
-    const int x = (int)(r % p.w);
-    r /= p.w;
-    const int sg = (int)(r % nseg);
-    const int img = (int)(r / nseg);
-    const int i0 = sg * p.seg_v;
-    const int i1 = i0 + p.seg_v < p.oh ? i0 + p.seg_v : p.oh;
-    const unsigned char* col = (const unsigned char*)p.x + (((int64_t)img * p.h * p.w + x) * p.c + g * 8) * ES;
-    float* vout = p.v + (((int64_t)img * p.oh * p.w + x) * p.c + g * 8);
-    double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int y = i0; y < i0 + p.k1 - 1; ++y) add8(s, load8<XDT>(col + y * row * ES), 1.0);
-#pragma unroll 4
-    for (int i = i0; i < i1; ++i) {
-      add8(s, load8<XDT>(col + (int64_t)(i + p.k1 - 1) * row * ES), 1.0);
-      float* o = vout + (int64_t)i * row;
-      *reinterpret_cast<f32x4*>(o) = f32x4{(float)s[0], (float)s[1], (float)s[2], (float)s[3]};
-      *reinterpret_cast<f32x4*>(o + 4) = f32x4{(float)s[4], (float)s[5], (float)s[6], (float)s[7]};
-      add8(s, load8<XDT>(col + (int64_t)i * row * ES), -1.0);
-    }
+// channel c of a raw 16-byte load: 8 bf16 or 4 fp32
+template <int DT>
+__device__ __forceinline__ float raw_elem(const u32x4& q, int c) {
+  if constexpr (DT == DT_BF16) {
+    const unsigned w = q[c >> 1];
+    return __uint_as_float((c & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return __uint_as_float(q[c]);
   }
 }
 
-template <int ODT>
-__global__ void __launch_bounds__(256) box_h_kernel(const BoxP p) {
-  const int g8 = p.c >> 3;
-  const int nseg = (p.ow + p.seg_h - 1) / p.seg_h;
-  const int64_t units = (int64_t)p.n * p.oh * nseg * g8;
-  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
-    const int g = (int)(u % g8);
-    int64_t r = u / g8;
-    const int sg = (int)(r % nseg);
-    const int64_t irow = r / nseg;  // img * OH + i
-    const int j0 = sg * p.seg_h;
-    const int j1 = j0 + p.seg_h < p.ow ? j0 + p.seg_h : p.ow;
-    const float* vrow = p.v + (irow * p.w) * p.c + g * 8;
-    const int64_t orow = (irow * p.ow) * p.c + g * 8;
-    double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int x = j0; x < j0 + p.k2 - 1; ++x) add8(s, load8<DT_F32>(vrow + (int64_t)x * p.c), 1.0);
-#pragma unroll 4
-    for (int j = j0; j < j1; ++j) {
-      add8(s, load8<DT_F32>(vrow + (int64_t)(j + p.k2 - 1) * p.c), 1.0);
-      float o[8];
+template <int XDT, int YDT>
+__global__ void __launch_bounds__(256) box_pass_kernel(const BoxPass p) {
+  constexpr int E = XDT == DT_BF16 ? 8 : 4;  // channels per 16-byte load
+  constexpr int XES = XDT == DT_BF16 ? 2 : 4;
+  constexpr int YES = YDT == DT_BF16 ? 2 : 4;
+  __shared__ double part[2][256][E];         // A_s, B_s of every thread
+  const int tid = threadIdx.x;
+  const int qi = tid % p.QW, s = tid / p.QW;
+  int64_t wg = blockIdx.x;
+  const int qg = (int)(wg % p.nqg);
+  wg /= p.nqg;
+  const int b = (int)(wg % p.nblk);
+  const int64_t plane = wg / p.nblk;
+  const int64_t e0 = ((int64_t)qg * p.QW + qi) * E;  // first channel of this lane group
+  const bool live = e0 < p.inner;
+  const unsigned char* xp = (const unsigned char*)p.x + (plane * p.L * p.inner + e0) * XES;
+  const int64_t pitch = p.inner * XES;
+  const int64_t r0 = (int64_t)b * p.k + (int64_t)s * p.R;  // first position of the thread
+  const int64_t pend = (int64_t)s * p.R + p.R < p.k ? (int64_t)s * p.R + p.R : p.k;
+  const int nj = pend > (int64_t)s * p.R ? (int)(pend - (int64_t)s * p.R) : 0;  // positions in the block
+  // rows r0 + j of block b and r0 + k + j of block b + 1 (zero past the axis)
+  auto load_rows = [&](int j0, u32x4 (&va)[BOX_BATCH], u32x4 (&vb)[BOX_BATCH]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (float)(s[i] / p.area);
-      const int64_t oo = orow + (int64_t)j * p.c;
-      if constexpr (ODT == DT_BF16) {
-        u32x4 q;
+    for (int j = 0; j < BOX_BATCH; ++j) {
+      const int64_t ra = r0 + j0 + j, rb = ra + p.k;
+      va[j] = vb[j] = u32x4{0u, 0u, 0u, 0u};
+      if (live && j0 + j < nj && ra < p.L) va[j] = *reinterpret_cast<const u32x4*>(xp + ra * pitch);
+      if (live && j0 + j < nj && rb < p.L) vb[j] = *reinterpret_cast<const u32x4*>(xp + rb * pitch);
+    }
+  };
+  double sa[E], sb[E];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          q[i] = (unsigned)f32_to_bf16_bits(o[2 * i]) | ((unsigned)f32_to_bf16_bits(o[2 * i + 1]) << 16);
-        *reinterpret_cast<u32x4*>((unsigned short*)p.out + oo) = q;
-      } else {
-        float* op = (float*)p.out + oo;
-        *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<f32x4*>(op + 4) = f32x4{o[4], o[5], o[6], o[7]};
+  for (int c = 0; c < E; ++c) sa[c] = sb[c] = 0.0;
+  for (int j0 = 0; j0 < nj; j0 += BOX_BATCH) {
+    u32x4 va[BOX_BATCH], vb[BOX_BATCH];
+    load_rows(j0, va, vb);
+#pragma unroll
+    for (int j = 0; j < BOX_BATCH; ++j)
+#pragma unroll
+      for (int c = 0; c < E; ++c) {
+        sa[c] += (double)raw_elem<XDT>(va[j], c);
+        sb[c] += (double)raw_elem<XDT>(vb[j], c);
       }
-      add8(s, load8<DT_F32>(vrow + (int64_t)j * p.c), -1.0);
+  }
+#pragma unroll
+  for (int c = 0; c < E; ++c) {
+    part[0][tid][c] = sa[c];
+    part[1][tid][c] = sb[c];
+  }
+  __syncthreads();
+  double w[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) w[c] = 0.0;
+  for (int t = 0; t < p.T; ++t) {
+    const double* src = part[t >= s ? 0 : 1][t * p.QW + qi];  // A from sub-range s on, B before it
+#pragma unroll
+    for (int c = 0; c < E; ++c) w[c] += src[c];
+  }
+  if (!live) return;
+  unsigned char* yp = (unsigned char*)p.y + (plane * p.y_plane + e0) * YES;
+  // the recurrence over this thread's positions (rows re-read: L1 / L2 hits)
+  for (int j0 = 0; j0 < nj; j0 += BOX_BATCH) {
+    u32x4 va[BOX_BATCH], vb[BOX_BATCH];
+    load_rows(j0, va, vb);
+#pragma unroll
+    for (int j = 0; j < BOX_BATCH; ++j) {
+      const int64_t i = r0 + j0 + j;
+      if (j0 + j < nj && i < p.lo) {
+        unsigned char* o = yp + i * p.inner * YES;
+        if constexpr (YDT == DT_BF16) {
+          unsigned q[E / 2];
+#pragma unroll
+          for (int c = 0; c < E / 2; ++c)
+            q[c] = (unsigned)f32_to_bf16_bits((float)(w[2 * c] * p.scale)) |
+                   ((unsigned)f32_to_bf16_bits((float)(w[2 * c + 1] * p.scale)) << 16);
+          if constexpr (E == 8) *reinterpret_cast<u32x4*>(o) = u32x4{q[0], q[1], q[2], q[3]};
+          else *reinterpret_cast<u32x2*>(o) = u32x2{q[0], q[1]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < E; c += 4)
+            *reinterpret_cast<f32x4*>(o + c * 4) = f32x4{(float)(w[c] * p.scale), (float)(w[c + 1] * p.scale),
+                                                         (float)(w[c + 2] * p.scale), (float)(w[c + 3] * p.scale)};
+        }
+#pragma unroll
+        for (int c = 0; c < E; ++c) w[c] += (double)raw_elem<XDT>(vb[j], c) - (double)raw_elem<XDT>(va[j], c);
+      }
     }
   }
 }
@@ -228,27 +269,49 @@ extern "C" int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int
   CLARUS_REQUIRE(n * h * w * c < ((int64_t)1 << 40) && h < (1 << 30) && w < (1 << 30), "boxmean: problem too large");
   const size_t need = clarus_hip_boxmean_workspace(n, h, w, c, k1, k2);
   CLARUS_REQUIRE(scratch_bytes >= need, "boxmean: scratch holds %zu bytes, needs %zu", scratch_bytes, need);
-  const int64_t oh = h - k1 + 1, ow = w - k2 + 1, g8 = c / 8;
-  // segments: enough independent running sums to fill the GPU, not much shorter than the window
-  auto seg_for = [](int64_t outs, int64_t streams, int64_t want) {
-    int64_t nseg = streams >= want ? 1 : (want + streams - 1) / streams;
-    int64_t maxseg = (outs + 15) / 16;
-    if (nseg > maxseg) nseg = maxseg;
-    if (nseg < 1) nseg = 1;
-    return (int)((outs + nseg - 1) / nseg);
-  };
-  BoxP p{x, (float*)scratch, out, (int)n, (int)h, (int)w, (int)c, (int)k1, (int)k2, (int)oh, (int)ow,
-         seg_for(oh, n * w * g8, 32768), seg_for(ow, n * oh * g8, 65536), x_dtype, o_dtype,
-         (double)k1 * (double)k2};
-  const int64_t uv = n * w * g8 * ((oh + p.seg_v - 1) / p.seg_v);
-  const int64_t uh = n * oh * g8 * ((ow + p.seg_h - 1) / p.seg_h);
+  const int64_t oh = h - k1 + 1;
   hipStream_t s = (hipStream_t)stream;
-  const unsigned bv = (unsigned)std::min<int64_t>(cdiv(uv, 256), 8192);
-  const unsigned bh = (unsigned)std::min<int64_t>(cdiv(uh, 256), 8192);
-  if (x_dtype == DT_BF16) hipLaunchKernelGGL(box_v_kernel<DT_BF16>, dim3(bv), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(box_v_kernel<DT_F32>, dim3(bv), dim3(256), 0, s, p);
-  if (o_dtype == DT_BF16) hipLaunchKernelGGL(box_h_kernel<DT_BF16>, dim3(bh), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(box_h_kernel<DT_F32>, dim3(bh), dim3(256), 0, s, p);
+  // one 1-D pass over `outer` planes of L x inner elements
+  auto pass = [&](const void* src, int sdt, void* dst, int ddt, int64_t L, int64_t k, int64_t inner, int64_t outer,
+                  double scale) -> bool {
+    BoxPass q{};
+    q.x = src;
+    q.y = dst;
+    q.L = L;
+    q.k = k;
+    q.lo = L - k + 1;
+    q.inner = inner;
+    q.outer = outer;
+    q.y_plane = q.lo * inner;
+    // T threads per line block. A thread reads T partial sums (T x 64 B) in the exchange and
+    // ~4 k / T rows of 16 B: the two balance at T ~ sqrt(k). T is raised so no lane group of a
+    // workgroup is idle (T >= 256 / lane groups in a row), and doubled once more when the GPU
+    // would have fewer than ~128 K threads.
+    const int E = sdt == DT_BF16 ? 8 : 4;
+    const int64_t groups = cdiv(inner, E);
+    const int64_t lines = outer * cdiv(q.lo, k) * groups;
+    int T0 = 1;
+    while ((int64_t)(2 * T0) * (2 * T0) <= k) T0 *= 2;
+    int T = T0;
+    while (T < 256 && T * groups < 256) T *= 2;
+    if (T == T0 && T < 256 && lines * T < 131072) T *= 2;
+    q.T = T;
+    q.R = (int)cdiv(k, T);
+    q.QW = 256 / T;
+    q.nblk = (int)cdiv(q.lo, k);
+    q.nqg = (int)cdiv(cdiv(inner, E), q.QW);
+    q.scale = scale;
+    const int64_t blocks = outer * q.nblk * q.nqg;
+    if (blocks >= ((int64_t)1 << 31)) return false;
+    if (sdt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_BF16, DT_F32>), dim3((unsigned)blocks), dim3(256), 0, s, q);
+    else if (ddt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_BF16>), dim3((unsigned)blocks), dim3(256), 0, s, q);
+    else hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_F32>), dim3((unsigned)blocks), dim3(256), 0, s, q);
+    return true;
+  };
+  // vertical: planes are images, lines the (x, c) columns; horizontal: planes are V rows
+  CLARUS_REQUIRE(pass(x, x_dtype, scratch, DT_F32, h, k1, w * c, n, 1.0), "boxmean: too many workgroups");
+  CLARUS_REQUIRE(pass(scratch, DT_F32, out, o_dtype, w, k2, c, n * oh, 1.0 / ((double)k1 * (double)k2)),
+                 "boxmean: too many workgroups");
   return check_launch("boxmean");
 }
 
