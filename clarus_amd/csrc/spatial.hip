@@ -8,11 +8,13 @@
 // Semantics of the reference backend's dwconv (python/clarus/ops/torch_ref.py:143-155): fp32
 // math, one cast to the output dtype at the end.
 //
+// A workgroup owns a slice of 64 output channels (the taps and bias of its input channels,
+// < 5 KiB, staged in LDS once) and walks pixels 32 at a time, so occupancy does not depend
+// on C (a tap table of all C channels per workgroup left one workgroup per CU at C = 2048).
 // A thread computes 8 consecutive output channels of one pixel: per tap one 16-byte load of
-// each input half (bf16) or two (fp32), fp32 FMAs with the tap weights read from LDS, then
-// the gate and a 16-byte store. Lanes are channel-group-minor, so a wave reads whole pixel
-// rows; the 3x3 neighbourhood is re-read from L1 / L2. The grid is persistent so the tap
-// table ([9][C] fp32, copied as 16-byte vectors) is staged once per block.
+// each input half (bf16) or two (fp32), fp32 FMAs with the tap weights, then the gate and a
+// 16-byte store. The 8 lanes of a pixel read 128 contiguous bytes per input half; the 3x3
+// neighbourhood is re-read from L1 / L2.
 #include <algorithm>
 
 #include "capi.hpp"
@@ -29,39 +31,49 @@ struct DwP {
   int dil, gate, act, x_dt, o_dt;
 };
 
+constexpr int DW_SLICE = 64;  // output channels per workgroup slice (8 lanes of 8 channels)
+
 template <int XDT, int GATE>
 __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
-  extern __shared__ __attribute__((aligned(16))) float wsh[];  // [9][cin] taps, then [cin] bias
-  const int cin = (int)p.cin;
-  {
-    const f32x4* src = reinterpret_cast<const f32x4*>(p.w);  // [9][cin], cin % 8 == 0
-    for (int i = threadIdx.x; i < 9 * cin / 4; i += 256) reinterpret_cast<f32x4*>(wsh)[i] = src[i];
-    for (int i = threadIdx.x; i < cin; i += 256) wsh[9 * cin + i] = p.b ? p.b[i] : 0.f;
+  // taps of the slice's input channels: [9][2][DW_SLICE] fp32 (second half with a gate), bias [2][DW_SLICE]
+  __shared__ __attribute__((aligned(16))) float wsh[10][2][DW_SLICE];
+  const int cin = (int)p.cin, cout = (int)p.cout;
+  const int half = GATE ? cout : 0;  // channel offset of the second input half
+  const int nslices = (cout + DW_SLICE - 1) / DW_SLICE;
+  const int slice = blockIdx.x % nslices;
+  const int cs = slice * DW_SLICE;
+  for (int i = threadIdx.x; i < 10 * 2 * DW_SLICE; i += 256) {
+    const int tap = i / (2 * DW_SLICE), hh = (i / DW_SLICE) & 1, cc = cs + (i % DW_SLICE);
+    const int ci = cc + hh * half;
+    float v = 0.f;
+    if (cc < cout && (GATE || hh == 0)) v = tap < 9 ? p.w[(int64_t)tap * cin + ci] : (p.b ? p.b[ci] : 0.f);
+    wsh[tap][hh][i % DW_SLICE] = v;
   }
   __syncthreads();
 
   constexpr int XES = (XDT == DT_BF16) ? 2 : 4;
-  const int cout = (int)p.cout;
-  const int groups = cout / 8;  // output channel groups of 8
+  const int o = threadIdx.x & 7;                    // channel lane of the slice
+  const int c0 = cs + o * 8;
   const int H = (int)p.h, W = (int)p.w_, hw = H * W;
-  const int total = (int)(p.n * hw) * groups;  // the host checks that this fits 31 bits
-  const int half = GATE ? cout : 0;            // channel offset of the second half
+  const int npix = (int)p.n * hw;                   // the host checks that this fits 31 bits
+  const int pstride = (gridDim.x / nslices) * 32;   // pixels per sweep of the grid
   const unsigned char* X = (const unsigned char*)p.x;
-  for (int t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
-    const int pix = t / groups;
-    const int c0 = (t - pix * groups) * 8;
+  const float* wb = &wsh[0][0][0] + o * 8;          // tap t, half h at wb + (2 t + h) DW_SLICE
+  if (c0 >= cout) return;  // no barrier below
+  for (int pix = (blockIdx.x / nslices) * 32 + (threadIdx.x >> 3); pix < npix; pix += pstride) {
     const int img = pix / hw;
     const int r = pix - img * hw;
     const int y = r / W, x = r - (r / W) * W;
     float a1[8], a2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      a1[i] = wsh[9 * cin + c0 + i];
-      a2[i] = GATE ? wsh[9 * cin + half + c0 + i] : 0.f;
+      a1[i] = wb[18 * DW_SLICE + i];
+      a2[i] = GATE ? wb[19 * DW_SLICE + i] : 0.f;
     }
 #pragma unroll
     for (int ky = 0; ky < 3; ++ky) {
       const int yy = y + (ky - 1) * p.dil;
+      asm volatile("" ::: "memory");  // one tap row of loads in flight at a time: 8 waves per SIMD
       if (yy < 0 || yy >= H) continue;
 #pragma unroll
       for (int kx = 0; kx < 3; ++kx) {
@@ -72,7 +84,7 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
         const f32x8 v1 = load8<XDT>(src);
         f32x8 v2;
         if constexpr (GATE != 0) v2 = load8<XDT>(src + (int64_t)half * XES);
-        const float* wt = wsh + tap * cin + c0;
+        const float* wt = wb + 2 * tap * DW_SLICE;
         const f32x4 w1a = *reinterpret_cast<const f32x4*>(wt), w1b = *reinterpret_cast<const f32x4*>(wt + 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -80,8 +92,8 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
           a1[4 + i] = fmaf(w1b[i], v1.v[4 + i], a1[4 + i]);
         }
         if constexpr (GATE != 0) {
-          const f32x4 w2a = *reinterpret_cast<const f32x4*>(wt + half);
-          const f32x4 w2b = *reinterpret_cast<const f32x4*>(wt + half + 4);
+          const f32x4 w2a = *reinterpret_cast<const f32x4*>(wt + DW_SLICE);
+          const f32x4 w2b = *reinterpret_cast<const f32x4*>(wt + DW_SLICE + 4);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             a2[i] = fmaf(w2a[i], v2.v[i], a2[i]);
@@ -90,24 +102,24 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const DwP p) {
         }
       }
     }
-    float o[8];
+    float out[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if constexpr (GATE == 1) o[i] = a1[i] * a2[i];
-      else if constexpr (GATE == 2) o[i] = gelu_erf(a1[i]) * a2[i];
-      else o[i] = p.act == ACT_GELU ? gelu_erf(a1[i]) : a1[i];
+      if constexpr (GATE == 1) out[i] = a1[i] * a2[i];
+      else if constexpr (GATE == 2) out[i] = gelu_erf(a1[i]) * a2[i];
+      else out[i] = p.act == ACT_GELU ? gelu_erf(a1[i]) : a1[i];
     }
     const int64_t oo = (int64_t)pix * cout + c0;
     if (p.o_dt == DT_BF16) {
       u32x4 q;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        q[i] = (unsigned)f32_to_bf16_bits(o[2 * i]) | ((unsigned)f32_to_bf16_bits(o[2 * i + 1]) << 16);
+        q[i] = (unsigned)f32_to_bf16_bits(out[2 * i]) | ((unsigned)f32_to_bf16_bits(out[2 * i + 1]) << 16);
       *reinterpret_cast<u32x4*>((unsigned short*)p.out + oo) = q;
     } else {
       float* op = (float*)p.out + oo;
-      *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<f32x4*>(op + 4) = f32x4{o[4], o[5], o[6], o[7]};
+      *reinterpret_cast<f32x4*>(op) = f32x4{out[0], out[1], out[2], out[3]};
+      *reinterpret_cast<f32x4*>(op + 4) = f32x4{out[4], out[5], out[6], out[7]};
     }
   }
 }
@@ -329,24 +341,27 @@ extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float*
   CLARUS_REQUIRE((gate == 0 || c % 2 == 0) && cout % 8 == 0, "dwconv3x3: output channels must be a multiple of 8");
   CLARUS_REQUIRE(n * h * wd * (cout / 8) < ((int64_t)1 << 31) && n * h * wd * c < ((int64_t)1 << 40),
                  "dwconv3x3: problem too large for 32-bit pixel indexing");
-  CLARUS_REQUIRE(aligned(x, 16) && aligned(out, 16) && aligned(w, 16), "dwconv3x3: 16-byte alignment");
-  const size_t lds = (size_t)10 * c * sizeof(float);
-  CLARUS_REQUIRE(lds <= 160 * 1024, "dwconv3x3: %lld channels exceed the LDS tap table", (long long)c);
+  CLARUS_REQUIRE(aligned(x, 16) && aligned(out, 16), "dwconv3x3: 16-byte alignment");
   DwP p{x, w, bias, out, n, h, wd, c, cout, dil, gate, act, x_dtype, o_dtype};
-  const int64_t total = n * h * wd * (cout / 8);
-  // persistent grid: as many blocks as fit the LDS tap table (at most 8 per CU on 256 CUs)
-  int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)(lds + 1024);
-  per_cu = per_cu < 1 ? 1 : (per_cu > 8 ? 8 : per_cu);
-  int64_t blocks = cdiv(total, 256);
-  if (blocks > 256 * per_cu) blocks = 256 * per_cu;
+  // workgroups: channel slices x pixel chunks of 32, persistent with every workgroup resident
+  // (a grid-stride loop over more workgroups than fit leaves a tail of late starters)
+  const int64_t nslices = cdiv(cout, DW_SLICE);
+  const int64_t chunks = cdiv(n * h * wd, 32);
   hipStream_t s = (hipStream_t)stream;
-#define DW_LAUNCH(XDT, G)                                                                                  \
-  do {                                                                                                     \
-    static const bool attr = (hipFuncSetAttribute(reinterpret_cast<const void*>(&dwconv3x3_kernel<XDT, G>), \
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024), \
-                              true);                                                                       \
-    (void)attr;                                                                                            \
-    hipLaunchKernelGGL((dwconv3x3_kernel<XDT, G>), dim3((unsigned)blocks), dim3(256), lds, s, p);          \
+#define DW_LAUNCH(XDT, G)                                                                                       \
+  do {                                                                                                          \
+    auto fn = &dwconv3x3_kernel<XDT, G>;                                                                        \
+    static const int per_cu = [&] {                                                                             \
+      int k = 0;                                                                                                \
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, reinterpret_cast<const void*>(fn), 256, 0) !=       \
+              hipSuccess ||                                                                                     \
+          k < 1)                                                                                                \
+        k = 1;                                                                                                  \
+      return k;                                                                                                 \
+    }();                                                                                                        \
+    const int64_t cap = std::max<int64_t>(1, 256LL * per_cu / nslices);                                        \
+    const unsigned blocks = (unsigned)(nslices * std::min<int64_t>(chunks, cap));                               \
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);                                                   \
   } while (0)
   if (x_dtype == DT_BF16) {
     if (gate == 1) DW_LAUNCH(DT_BF16, 1); else if (gate == 2) DW_LAUNCH(DT_BF16, 2); else DW_LAUNCH(DT_BF16, 0);
