@@ -13,6 +13,9 @@ How each function is pinned (tests/test_oracle.py): against float64 brute force 
 shapes (matmul sums, conv windows, space-to-depth / pixel-shuffle index maps, two-pass
 LayerNorm), the reference's own known-answer tests (400*200*64*1e-4 = 512, the gate 65536,
 2^-6, TLC windows), numpy.fft for the patch DFT ops, and closed forms (softmax rows sum to 1,
-Gram symmetry, Parseval). The reference ships no golden-vector files (its tests draw seeded
-torch.randn inputs and compare against torch in the same run), so there are none to load.
+Gram symmetry, Parseval). The reference ships no golden-vector files, so the compositions those
+checks leave open (the NAFNet model adapter's fold / wiring / residual dtypes, and combined
+prologue + epilogue orders of linear, ln_mul_linear, conv3x3 and linear_per_image) are pinned by
+fixtures that the reference itself wrote (tests/golden/make_golden.py): tests/test_golden.py
+requires the oracle to reproduce them bit for bit.
 """

@@ -1,0 +1,163 @@
+"""Write the golden fixtures of tests/golden/ from the reference implementation itself.
+
+Run in the build container only (the reference source is not present on the GPU box, and no
+part of it is copied here: the fixtures hold inputs, weights and outputs, nothing else):
+
+    python tests/golden/make_golden.py [/root/reference]
+
+What it pins, and why an import is needed for it: the closed-form and known-answer checks of
+tests/test_oracle.py pin every single GEMM-family op, but not how the reference *composes* them.
+
+* nafnet_tiny.safetensors: the reference NAFNetLocal model adapter
+  (python/clarus/models/nafnet/__init__.py:60-185: weight fold, TLC windows, residual dtypes,
+  block wiring, pad / crop) running on its PyTorch backend (ops/torch_ref.py) on the CPU, on a
+  tiny network (width 8, enc [1, 1, 1], mid 1, dec [1, 1, 1], train_size 24x40) and a 30x45
+  input that needs padding. Outputs for fp32 and bf16 activations, and the exact seeded state
+  dict the model was built from (written to a temporary checkpoint and loaded by the
+  reference's own load_checkpoint).
+* ops_combined.safetensors: reference TorchOps calls whose epilogue / prologue combinations
+  fix an operation order, in fp32 and bf16: torch_ref.py:103-131 linear with a TLC-map
+  multiply or LN prologue and bias + gate + GELU + scale + residual, :290-302 ln_mul_linear,
+  :178-199 conv3x3 with up2 + act + out_scale + residual, :237-245 linear_per_image with
+  bias + residual.
+
+Inputs are drawn from one torch.Generator seeded per case; the generator is in this file, so the
+fixtures can be rewritten, but the tests read only the stored tensors.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+import tempfile
+
+import torch
+from safetensors.torch import save_file
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+TINY = {"width": 8, "enc": [1, 1, 1], "mid": 1, "dec": [1, 1, 1], "train_size": [1, 3, 24, 40],
+        "res_fp32_level": 2, "h": 30, "w": 45}
+
+
+def _seeded_state_dict(shapes: dict, seed: int) -> dict:
+    """Conv weights / biases U(-1/sqrt(fan_in), 1/sqrt(fan_in)); LayerNorm weight 1 + 0.1 N,
+    bias 0.1 N; beta / gamma 0.2 N (non-zero, so the residual branches matter); the final conv
+    scaled by 0.1 to keep the restored image near the input."""
+    g = torch.Generator().manual_seed(seed)
+    sd = {}
+    for k, shape in shapes.items():
+        if k.endswith(("beta", "gamma")):
+            v = 0.2 * torch.randn(shape, generator=g)
+        elif ".norm" in k:
+            v = (1.0 if k.endswith("weight") else 0.0) + 0.1 * torch.randn(shape, generator=g)
+        else:
+            ws = shapes[k[:-len("bias")] + "weight"] if k.endswith("bias") else shape
+            fan_in = ws[1] * ws[2] * ws[3]
+            v = (torch.rand(shape, generator=g) * 2 - 1) / fan_in ** 0.5
+            if k.startswith("ending."):
+                v = v * 0.1
+        sd[k] = v.float().contiguous()
+    return sd
+
+
+def nafnet_fixture(ref_root: str) -> tuple[dict, dict]:
+    from clarus.models import create_model
+    from clarus.models.nafnet import state_dict_shapes
+    from clarus.ops import Ops
+
+    sd = _seeded_state_dict(state_dict_shapes(TINY["width"], TINY["enc"], TINY["mid"], TINY["dec"]), seed=11)
+    g = torch.Generator().manual_seed(12)
+    x = torch.rand(1, 3, TINY["h"], TINY["w"], generator=g)
+    out = {"input": x}
+    out.update({f"sd.{k}": v for k, v in sd.items()})
+    with tempfile.TemporaryDirectory() as tmp:
+        ckpt = os.path.join(tmp, "tiny.pth")
+        torch.save({"params": sd}, ckpt)
+        cfg = {"name": "nafnet", "checkpoint": ckpt,
+               "network_g": {"type": "NAFNetLocal", "width": TINY["width"], "enc_blk_nums": TINY["enc"],
+                             "middle_blk_num": TINY["mid"], "dec_blk_nums": TINY["dec"],
+                             "train_size": TINY["train_size"]},
+               "options": {"residual_fp32_from_level": TINY["res_fp32_level"]}}
+        for tag, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+            ops = Ops(["torch"], dt, torch.device("cpu"))
+            model = create_model(cfg, ops, torch.device("cpu"), dt)
+            with torch.no_grad():
+                out[f"out_{tag}"] = model.forward(x).float().contiguous()
+            out[f"tlc_{tag}"] = torch.tensor([list(model._tlc_kernel(lv)) for lv in range(len(TINY["enc"]) + 1)])
+    return out, {"tiny": json.dumps(TINY)}
+
+
+def ops_fixture(ref_root: str) -> dict:
+    from clarus.ops.torch_ref import Small, TorchOps
+
+    out = {}
+    for tag, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        r = TorchOps(dt, torch.device("cpu"))
+        g = torch.Generator().manual_seed(21)
+
+        def rnd(*s, scale=1.0):
+            return (torch.randn(*s, generator=g) * scale)
+
+        # linear: TLC-map multiply -> GEMM -> bias -> gate -> GELU -> scale -> residual
+        x = rnd(1, 9, 13, 24).to(dt)
+        sm = Small(rnd(1, 4, 6, 24).to(dt), 2, 3, 9, 13)
+        w = rnd(24, 64, scale=24 ** -0.5).to(dt)
+        b, s = rnd(64, scale=0.1), rnd(32, scale=0.5)
+        res = rnd(1, 9, 13, 32).to(dt)
+        y = r.linear(x, w, b, act="gelu", gate=True, scale=s, residual=res, mul=sm, out_dtype=torch.float32)
+        out.update({f"lin1_{tag}.x": x, f"lin1_{tag}.map": sm.data, f"lin1_{tag}.w": w, f"lin1_{tag}.b": b,
+                    f"lin1_{tag}.s": s, f"lin1_{tag}.res": res, f"lin1_{tag}.y": y})
+        # linear: LN -> GEMM -> bias -> gate -> GELU -> scale -> residual
+        x = rnd(1, 7, 10, 32).to(dt)
+        w = rnd(32, 48, scale=32 ** -0.5).to(dt)
+        b, s = rnd(48, scale=0.1), rnd(24, scale=0.5)
+        res = rnd(1, 7, 10, 24).to(dt)
+        y = r.linear(x, w, b, ln=True, act="gelu", gate=True, scale=s, residual=res, out_dtype=torch.float32)
+        out.update({f"lin3_{tag}.x": x, f"lin3_{tag}.w": w, f"lin3_{tag}.b": b, f"lin3_{tag}.s": s,
+                    f"lin3_{tag}.res": res, f"lin3_{tag}.y": y})
+        # linear: RMS prologue, no gate, scale + residual, activation-dtype output
+        x = rnd(2, 5, 7, 40).to(dt)
+        w = rnd(40, 24, scale=40 ** -0.5).to(dt)
+        b, s = rnd(24, scale=0.1), rnd(24, scale=0.5)
+        res = rnd(2, 5, 7, 24).to(dt)
+        y = r.linear(x, w, b, ln="rms", scale=s, residual=res)
+        out.update({f"lin2_{tag}.x": x, f"lin2_{tag}.w": w, f"lin2_{tag}.b": b, f"lin2_{tag}.s": s,
+                    f"lin2_{tag}.res": res, f"lin2_{tag}.y": y})
+        # ln_mul_linear with a GELU multiplier, bias and residual (eps 1e-5)
+        x, m = rnd(1, 6, 11, 32).to(dt), rnd(1, 6, 11, 32).to(dt)
+        lw, lb = 1 + rnd(32, scale=0.1), rnd(32, scale=0.1)
+        w = rnd(32, 16, scale=32 ** -0.5).to(dt)
+        b, res = rnd(16, scale=0.1), rnd(1, 6, 11, 16).to(dt)
+        y = r.ln_mul_linear(x, lw, lb, m, w, bias=b, m_act="gelu", residual=res, out_dtype=torch.float32)
+        out.update({f"lml_{tag}.x": x, f"lml_{tag}.m": m, f"lml_{tag}.lw": lw, f"lml_{tag}.lb": lb,
+                    f"lml_{tag}.w": w, f"lml_{tag}.b": b, f"lml_{tag}.res": res, f"lml_{tag}.y": y})
+        # conv3x3: nearest x2 input, LeakyReLU, out_scale, residual
+        x = rnd(1, 5, 7, 32).to(dt)
+        w = rnd(16, 32, 3, 3, scale=(9 * 32) ** -0.5).to(dt)
+        b, res = rnd(16, scale=0.1), rnd(1, 10, 14, 16).to(dt)
+        y = r.conv3x3(x, w, b, out_dtype=torch.float32, act="lrelu", residual=res, out_scale=0.2, up2=True)
+        out.update({f"c3_{tag}.x": x, f"c3_{tag}.w": w, f"c3_{tag}.b": b, f"c3_{tag}.res": res,
+                    f"c3_{tag}.y": y})
+        # linear_per_image: per-image weights, bias and residual
+        x = rnd(2, 6, 5, 48).to(dt)
+        w = rnd(2, 48, 48, scale=48 ** -0.5).to(dt)
+        b, res = rnd(48, scale=0.1), rnd(2, 6, 5, 48).to(dt)
+        y = r.linear_per_image(x, w, residual=res, out_dtype=torch.float32, bias=b)
+        out.update({f"lpi_{tag}.x": x, f"lpi_{tag}.w": w, f"lpi_{tag}.b": b, f"lpi_{tag}.res": res,
+                    f"lpi_{tag}.y": y})
+    return {k: v.contiguous() for k, v in out.items()}
+
+
+def main(ref_root: str = "/root/reference") -> None:
+    sys.path.insert(0, os.path.join(ref_root, "python"))
+    torch.manual_seed(0)
+    tensors, meta = nafnet_fixture(ref_root)
+    save_file(tensors, os.path.join(HERE, "nafnet_tiny.safetensors"), metadata=meta)
+    save_file(ops_fixture(ref_root), os.path.join(HERE, "ops_combined.safetensors"))
+    for f in ("nafnet_tiny.safetensors", "ops_combined.safetensors"):
+        print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
+
+
+if __name__ == "__main__":
+    main(*sys.argv[1:])
