@@ -274,9 +274,16 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const bool dma_ok = lds_shape && opm == OPM_BF16 && a->pro == PRO_NONE && a->k % 32 == 0 &&
                       (a->lda * 2) % 16 == 0 &&
                       cdiv(a->m, 128) * cdiv(a->n, 64) < ((int64_t)1 << 31);  // tile index in 31 bits
-  const bool m32_ok = dma_ok && a->k % 64 == 0 && (!run_div || run_div % kGemmM32Run == 0);
+  const bool m32_ok = dma_ok && a->k % 64 == 0 && (!run_div || run_div % kGemmM32Run == 0) &&
+                      epi32_tables_fit(a->n, a->gate != 0);  // bias / scale tables in LDS
   CLARUS_REQUIRE(a->tile != 11 || dma_ok, "gemm: the DMA-pipelined kernel does not take this problem");
   CLARUS_REQUIRE(a->tile != 13 || m32_ok, "gemm: the 32x32 DMA-pipelined kernel does not take this problem");
+  CLARUS_REQUIRE((a->tile != 14 && a->tile != 15) || m32_ok,
+                 "gemm: the big-tile DMA-pipelined kernel does not take this problem");
+  if (a->tile == 14 || a->tile == 15) {
+    launch_gemm_big(p, a->gate != 0, a->tile == 14 ? 2 : 1, (hipStream_t)stream);
+    return check_launch("gemm");
+  }
   if (a->tile == 13 || (m32_ok && a->tile == 0 && (auto_dma || use_lds))) {
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");

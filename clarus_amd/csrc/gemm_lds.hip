@@ -2,6 +2,7 @@
 #include "capi.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_mfma32.hpp"
+#include "gemm_big.hpp"
 #include "gemm_lds.hpp"
 #include "gemm_lds_dispatch.hpp"
 
@@ -75,7 +76,43 @@ void launch_m32(GemmP& p, hipStream_t s) {
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), M32_LDS, s, p);
 }
 
+template <bool GATE, int WP>
+void launch_big(GemmP& p, hipStream_t s) {
+  using C = BigCfg<WP>;
+  auto fn = &gemm_big_kernel<GATE, WP>;
+  static const int per_cu = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), C::NT, C::LDS) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  p.ptiles = cdiv(p.m, C::P);
+  const int64_t tiles = p.ptiles * cdiv(p.n, BIG_R / (GATE ? 2 : 1));
+  int64_t gx = 256LL * per_cu;
+  const int64_t need = cdiv(tiles, 8) * 8;
+  if (gx > need) gx = need;
+  hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(C::NT), C::LDS, s, p);
+}
+
 }  // namespace
+
+int64_t gemm_big_tiles(int64_t m, int64_t n, bool gate, int wp) {
+  return cdiv(m, 128 * wp) * cdiv(n, BIG_R / (gate ? 2 : 1));
+}
+
+void launch_gemm_big(GemmP& p, bool gate, int wp, hipStream_t s) {
+  if (wp == 2) {
+    if (gate) launch_big<true, 2>(p, s);
+    else launch_big<false, 2>(p, s);
+  } else {
+    if (gate) launch_big<true, 1>(p, s);
+    else launch_big<false, 1>(p, s);
+  }
+}
 
 void launch_gemm_m32(GemmP& p, bool gate, hipStream_t s) {
   if (gate) launch_m32<true>(p, s);

@@ -1,7 +1,7 @@
 // Launcher of gemm_lds_kernel (pipelined LDS-tiled GEMM for long-K row operands).
 #pragma once
 
-#include "gemm_kernel.hpp"
+#include "gemm_epi32.hpp"
 
 namespace clarus {
 
@@ -13,8 +13,14 @@ bool launch_gemm_lds(GemmP& p, bool gate, int opm, int ta, bool x2, hipStream_t 
 void launch_gemm_dma(GemmP& p, bool gate, hipStream_t s);
 
 // Launches gemm_mfma32_kernel for p (AM_ROWS, batch 1, bf16 A and W, no prologue, K % 64 == 0,
-// a pixel-shuffle quadrant a multiple of 16 channels).
+// a pixel-shuffle quadrant a multiple of 16 channels, epi32_tables_fit(n, gate)).
 void launch_gemm_m32(GemmP& p, bool gate, hipStream_t s);
+
+// Launches gemm_big_kernel for p (same operands as launch_gemm_m32): 256 W^T rows x 128 * wp
+// pixels per tile, wp in {1, 2}.
+void launch_gemm_big(GemmP& p, bool gate, int wp, hipStream_t s);
+// number of gemm_big_kernel tiles of a problem
+int64_t gemm_big_tiles(int64_t m, int64_t n, bool gate, int wp);
 
 // Launches conv_halo_kernel for p (bf16 x and weights, cin % 32 == 0, row output). Returns
 // false when the resident weights of even a 32-channel tile do not fit in LDS.

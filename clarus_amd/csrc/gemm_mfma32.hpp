@@ -31,11 +31,9 @@
 // group, so every wait is vmcnt(0) (it also covers an epilogue's loads and stores).
 #pragma once
 
-#include "gemm_lds.hpp"
+#include "gemm_epi32.hpp"
 
 namespace clarus {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int M32_P = 128;                        // pixels per tile
 constexpr int M32_R = 128;                        // W^T rows per tile
@@ -47,7 +45,8 @@ constexpr int M32_STAGE = M32_ABYTES + M32_WBYTES;
 constexpr int M32_COPIES = M32_STAGE / 1024 / 4;  // 16-byte copies per lane per stage (8)
 constexpr int M32_RUN = 16;                       // consecutive output channels per lane
 constexpr int M32_STAGES = 2;                     // LDS ring depth
-constexpr int M32_LDS = M32_STAGES * M32_STAGE;   // 64 KiB: two workgroups per CU
+constexpr int M32_RING = M32_STAGES * M32_STAGE;  // 64 KiB
+constexpr int M32_LDS = M32_RING + EPI32_TABLE_FLOATS * 4;  // + epilogue tables: 80 KiB, two workgroups per CU
 
 __device__ __forceinline__ int m32_swz(int row, int unit) { return unit ^ ((row >> 1) & 7); }
 
@@ -88,6 +87,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int t_end = (xcd + 1) * span < T ? (xcd + 1) * span : T;
   const int ntiles = t0 < t_end ? (t_end - t0 + per - 1) / per : 0;
   const int nsteps = ntiles * nch;
+  if (nsteps == 0) return;  // nothing to do (before any LDS or memory traffic)
+
+  // epilogue tables (bias, scale) in LDS (the host checks that they fit)
+  float* tb = reinterpret_cast<float*>(ring + M32_RING);
 
   // copies of one chunk into ring stage st: 32 KiB = 32 x 1 KiB; wave w takes the KiBs w + 4 j
   // (the first 16 are A, the rest W^T). A KiB is 8 rows x 128 B: lane i fills row 8 (KiB % 16)
@@ -168,20 +171,26 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf[buf][rb], af[buf][pb], acc[pb][rb]);
   };
 
-  if (nsteps == 0) return;  // nothing issued
   set_issue_tile();
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nsteps) issue();
+  // the tables' loads overlap the first chunk copies; they are stored after the first wait and
+  // published by the barrier that ends chunk 0
+  float tv[EPI32_TABLE_FLOATS / 256];
+  epi32_table_load<GATE, 256>(p, tid, tv);
   // chunk 0 landed everywhere; the ring's last stage is free
   wait_vmcnt<0>();
   barrier_keep_vm();
   if (STAGES - 1 < nsteps) issue();
+  epi32_table_store<GATE, 256>(p, tb, tid, tv);
   load_frags(0, 0, 0);
   int s = 0;        // global step (chunk) index
   int c_stage = 0;  // ring stage of step s
 
   for (int tl = 0; tl < ntiles; ++tl) {
     // ---- the tile's K loop: one 64-k chunk per step, 4 MFMA steps of 16 k
+    int last_stage = 0;     // ring stage of the tile's last chunk: the epilogue's staging area
+    bool deferred = false;  // the copy that would refill that stage waits for the epilogue
     for (int kc = 0; kc < nch; ++kc, ++s) {
 #pragma unroll
       for (int ks = 0; ks < M32_KC / 16 - 1; ++ks) {
@@ -190,72 +199,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
       // last MFMA step: chunk s + 1 must have landed (this thread's copies, then everyone's);
       // with two stages it is the newest copy group, so the wait is for all. After the barrier
-      // every wave has finished its LDS reads of chunk s, whose stage takes chunk s + 2.
+      // every wave has finished its LDS reads of chunk s, whose stage takes chunk s + 2 (after
+      // the epilogue when chunk s ends a tile).
       const int n_stage = c_stage + 1 == STAGES ? 0 : c_stage + 1;
       if (s + 1 < nsteps) {
         wait_vmcnt<0>();
         barrier_keep_vm();
-        if (s + STAGES < nsteps) issue();
+        if (s + STAGES < nsteps) {
+          if (kc == nch - 1) deferred = true;
+          else issue();
+        }
         load_frags(0, n_stage, 0);
+      } else {
+        barrier_keep_vm();  // the last chunk: every wave is past its reads of this stage
       }
+      last_stage = c_stage;
       products(1);
       c_stage = n_stage;
     }
 
-    // ---- epilogue of the tile: lane l owns pixel l % 32 of each pixel block and channels
-    // 16 (l / 32) + [0, 16) of each run
+    // ---- epilogue of the tile through LDS rows (gemm_epi32.hpp): wave (wp, wn) owns pixels
+    // wp * 64 + [0, 64) and channels wn * 64 (gate: wn * 32) + [0, 64 (32))
     {
       const int t = t0 + tl * per;
       const int pt = t / ntn, nt = t - pt * ntn;
+      float* stg = reinterpret_cast<float*>(ring + last_stage * M32_STAGE + wave * EPI32_STAGE_BYTES);
+      const int64_t c0 = (int64_t)nt * TNO + (GATE ? wn * 32 : wn * 64);
 #pragma unroll
-      for (int ro = 0; ro < (GATE ? 1 : 2); ++ro) {
-        const int64_t run0 = (int64_t)nt * TNO + (GATE ? wn * 32 : wn * 64 + ro * 32) + 16 * hl;
-        const bool full_n = run0 + M32_RUN <= p.n;
-        float b1[M32_RUN], b2[GATE ? M32_RUN : 1], sc[M32_RUN];
-#pragma unroll
-        for (int i = 0; i < M32_RUN; ++i) {
-          const bool ok = run0 + i < p.n;
-          b1[i] = (p.bias && ok) ? p.bias[run0 + i] : 0.f;
-          if constexpr (GATE) b2[i] = (p.bias && ok) ? p.bias[p.n + run0 + i] : 0.f;
-          sc[i] = ((p.scale && ok) ? p.scale[run0 + i] : 1.f) * p.out_scale;
-        }
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-          const int64_t q = (int64_t)pt * M32_P + wp * 64 + pb * 32 + l32;
-          float v[M32_RUN];
-          if constexpr (GATE) {
-#pragma unroll
-            for (int j = 0; j < M32_RUN; ++j) v[j] = (acc[pb][0][j] + b1[j]) * (acc[pb][1][j] + b2[j]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < M32_RUN; ++j) v[j] = acc[pb][ro][j] + b1[j];
-          }
-          if (q >= p.m) continue;
-          if (p.act == ACT_GELU) {
-#pragma unroll
-            for (int i = 0; i < M32_RUN; ++i) v[i] = gelu_erf(v[i]);
-          } else if (p.act == ACT_LRELU) {
-#pragma unroll
-            for (int i = 0; i < M32_RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
-          }
-#pragma unroll
-          for (int i = 0; i < M32_RUN; ++i) v[i] *= sc[i];
-          int64_t oo, rof;
-          if (p.c_mode == CM_SHUFFLE) {
-            const int64_t hwi = (int64_t)p.h * p.w;
-            const int64_t im = q / hwi;
-            const int rr = (int)(q - im * hwi);
-            const int y = rr / p.w, x = rr - (rr / p.w) * p.w;
-            const int64_t cq = p.n >> 2;
-            const int64_t qd = run0 / cq, cc = run0 - qd * cq;
-            oo = ((im * 2 * p.h + 2 * y + (qd >> 1)) * 2 * p.w + 2 * x + (qd & 1)) * cq + cc;
-            rof = oo;
-          } else {
-            oo = q * p.ldc + run0;
-            rof = q * p.ldr + run0;
-          }
-          store_run<M32_RUN>(p, v, oo, rof, run0, full_n);
-        }
+      for (int pb = 0; pb < 2; ++pb)
+        epi32_block<GATE>(p, acc[pb][0], acc[pb][1], (int64_t)pt * M32_P + wp * 64 + pb * 32, c0, stg, tb, lane);
+      if (deferred) {  // every wave is done with its staging rows: refill the stage
+        barrier_keep_vm();
+        issue();
       }
 #pragma unroll
       for (int a = 0; a < 2; ++a)

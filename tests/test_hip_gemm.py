@@ -119,11 +119,12 @@ def test_linear_long_k(k, nout, gate, hip_bf16):
     check(got.cpu(), REF.linear(x, wt, b, gate=gate, act=act, scale=sc, residual=res), f"linear K{k} N{nout} gate={gate}")
 
 
-@pytest.mark.parametrize("tile", [0, 10, 11, 13])
+@pytest.mark.parametrize("tile", [0, 10, 11, 13, 14, 15])
 def test_long_k_kernels_agree(tile, hip_bf16):
     """Through the C ABI, the pipelined LDS tile kernel (10), the DMA-pipelined kernels (11:
-    16x16 MFMAs and 32-k chunks; 13: 32x32 MFMAs and 64-k chunks) and the library's choice (0)
-    on one long-K problem with a gate, against the oracle."""
+    16x16 MFMAs and 32-k chunks; 13: 32x32 MFMAs and 64-k chunks; 14 / 15: 32x32 MFMAs on
+    256-row tiles of 256 / 128 pixels) and the library's choice (0) on one long-K problem with a
+    gate, against the oracle."""
     import ctypes
 
     from clarus_amd import _lib
@@ -144,12 +145,12 @@ def test_long_k_kernels_agree(tile, hip_bf16):
     assert_fp32(out.cpu(), ref, rel=1e-5, what=f"long-K gated GEMM tile {tile}")
 
 
-@pytest.mark.parametrize("gate,k", [(False, 1024), (True, 192), (False, 64), (True, 2048)])
-def test_m32_kernel_epilogues(gate, k, hip_bf16):
-    """Through the C ABI, the 32x32-MFMA DMA-pipelined kernel with bf16 output: ragged pixel
-    count and channel count (a partial lane run), bias + GELU or gate, scale and a bf16 residual;
-    K from one chunk to 32 chunks."""
-    tile = 13
+@pytest.mark.parametrize("tile", [13, 14, 15])
+@pytest.mark.parametrize("gate,k", [(False, 1024), (True, 192), (False, 64), (True, 2048), (True, 128)])
+def test_m32_kernel_epilogues(gate, k, tile, hip_bf16):
+    """Through the C ABI, the 32x32-MFMA DMA-pipelined kernels (13: 128 x 128 tiles; 14 / 15:
+    256-row tiles) with bf16 output: ragged pixel count and channel count (a partial lane run),
+    bias + GELU or gate, scale and a bf16 residual; K from one chunk to 32 chunks."""
     import ctypes
 
     from clarus_amd import _lib
