@@ -61,6 +61,10 @@ def _vec16(t: torch.Tensor, *strides: int) -> bool:
 @register_backend("hip")
 class HipOps(Backend):
     name = "hip"
+    # linear with a prologue (LN / RMS / TLC map) and bf16 weights takes the split-operand path
+    # (one prologue pass writing [hi | lo] bf16 rows, then a plain bf16 GEMM with K' = 2K) from
+    # this K on; shorter rows keep the prologue inside the streaming kernel
+    split_min_k = 128
 
     def __init__(self, dtype, device):
         super().__init__(dtype, device)
@@ -113,6 +117,11 @@ class HipOps(Backend):
     def _wt(self, w: torch.Tensor) -> torch.Tensor:
         """[K, N] weight -> W^T [N, K] (K contiguous), kept in its dtype."""
         return self.cached(w, "wt", lambda t: t.t().contiguous())
+
+    def _wt2(self, w: torch.Tensor) -> torch.Tensor:
+        """[K, N] weight -> [W | W]^T [N, 2K]: the weights of the split-operand GEMM, whose
+        A rows are [hi | lo] (clarus_hip_rows_split)."""
+        return self.cached(w, "wt2", lambda t: torch.cat([t.t(), t.t()], dim=1).contiguous())
 
     def _mats(self, device):
         key = ("dft8", str(device))
@@ -179,10 +188,23 @@ class HipOps(Backend):
         elif sm is not None:
             pro = _lib.PRO_MUL
             geom = (h, wd, sm.shape[1], sm.shape[2], mul.pt, mul.pl)
-        return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=n * h * wd, n=nout, k=k, lda=k, ldc=nout,
-                          bias=self._bias(bias), scale=self._bias(scale), res=residual, ldr=nout, gate=gate,
-                          act=_lib.ACT_GELU if act == "gelu" else 0, pro=pro, small=sm, geom=geom,
-                          ln_eps=float(ln_eps))
+        epi = dict(bias=self._bias(bias), scale=self._bias(scale), res=residual, ldr=nout, gate=gate,
+                   act=_lib.ACT_GELU if act == "gelu" else 0)
+        m = n * h * wd
+        if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0:
+            # split-operand path (the fp32-accurate form of triton_cuda.py:101-108's separate
+            # ln_rows / mul_small passes): prologue rows as [hi | lo], then K' = 2K
+            rows = torch.empty((m, 2 * k), device=x.device, dtype=torch.bfloat16)
+            hh, ww, oh, ow, pt, pl = geom
+            args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
+                                 pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
+                                 s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
+                                 h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
+            _lib.check(self.lib.clarus_hip_rows_split(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
+            return self._gemm("linear", a=rows, wt=self._wt2(w), c=out, m=m, n=nout, k=2 * k, lda=2 * k, ldc=nout,
+                              **epi)
+        return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
+                          small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
 
     def down(self, x, w4d, b, out_dtype=None):
         if tuple(w4d.shape[-2:]) != (2, 2) or not _dense(x, b):

@@ -109,6 +109,19 @@ typedef struct ClarusGemmArgs {
 int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
 
 /*
+ * Prologue pass of the split-operand GEMM path. Applies the prologue of args (pro = LN, RMS
+ * or the TLC map multiply, with its eps / map geometry; a, lda, m, k, a_dtype) to every row in
+ * fp32 and writes out[r] = [hi(0..k) | lo(0..k)], bf16, 2k elements per row, hi = bf16(v),
+ * lo = bf16(v - hi). clarus_hip_gemm on out with k' = 2k and the weights duplicated along k
+ * ([W | W]) then equals the prologue GEMM to within 2^-16 relative per operand element.
+ * batch must be 1 (images folded into m); k a multiple of 8, at most 2048; a and out 16-byte
+ * aligned, out dense [m][2k].
+ * replaces kernels/spatial.py:312 ln_rows and mul_small, the separate prologue passes of
+ * ops/triton_cuda.py:101-108 (which round the prologue's output to the compute dtype instead)
+ */
+int clarus_hip_rows_split(const ClarusGemmArgs* args, void* out, void* stream);
+
+/*
  * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:
  *   y = act(conv3x3(up2 ? nearest_x2(x) : x) + bias) * out_scale (+ residual)
  * x [batch, h, w, cin] with pixel stride ldx (h, w = INPUT size); wt [cout][9 * cin] with
