@@ -232,6 +232,67 @@ def test_linear_mul_prologue(k, hip_bf16):
     assert_fp32(got.cpu(), REF.linear(x, wt, mul=s, scale=sc), rel=1e-5, what=f"linear mul large k{k}")
 
 
+@pytest.mark.parametrize("pro", ["ln", "rms", "mul"])
+@pytest.mark.parametrize("adt", [torch.bfloat16, torch.float32])
+def test_split_operand_path(pro, adt, hip_bf16):
+    """Prologue GEMMs with K >= split_min_k take the split-operand path (clarus_hip_rows_split,
+    then a bf16 GEMM with K' = 2K on [W | W]); shorter thresholds force it, a huge one keeps the
+    prologue in the GEMM kernel. Both against the oracle, with gate + scale + residual and two
+    images (the TLC map is indexed per image)."""
+    from clarus_amd.hip_ops import HipOps
+    g = gen(41)
+    n, h, w, k, c = 2, 11, 19, 256, 72
+    x = (3 + rnd(g, n, h, w, k)).to(adt)
+    wt, b = rnd(g, k, 2 * c, scale=k ** -0.5, dtype=torch.bfloat16), rnd(g, 2 * c)
+    sc, res = rnd(g, c), rnd(g, n, h, w, c, dtype=torch.bfloat16)
+    kw = dict(gate=True, scale=sc, residual=res)
+    if pro == "mul":
+        k1, k2, oh, ow, pt, pl = box_geometry(h, w, 6)
+        s = Small(rnd(g, n, oh, ow, k, dtype=torch.bfloat16), pt, pl, h, w)
+        ref = REF.linear(x, wt, b, mul=s, **kw)
+        kwd = dict(mul=Small(s.data.cuda(), pt, pl, h, w))
+    else:
+        mode = True if pro == "ln" else "rms"
+        ref = REF.linear(x, wt, b, ln=mode, **kw)
+        kwd = dict(ln=mode)
+    saved = HipOps.split_min_k
+    try:
+        for thr in (128, 1 << 30):
+            HipOps.split_min_k = thr
+            got = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), residual=res.cuda(), gate=True,
+                                  out_dtype=torch.float32, **kwd)
+            assert_fp32(got.cpu(), ref, rel=1e-5, what=f"linear {pro} A {adt} split_min_k {thr}")
+    finally:
+        HipOps.split_min_k = saved
+
+
+@pytest.mark.parametrize("k", [128, 200, 1024, 2048])
+def test_rows_split_abi(k, hip_bf16):
+    """Through the C ABI: clarus_hip_rows_split's rows [hi | lo] are bf16 pairs whose sum equals
+    fp64 LayerNorm rows to within the documented 2^-16 of the row scale (the pair itself is exact
+    to 2^-18 relative, the fp32 statistics add ~1e-7), and lo is the residual of hi's rounding."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(42)
+    m = 301
+    x = 7 + 3 * rnd(g, m, k)
+    xd = x.cuda()
+    out = torch.empty(m, 2 * k, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.F32, pro=_lib.PRO_LN, ln_eps=1e-6)
+    _lib.check(lib.clarus_hip_rows_split(ctypes.byref(args), out.data_ptr(),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "rows_split")
+    o = out.cpu().float()
+    hi, lo = o[:, :k], o[:, k:]
+    x64 = x.double()
+    ref = (x64 - x64.mean(1, keepdim=True)) / torch.sqrt(x64.var(1, unbiased=False, keepdim=True) + 1e-6)
+    err = ((hi.double() + lo.double()) - ref).abs().max().item()
+    # hi + lo carries v to 2^-18 relative (two bf16 roundings); the fp32 statistics add ~1e-7
+    assert err <= 2.0 ** -16 * ref.abs().max().item(), f"hi + lo vs fp64 LN rows: {err}"
+    assert (lo.abs() <= hi.abs() * 2.0 ** -8 + 1e-30).all(), "lo is not the residual of a bf16 rounding"
+
+
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
 def test_linear_range(k, nout, gate, hip_bf16):
     """|x| ~ 400, |w| ~ 200, scale 1e-4 -> fp32 (tools/test_ops_contracts.py:76-86): bf16
