@@ -18,7 +18,7 @@
 #include <algorithm>
 
 #include "capi.hpp"
-#include "common.hpp"
+#include "gemm_kernel.hpp"
 
 namespace clarus {
 
@@ -327,6 +327,120 @@ extern "C" int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int
   return check_launch("boxmean");
 }
 
+// Sliding-window variant for dilation 1 and narrow rows. A lane owns 8
+// consecutive channels of ONE input half (with a gate, lanes l and l + 32 hold the two halves of
+// the same output channels) and walks a run of R consecutive pixels along a row: per step it
+// loads one new column of 3 pixels (3 16-byte loads per output instead of 9 per half) and adds
+// it to the up to 3 outputs whose window contains that column, so 3 partial outputs are live.
+// Its 72 tap weights and 8 biases stay in registers for the whole run. SimpleGate / GELU gate
+// combine the halves with a cross-lane exchange (l <-> l ^ 32). The 8 lanes of a pixel read
+// 128 contiguous bytes per half; a wave covers 8 (gate: 4) runs of 64 channels.
+// Per output the taps are summed column by column (kx outer, ky inner) after the bias.
+template <int XDT, int GATE, int R>
+__global__ void __launch_bounds__(256) dw_rows_kernel(const DwP p) {
+  constexpr int XES = (XDT == DT_BF16) ? 2 : 4;
+  constexpr int RPW = GATE ? 4 : 8;  // runs per wave
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hf = GATE ? (lane >> 5) : 0;
+  const int l = GATE ? (lane & 31) : lane;
+  const int cg = l & 7, rw = l >> 3;
+  const int cout = (int)p.cout, cin = (int)p.cin;
+  const int nslices = (cout + DW_SLICE - 1) / DW_SLICE;
+  const int slice = blockIdx.x % nslices;
+  const int c0 = slice * DW_SLICE + cg * 8;      // first output channel of the lane
+  const bool active = c0 < cout;                 // the same for both halves of a pair
+  const int ci = c0 + (GATE ? hf * cout : 0);    // first input channel of the lane's half
+  float wt[9][8], bs[8];
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wt[t][i] = active ? p.w[(int64_t)t * cin + ci + i] : 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bs[i] = (active && p.b) ? p.b[ci + i] : 0.f;
+
+  const int H = (int)p.h, W = (int)p.w_;
+  const int rpr = (W + R - 1) / R;               // runs per image row
+  const int total = (int)p.n * H * rpr;          // the host checks that this fits 31 bits
+  const int per_wg = 4 * RPW;
+  const int stride = (gridDim.x / nslices) * per_wg;
+  const unsigned char* X = (const unsigned char*)p.x;
+  for (int run = (blockIdx.x / nslices) * per_wg + wave * RPW + rw; run < total; run += stride) {
+    const int img = run / (H * rpr);
+    const int rr = run - img * H * rpr;
+    const int y = rr / rpr;
+    const int x0 = (rr - y * rpr) * R;
+    const unsigned char* rowp[3];
+    bool rok[3];
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+      const int yy = y + ky - 1;
+      rok[ky] = active && yy >= 0 && yy < H;
+      rowp[ky] = X + ((int64_t)(img * H + (rok[ky] ? yy : 0)) * W * cin + ci) * XES;
+    }
+    // every load of the run is issued before the first FMA (one memory round trip per run)
+    RawFrag<XDT> raw[R + 2][3];
+#pragma unroll
+    for (int cc = 0; cc < R + 2; ++cc) {
+      const int x = x0 - 1 + cc;
+      const bool xok = x >= 0 && x < W;
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky)
+        raw[cc][ky] = (xok && rok[ky]) ? raw_load<XDT>(rowp[ky] + (int64_t)x * cin * XES) : raw_zero<XDT>();
+    }
+    float acc[3][8];
+#pragma unroll
+    for (int cc = 0; cc < R + 2; ++cc) {  // column x0 - 1 + cc
+      if (cc < R) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[cc % 3][i] = bs[i];
+      }
+      f32x8 col[3];
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky) col[ky] = raw_f32<XDT>(raw[cc][ky]);
+#pragma unroll
+      for (int j = cc - 2; j <= cc; ++j) {  // outputs whose window holds this column (kx = cc - j)
+        if (j < 0 || j >= R) continue;
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[j % 3][i] = fmaf(wt[ky * 3 + cc - j][i], col[ky].v[i], acc[j % 3][i]);
+      }
+      if (cc < 2) continue;
+      // output j = cc - 2 is complete
+      const int j = cc - 2;
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = acc[j % 3][i];
+      if constexpr (GATE != 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float o = __shfl_xor(v[i], 32, 64);  // the other half of the same channel
+          v[i] = GATE == 1 ? v[i] * o : gelu_erf(v[i]) * o;
+        }
+      } else if (p.act == ACT_GELU) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);
+      }
+      const int xo = x0 + j;
+      if (hf != 0 || !active || xo >= W) continue;
+      const int64_t oo = ((int64_t)(img * H + y) * W + xo) * cout + c0;
+      if (p.o_dt == DT_BF16) {
+        u32x4 q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          q[i] = (unsigned)f32_to_bf16_bits(v[2 * i]) | ((unsigned)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+        *reinterpret_cast<u32x4*>((unsigned short*)p.out + oo) = q;
+      } else {
+        float* op = (float*)p.out + oo;
+        *reinterpret_cast<f32x4*>(op) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(op + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      }
+    }
+  }
+}
+
+constexpr int DW_RUN = 4;  // pixels per run of dw_rows_kernel
+
 extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float* w, const float* bias, void* out,
                                     int32_t o_dtype, int64_t n, int64_t h, int64_t wd, int64_t c, int32_t dil,
                                     int32_t gate, int32_t act, void* stream) {
@@ -363,6 +477,37 @@ extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float*
     const unsigned blocks = (unsigned)(nslices * std::min<int64_t>(chunks, cap));                               \
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);                                                   \
   } while (0)
+  // sliding-window kernel for dilation 1 and up to 256 input channels (measured on the NAFNet
+  // 720p levels: 127 vs 151 us at 128 channels, even at 256, slower from 512 channels on, where
+  // the per-pixel kernel's higher occupancy wins): runs of DW_RUN pixels, workgroups of 16
+  // (gate) / 32 runs
+  if (dil == 1 && c <= 256) {
+    const int64_t runs = n * h * cdiv(wd, DW_RUN);
+    CLARUS_REQUIRE(runs < ((int64_t)1 << 31), "dwconv3x3: problem too large for 32-bit run indexing");
+    const int64_t rchunks = cdiv(runs, gate ? 16 : 32);
+#define DW_ROWS(XDT, G)                                                                                         \
+  do {                                                                                                          \
+    auto fn = &dw_rows_kernel<XDT, G, DW_RUN>;                                                                  \
+    static const int per_cu = [&] {                                                                             \
+      int k = 0;                                                                                                \
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, reinterpret_cast<const void*>(fn), 256, 0) !=       \
+              hipSuccess ||                                                                                     \
+          k < 1)                                                                                                \
+        k = 1;                                                                                                  \
+      return k;                                                                                                 \
+    }();                                                                                                        \
+    const int64_t cap = std::max<int64_t>(1, 256LL * per_cu / nslices);                                        \
+    const unsigned blocks = (unsigned)(nslices * std::min<int64_t>(rchunks, cap));                              \
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);                                                   \
+  } while (0)
+    if (x_dtype == DT_BF16) {
+      if (gate == 1) DW_ROWS(DT_BF16, 1); else if (gate == 2) DW_ROWS(DT_BF16, 2); else DW_ROWS(DT_BF16, 0);
+    } else {
+      if (gate == 1) DW_ROWS(DT_F32, 1); else if (gate == 2) DW_ROWS(DT_F32, 2); else DW_ROWS(DT_F32, 0);
+    }
+#undef DW_ROWS
+    return check_launch("dwconv3x3");
+  }
   if (x_dtype == DT_BF16) {
     if (gate == 1) DW_LAUNCH(DT_BF16, 1); else if (gate == 2) DW_LAUNCH(DT_BF16, 2); else DW_LAUNCH(DT_BF16, 0);
   } else {

@@ -188,15 +188,16 @@ def test_config5_upconv(h, w, hip_bf16):
 
 
 # ------------------------------------------------------------------ depthwise 3x3 (next op on the NAFNet path)
+@pytest.mark.parametrize("c", [96, 528])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("gate,act,dil", [(True, None, 1), ("gelu", None, 1), (False, None, 1),
                                           (False, "gelu", 1), (False, None, 2)])
-def test_dwconv(dt, gate, act, dil, hip_bf16, hip_f32):
+def test_dwconv(dt, gate, act, dil, c, hip_bf16, hip_f32):
     """Depthwise 3x3 + SimpleGate / GELU gate / GELU / dilation 2 (tools/test_kernels.py:110-121,
-    193-199), odd sizes."""
+    193-199), odd sizes; 96 channels take the sliding-window kernel (dilation 1), 528 the
+    per-pixel one."""
     hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
     g = gen(8)
-    c = 96
     x, w, b = rnd(g, 2, 37, 53, c, dtype=dt), rnd(g, c, 1, 3, 3), rnd(g, c)
     got = hip.dwconv(x.cuda(), w.cuda(), b.cuda(), dil=dil, gate=gate, act=act)
     ref = TorchRef(torch.float32, "cpu").dwconv(x, w, b, dil=dil, gate=gate, act=act)
