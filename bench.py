@@ -24,6 +24,7 @@ Extra fields of the JSON line:
 
   python bench.py --summarize-trace DIR   per-(kernel, grid) durations from a rocprofv3
                                           kernel trace written under DIR
+  python bench.py --summarize-e2e DIR     the same for the NAFNet forwards only, per forward
 
 HBM traffic of the step's kernels (roofline.traffic), from two rocprofv3 counter passes of
 `python bench.py --pmc-pass` (FETCH_SIZE, then WRITE_SIZE): that mode ends with one plain copy
@@ -73,6 +74,35 @@ def summarize_trace(directory: str) -> None:
         short = name if len(name) < 110 else name[:107] + "..."
         print(f"{len(d):6d} {statistics.mean(d):9.2f} {statistics.median(d):9.2f} {sum(d) / 1e3:9.3f}  "
               f"{'x'.join(g for g in grid if g)}  {short}")
+
+
+def summarize_e2e(directory: str, top: int = 40) -> None:
+    """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: launches from
+    the first intro_kernel (the NAFNet stem) on, grouped by (kernel, grid), divided by the number
+    of forwards in the trace (one intro_kernel each)."""
+    files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {directory}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    first = next((i for i, r in enumerate(rows) if "intro_kernel" in r.get("Kernel_Name", "")), None)
+    if first is None:
+        raise SystemExit("no NAFNet forward (intro_kernel) in the trace")
+    e2e = rows[first:]
+    nfwd = sum(1 for r in e2e if "intro_kernel" in r.get("Kernel_Name", ""))
+    groups: dict = {}
+    for r in e2e:
+        name = r.get("Kernel_Name", "?").split("(")[0].replace("void ", "")
+        grid = r.get("Grid_Size_X") or r.get("Grid_Size", "?")
+        groups.setdefault((name, grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    total = sum(sum(v) for v in groups.values()) / nfwd
+    print(f"forwards {nfwd}, launches per forward {len(e2e) / nfwd:.0f}, kernel time per forward {total:.0f} us")
+    print(f"{'us/fwd':>8} {'calls':>6} {'mean_us':>8}  grid  kernel")
+    for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        print(f"{sum(d) / nfwd:8.1f} {len(d) / nfwd:6.1f} {statistics.mean(d):8.2f}  {grid}  {name[:100]}")
 
 
 COPY_BYTES = 256 * 1024 * 1024  # the pmc pass's calibration copy: this many bytes read and written
@@ -176,11 +206,15 @@ def main() -> None:
     ap.add_argument("--no-ops", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--summarize-trace", default=None)
+    ap.add_argument("--summarize-e2e", default=None, help="per-forward kernel breakdown of the NAFNet e2e phase")
     ap.add_argument("--pmc-pass", action="store_true", help="one copy + each step op once (counter runs)")
     ap.add_argument("--summarize-pmc", nargs=2, default=None, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_e2e:
+        summarize_e2e(args.summarize_e2e)
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
@@ -285,7 +319,7 @@ def main() -> None:
             t = json.load(fh)
         traffic = t.get("ops", {}).get(dc.name, {}).get("bytes_per_launch")
     roofline = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": unit, "frac": round(ach / peak, 3),
-                "traffic": traffic, "kernel": f"gemm_kernel ({dc.name})", "avg_us": round(dus, 2),
+                "traffic": traffic, "op": dc.name, "avg_us": round(dus, 2),
                 "algorithmic_bytes": int(dc.nbytes), "algorithmic_flops": int(dc.flops)}
 
     # ------------------------------------------------------------ other configs, cold per op
