@@ -118,6 +118,13 @@ __device__ __forceinline__ void barrier_keep_vm() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// vmcnt(N) (expcnt / lgkmcnt untouched): the count's low 4 bits in [3:0], high 2 bits in [15:14]
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 // exact-erf GELU (torch.nn.functional.gelu default)
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));

@@ -54,13 +54,6 @@ __device__ __forceinline__ f32x16 mfma32_bf16(const bf16x8& a, const bf16x8& b, 
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// vmcnt(N) (expcnt / lgkmcnt untouched): the count's low 4 bits in [3:0], high 2 bits in [15:14]
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 
 // two workgroups per CU: registers capped at 256 per lane
 template <bool GATE>

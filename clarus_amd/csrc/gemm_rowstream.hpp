@@ -1,0 +1,336 @@
+// Streaming fused GEMM with an LDS ring per wave (NHWC rows, short K, no prologue), gfx950.
+//
+// Same math, MFMA mapping and epilogue as gemm_stream_kernel (D[channel][pixel] = W^T . A^T on
+// 16x16 MFMAs, a lane holds 4 * NB consecutive output channels of one pixel, all of W^T for the
+// workgroup's channel tile resident in LDS). What changes is how A reaches the MFMAs:
+//   * gemm_stream_kernel keeps the next 16-pixel block in registers, one block per wave in
+//     flight. With 160-250 VGPRs it runs 2-3 waves per SIMD, so a CU holds 16-24 KiB of A in
+//     flight: at HBM latency that caps the stream near 4 TB/s (measured: c64 expand 4.3 TB/s,
+//     c128 expand 2.9 TB/s);
+//   * here every wave owns a ring of RS_DEPTH (2-4, what fits in LDS next to W^T) blocks,
+//     filled by direct global -> LDS copies (16 bytes per lane), so RS_DEPTH - 1 blocks are in
+//     flight without costing registers. The residual block travels in the same ring. Waits are
+//     per-wave vmcnt counts (the copies complete in issue order; stores only add to the count):
+//     at block b the copies of blocks b + 1 .. b + RS_DEPTH - 2 may stay in flight. No
+//     workgroup barrier after W is staged.
+// Ring slot of a block: 16 pixel rows of RB bytes (A, K padded to 32 * KS elements) followed by
+// 16 rows of residual. Row r stores its 16-byte unit u at slot u ^ f(r), f(r) = (r / (256 /
+// RB)) % U (U units per row): the 16 lanes reading one unit of 16 consecutive rows hit 16
+// distinct 16-byte bank groups. Units past K (and rows past M) are copied from clamped
+// addresses and masked when read.
+#pragma once
+
+#include "gemm_stream.hpp"
+
+namespace clarus {
+
+constexpr int RS_MAX_DEPTH = 4;  // ring blocks per wave, at most
+
+template <int KS, int TA>
+struct RsA {
+  static constexpr int ES = TA == DT_BF16 ? 2 : 4;
+  static constexpr int RB = KS * 32 * ES;       // bytes per A row in the ring
+  static constexpr int U = RB / 16;             // 16-byte units per row
+  static constexpr int RPB = RB >= 256 ? 1 : 256 / RB;  // rows per 256-byte bank row
+  static constexpr int BYTES = 16 * RB;         // one block of A
+};
+
+// residual bytes per block row: the workgroup's TN channels
+template <int NB, int RDT>
+struct RsR {
+  static constexpr int ES = RDT == DT_BF16 ? 2 : 4;
+  static constexpr int RB = NB * 16 * ES;
+  static constexpr int U = RB / 16;
+  static constexpr int RPB = RB >= 256 ? 1 : 256 / RB;
+  static constexpr int BYTES = 16 * RB;
+};
+
+template <int U, int RPB>
+__device__ __forceinline__ int rs_slot(int row, int unit) { return unit ^ ((row / RPB) & (U - 1)); }
+
+__host__ __device__ constexpr int rowstream_slot_bytes(int nb, int ks, int ta, int rdt, bool res) {
+  return 16 * ks * 32 * (ta == DT_BF16 ? 2 : 4) + (res ? 16 * nb * 16 * (rdt == DT_BF16 ? 2 : 4) : 0);
+}
+// ring depth (4 waves per workgroup): the deepest ring that still lets two workgroups share a
+// CU (80 KiB each; one workgroup of 4 waves per CU measured slower than two with a shallower
+// ring), else what fits in 160 KiB; below 2 the shape has no kernel
+__host__ __device__ constexpr int rowstream_depth(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res) {
+  const int slot4 = 4 * rowstream_slot_bytes(nb, ks, ta, rdt, res);
+  const int w = stream_lds_bytes(nb, gate, ks, opm);
+  const int d2 = (80 * 1024 - w) / slot4;
+  const int d = d2 >= 2 ? d2 : (160 * 1024 - w) / slot4;
+  return d > RS_MAX_DEPTH ? RS_MAX_DEPTH : d;
+}
+__host__ __device__ constexpr int rowstream_lds_bytes(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res) {
+  return stream_lds_bytes(nb, gate, ks, opm) +
+         4 * rowstream_depth(nb, gate, ks, opm, ta, rdt, res) * rowstream_slot_bytes(nb, ks, ta, rdt, res);
+}
+
+// RDT: residual dtype (ignored when RES is false)
+template <int NB, bool GATE, int OPM, int TA, int KS, bool RES, int RDT>
+__global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
+  constexpr int G = GATE ? 2 : 1;
+  constexpr int TN = NB * 16;
+  constexpr int RUN = 4 * NB;
+  constexpr int WES = stream_wes(OPM);
+  constexpr int ROWE = stream_wrow_elems(KS, OPM);
+  constexpr int ROWB = ROWE * WES;
+  constexpr int WB = G * TN * ROWB;
+  using AL = RsA<KS, TA>;
+  using RL = RsR<NB, RDT>;
+  constexpr int SLOT = AL::BYTES + (RES ? RL::BYTES : 0);
+  constexpr int CA = AL::BYTES / 1024;          // A copies per lane per block
+  constexpr int CR = RES ? RL::BYTES / 1024 : 0;  // residual copies per lane per block
+  static_assert(AL::BYTES % 1024 == 0 && (!RES || RL::BYTES % 1024 == 0), "blocks are whole copy instructions");
+  constexpr int C = CA + CR;                    // copy instructions per block
+  constexpr int RS_DEPTH = rowstream_depth(NB, GATE, KS, OPM, TA, RDT, RES);
+  static_assert(RS_DEPTH >= 2 && RS_DEPTH <= 4, "ring depth");
+  static_assert(2 * C < 64, "vmcnt range");
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  float* epi = reinterpret_cast<float*>(lds);
+  unsigned char* wlds = lds + gemm_epi_bytes(NB);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.y * TN;
+  const int64_t bz = blockIdx.z;
+  const int64_t run0 = n0 + lg * RUN;
+  const int64_t K = p.k;
+  const unsigned char* A = (const unsigned char*)p.a + bz * p.a_bs * AL::ES;
+  const unsigned char* Wt = (const unsigned char*)p.wt + bz * p.w_bs * WES;
+  unsigned char* ring = wlds + WB + wave * (RS_DEPTH * SLOT);
+
+  // ---- epilogue vectors and W^T rows (all of K) -> LDS, once (as gemm_stream_kernel)
+  for (int i = tid; i < (G + 1) * TN; i += 256) {
+    const int part = i / TN;
+    const int64_t c = n0 + (i - part * TN);
+    float v;
+    if (part < G) v = (p.bias && c < p.n) ? p.bias[part * p.n + c] : 0.f;
+    else v = ((p.scale && c < p.n) ? p.scale[c] : 1.f) * p.out_scale;
+    epi[i] = v;
+  }
+  for (int base = wave * 1024; base < WB; base += 4 * 1024) {
+    const int pos = base + lane * 16;
+    if (pos < WB) {
+      const int r = pos / ROWB;
+      int cb = pos - r * ROWB;
+      if (cb >= KS * 32 * WES) cb = 0;
+      const int half = r / TN;
+      const int rr = r - half * TN;
+      int64_t ch = n0 + ((rr & 15) >> 2) * RUN + (rr >> 4) * 4 + (rr & 3);
+      if (ch > p.n - 1) ch = p.n - 1;
+      int64_t kk = cb / WES;
+      if (kk > K - 16 / WES) kk = K - 16 / WES;
+      const unsigned char* src = Wt + ((half * p.n + ch) * K + kk) * WES;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(wlds + base), 16, 0, 0);
+    }
+  }
+  wait_vmem_all();
+  __syncthreads();
+
+  const bool lane_full = run0 + RUN <= p.n;
+  const int64_t nblk = cdiv(p.m, 16);
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t nmine = wid < nblk ? (nblk - 1 - wid) / stride + 1 : 0;  // blocks of this wave
+  const int ua_valid = (int)(K * AL::ES / 16);  // A units per row that hold k < K
+
+  auto out_offsets = [&](int64_t q, int64_t& oo, int64_t& ro) __attribute__((always_inline)) {
+    oo = bz * p.c_bs + q * p.ldc + run0;
+    ro = bz * p.r_bs + q * p.ldr + run0;
+  };
+  const bool fast = lane_full && p.vec_out && (!RES || p.vec_res);
+
+  // copies of block j (the wave's j-th block) into ring slot j % RS_DEPTH: copy instruction c
+  // covers 64 / U rows of the block, lane i row (64 c + i) / U, slot (64 c + i) % U
+  auto issue = [&](int64_t j) __attribute__((always_inline)) {
+    const int64_t blk = wid + j * stride;
+    unsigned char* slot = ring + (int)(j % RS_DEPTH) * SLOT;
+#pragma unroll
+    for (int c = 0; c < CA; ++c) {
+      const int idx = c * 64 + lane;
+      const int row = idx / AL::U, s = idx - row * AL::U;
+      int u = rs_slot<AL::U, AL::RPB>(row, s);
+      if (u > ua_valid - 1) u = ua_valid - 1;  // past K: any valid unit (masked when read)
+      int64_t q = blk * 16 + row;
+      if (q > p.m - 1) q = p.m - 1;            // past M: any valid row (not stored)
+      const unsigned char* src = A + (q * p.lda) * AL::ES + u * 16;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(slot + c * 1024), 16, 0, 0);
+    }
+    if constexpr (RES) {
+      unsigned char* rslot = slot + AL::BYTES;
+#pragma unroll
+      for (int c = 0; c < CR; ++c) {
+        const int idx = c * 64 + lane;
+        const int row = idx / RL::U, s = idx - row * RL::U;
+        const int u = rs_slot<RL::U, RL::RPB>(row, s);
+        int64_t q = blk * 16 + row;
+        if (q > p.m - 1) q = p.m - 1;
+        int64_t ch = n0 + u * (16 / RL::ES);
+        if (ch > p.n - 16 / RL::ES) ch = p.n - 16 / RL::ES;  // channels past N: not stored
+        const unsigned char* src = (const unsigned char*)p.res + (bz * p.r_bs + q * p.ldr + ch) * RL::ES;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(rslot + c * 1024), 16, 0, 0);
+      }
+    }
+  };
+
+  auto compute_block = [&](int64_t j) __attribute__((always_inline)) {
+    const int64_t blk = wid + j * stride;
+    const unsigned char* slot = ring + (int)(j % RS_DEPTH) * SLOT;
+    const int64_t q = blk * 16 + lc;
+    f32x4 acc[NB], acc2[GATE ? NB : 1];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (GATE) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int64_t k = ks * 32 + lg * 8;
+      const bool kok = k < K;
+      // this lane's 8 consecutive k of pixel lc, from the ring
+      RawFrag<TA> raw;
+      if constexpr (TA == DT_BF16) {
+        const int u = (int)(k / 8);
+        raw.q = kok ? *reinterpret_cast<const u32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
+                    : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        const int u = (int)(k / 4);
+        raw.a = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+        raw.b = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u + 1) * 16)
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      bf16x8 hi, lo;
+      f32x8 a;
+      if constexpr (OPM == OPM_BF16) {
+        hi = __builtin_bit_cast(bf16x8, raw.q);
+      } else {
+        a = raw_f32<TA>(raw);
+        if constexpr (OPM == OPM_SPLIT) split_bf16(a, hi, lo);
+      }
+#pragma unroll
+      for (int jb = 0; jb < NB; ++jb) {
+#pragma unroll
+        for (int hf = 0; hf < G; ++hf) {
+          const unsigned char* wp = wlds + (size_t)(hf * TN + jb * 16 + lc) * ROWB + (ks * 32 + lg * 8) * WES;
+          f32x4 t = hf ? acc2[GATE ? jb : 0] : acc[jb];
+          if constexpr (OPM == OPM_F32) {
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(wp);
+            const f32x4 w1 = *reinterpret_cast<const f32x4*>(wp + 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = mfma_f32(w0[i], a.v[i], t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = mfma_f32(w1[i], a.v[4 + i], t);
+          } else {
+            const bf16x8 wv = *reinterpret_cast<const bf16x8*>(wp);
+            t = mfma_bf16(wv, hi, t);
+            if constexpr (OPM == OPM_SPLIT) t = mfma_bf16(wv, lo, t);
+          }
+          if (hf) acc2[GATE ? jb : 0] = t; else acc[jb] = t;
+        }
+      }
+    }
+    if (q >= p.m) return;
+    float v[RUN];
+    const int e0 = lg * RUN;
+#pragma unroll
+    for (int jb = 0; jb < NB; ++jb) {
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(epi + e0 + jb * 4);
+      f32x4 b2 = b1;
+      if constexpr (GATE) b2 = *reinterpret_cast<const f32x4*>(epi + TN + e0 + jb * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = acc[jb][i] + b1[i];
+        if constexpr (GATE) x = x * (acc2[jb][i] + b2[i]);
+        v[jb * 4 + i] = x;
+      }
+    }
+    if (p.act == ACT_GELU) {
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) v[i] = gelu_erf(v[i]);
+    } else if (p.act == ACT_LRELU) {
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
+    }
+#pragma unroll
+    for (int jb = 0; jb < NB; ++jb) {
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(epi + G * TN + e0 + jb * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[jb * 4 + i] *= sc[i];
+    }
+    int64_t oo, ro;
+    out_offsets(q, oo, ro);
+    if (fast) {
+      if constexpr (RES) {  // the lane's RUN residual channels from the ring
+        const unsigned char* rrow = slot + AL::BYTES + lc * RL::RB;
+        constexpr int PER = 16 / RL::ES;  // channels per unit
+#pragma unroll
+        for (int u0 = 0; u0 < RUN / PER; ++u0) {
+          const int u = (lg * RUN) / PER + u0;
+          const u32x4 r = *reinterpret_cast<const u32x4*>(rrow + rs_slot<RL::U, RL::RPB>(lc, u) * 16);
+          if constexpr (RDT == DT_BF16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              v[u0 * 8 + 2 * i] += __uint_as_float(r[i] << 16);
+              v[u0 * 8 + 2 * i + 1] += __uint_as_float(r[i] & 0xffff0000u);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[u0 * 4 + i] += __uint_as_float(r[i]);
+          }
+        }
+      }
+      if (p.c_dt == DT_BF16) {
+        unsigned short* op = (unsigned short*)p.c + oo;
+#pragma unroll
+        for (int jj = 0; jj < RUN / 8; ++jj) {
+          u32x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            o[i] = (unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i]) | ((unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i + 1]) << 16);
+          if (p.vec_out == 2) {
+            *reinterpret_cast<u32x4*>(op + 8 * jj) = o;
+          } else {
+            *reinterpret_cast<u32x2*>(op + 8 * jj) = u32x2{o[0], o[1]};
+            *reinterpret_cast<u32x2*>(op + 8 * jj + 4) = u32x2{o[2], o[3]};
+          }
+        }
+      } else {
+        float* op = (float*)p.c + oo;
+#pragma unroll
+        for (int jj = 0; jj < RUN / 4; ++jj)
+          *reinterpret_cast<f32x4*>(op + 4 * jj) = f32x4{v[4 * jj], v[4 * jj + 1], v[4 * jj + 2], v[4 * jj + 3]};
+      }
+    } else {  // partial channel tile / unaligned output: element-wise
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) {
+        if (run0 + i >= p.n) continue;
+        float x = v[i];
+        if constexpr (RES) x += load1(p.res, p.r_dt, ro + i);
+        store1(p.c, p.c_dt, oo + i, x);
+      }
+    }
+  };
+
+  // ---- the ring: blocks 0 .. RS_DEPTH - 2 in flight before the first one is computed
+  int64_t issued = 0;
+  for (; issued < RS_DEPTH - 1 && issued < nmine; ++issued) issue(issued);
+  for (int64_t j = 0; j < nmine; ++j) {
+    // block j landed: the copies of the blocks issued after it may stay in flight (stores of
+    // earlier blocks complete before them in issue order, so they are covered as well)
+    const int64_t newer = issued - 1 - j;  // copy groups issued after block j's
+    if (newer >= 2) wait_vmcnt<2 * C>();
+    else if (newer == 1) wait_vmcnt<C>();
+    else wait_vmem_all();
+    // the wave's LDS reads of block j's slot come after the wait (the ring is per wave)
+    asm volatile("" ::: "memory");
+    if (issued < nmine) { issue(issued); ++issued; }
+    compute_block(j);
+  }
+}
+
+}  // namespace clarus

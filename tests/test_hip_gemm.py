@@ -174,6 +174,56 @@ def test_m32_kernel_epilogues(gate, k, tile, hip_bf16):
     check(out.cpu(), ref, f"32x32 DMA GEMM tile {tile} gate={gate} K{k}")
 
 
+@pytest.mark.parametrize("adt,wdt,gate,rdt,k,nout,batch", [
+    (torch.bfloat16, torch.bfloat16, True, None, 64, 64, 1),
+    (torch.bfloat16, torch.bfloat16, True, None, 128, 72, 1),
+    (torch.bfloat16, torch.bfloat16, False, torch.bfloat16, 64, 64, 1),
+    (torch.bfloat16, torch.bfloat16, False, torch.float32, 32, 200, 1),
+    (torch.bfloat16, torch.bfloat16, False, None, 48, 48, 3),
+    (torch.float32, torch.bfloat16, True, None, 64, 40, 1),
+    (torch.float32, torch.float32, True, None, 32, 32, 1),
+    (torch.float32, torch.float32, False, torch.float32, 32, 32, 1),
+    (torch.float32, torch.float32, False, None, 48, 48, 2),
+    (torch.float32, torch.float32, False, torch.float32, 24, 96, 1),
+])
+def test_ring_streaming_kernel(adt, wdt, gate, rdt, k, nout, batch, hip_bf16):
+    """Through the C ABI, the streaming kernel with an LDS ring per wave (tile 16): bf16 / fp32 A
+    and weights, gate, bf16 / fp32 residual, K from 24 to 128, channel tails, and batched
+    problems addressed like attn . V (heads as the batch, A a channel slice of a wider row); a
+    ragged pixel count so the last ring blocks are partial."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(43)
+    m = 3001
+    nw = 2 * nout if gate else nout
+    lda = batch * k + 16  # channel slices of a wider row
+    xa = rnd(g, m, lda, dtype=adt)
+    wts = [rnd(g, nw, k, scale=k ** -0.5, dtype=wdt) for _ in range(batch)]  # W^T per batch entry
+    b, sc = rnd(g, nw), rnd(g, nout)
+    res = rnd(g, m, batch * nout, dtype=rdt) if rdt is not None else None
+    refs = []
+    for e in range(batch):
+        x = xa[:, e * k:(e + 1) * k].contiguous()
+        r = res[:, e * nout:(e + 1) * nout].contiguous() if res is not None else None
+        refs.append(REF.linear(x, wts[e].t().contiguous(), b, gate=gate, scale=sc, residual=r))
+    ref = torch.cat(refs, dim=1)
+    xd, bd, sd = xa.cuda(), b.cuda(), sc.cuda()
+    wd = torch.stack(wts).cuda()
+    rd = res.cuda() if res is not None else None
+    out = torch.empty(m, batch * nout, device="cuda")
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=wd.data_ptr(), c=out.data_ptr(), bias=bd.data_ptr(),
+                         scale=sd.data_ptr(), res=_lib.ptr(rd), m=m, n=nout, k=k, batch=batch, lda=lda,
+                         ldc=batch * nout, ldr=batch * nout, a_bstride=k, w_bstride=nw * k, c_bstride=nout,
+                         r_bstride=nout, a_dtype=_lib.dtype_code(adt), w_dtype=_lib.dtype_code(wdt),
+                         c_dtype=_lib.F32, r_dtype=_lib.dtype_code(rdt) if rdt is not None else 0,
+                         gate=int(gate), out_scale=1.0, tile=16)
+    _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "gemm")
+    assert_fp32(out.cpu(), ref, rel=1e-5, what=f"ring streaming A {adt} W {wdt} gate {gate} res {rdt} K{k} N{nout}")
+
+
 def test_up_long_k(hip_bf16):
     """1x1 conv + PixelShuffle(2) with K = 256 (the DMA-pipelined kernels' store addressing)."""
     g = gen(36)
