@@ -237,21 +237,22 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
   int tile_override = 0;
   if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && !run_div) tile_override = 3;
-  // streaming kernel with an LDS ring per wave: rows without prologue or pixel shuffle, K <= 128
-  // (bf16 A) / 64 (fp32 A); a residual needs 16-byte rows and whole 16-byte channel units, and
-  // no gate. Automatic for K <= 64 and for K <= 128 without a gate (measured against the
+  // streaming kernel with an LDS ring per wave: rows without prologue, row or pixel-shuffle
+  // output (a lane's channel run inside one quadrant), K <= 128 (bf16 A) / 64 (fp32 A); a
+  // residual needs 16-byte rows and whole 16-byte channel units, and no gate. Automatic for K <= 64 and for K <= 128 without a gate (measured against the
   // register-prefetch streaming kernel and the 64 x 64 tiled kernel on the NAFNet, config-1 and
   // attn . V shapes: faster or equal except a gated K = 128); tile 16 forces it.
   {
     const int ks = rowstream_ks_for(a->k, a->a_dtype);
     const int er = a->res ? esize(a->r_dtype) : 2;
     const bool res_ok = !a->res || (p.vec_res == 2 && a->n % (16 / er) == 0 && !a->gate);
-    const bool ring_ok = a->a_mode == CLARUS_A_ROWS && a->pro == PRO_NONE && a->c_mode == CLARUS_C_ROWS && ks &&
-                         res_ok && (opm != OPM_SPLIT || a->a_dtype == DT_F32);
+    const int nb = (a->n <= 64 || a->gate) ? 4 : (run_div && run_div % 32 ? 4 : 8);
+    const bool ring_ok = a->a_mode == CLARUS_A_ROWS && a->pro == PRO_NONE && ks && res_ok &&
+                         (opm != OPM_SPLIT || a->a_dtype == DT_F32) &&
+                         (!run_div || (run_div % (4 * nb) == 0 && a->batch == 1));
     CLARUS_REQUIRE(a->tile != 16 || ring_ok, "gemm: the ring streaming kernel does not take this problem");
     const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || !a->gate);
     if (a->tile == 16 || ring_auto) {
-      const int nb = (a->n <= 64 || a->gate) ? 4 : 8;
       GemmP q = p;
       q.ptiles = 0;
       if (launch_gemm_rowstream(q, nb, a->gate != 0, opm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,

@@ -1,4 +1,5 @@
-// Streaming fused GEMM with an LDS ring per wave (NHWC rows, short K, no prologue), gfx950.
+// Streaming fused GEMM with an LDS ring per wave (NHWC rows, short K, no prologue; row or
+// pixel-shuffle output), gfx950.
 //
 // Same math, MFMA mapping and epilogue as gemm_stream_kernel (D[channel][pixel] = W^T . A^T on
 // 16x16 MFMAs, a lane holds 4 * NB consecutive output channels of one pixel, all of W^T for the
@@ -136,9 +137,25 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   const int64_t nmine = wid < nblk ? (nblk - 1 - wid) / stride + 1 : 0;  // blocks of this wave
   const int ua_valid = (int)(K * AL::ES / 16);  // A units per row that hold k < K
 
+  // element offset of (pixel q, channel c of the N space) in the output, which the residual
+  // shares under the pixel shuffle (N = (dy, dx, c'), output [*, 2h, 2w, N / 4])
+  auto shuffled = [&](int64_t q, int64_t c) __attribute__((always_inline)) -> int64_t {
+    const int64_t hwi = (int64_t)p.h * p.w;
+    const int64_t im = q / hwi;
+    const int rr = (int)(q - im * hwi);
+    const int y = rr / p.w, x = rr - (rr / p.w) * p.w;
+    const int64_t cq = p.n >> 2;
+    const int64_t qd = c / cq, cc = c - qd * cq;
+    return ((im * 2 * p.h + 2 * y + (qd >> 1)) * 2 * p.w + 2 * x + (qd & 1)) * cq + cc;
+  };
   auto out_offsets = [&](int64_t q, int64_t& oo, int64_t& ro) __attribute__((always_inline)) {
-    oo = bz * p.c_bs + q * p.ldc + run0;
-    ro = bz * p.r_bs + q * p.ldr + run0;
+    if (p.c_mode == CM_SHUFFLE) {
+      oo = shuffled(q, run0);
+      ro = oo;
+    } else {
+      oo = bz * p.c_bs + q * p.ldc + run0;
+      ro = bz * p.r_bs + q * p.ldr + run0;
+    }
   };
   const bool fast = lane_full && p.vec_out && (!RES || p.vec_res);
 
@@ -170,7 +187,8 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
         if (q > p.m - 1) q = p.m - 1;
         int64_t ch = n0 + u * (16 / RL::ES);
         if (ch > p.n - 16 / RL::ES) ch = p.n - 16 / RL::ES;  // channels past N: not stored
-        const unsigned char* src = (const unsigned char*)p.res + (bz * p.r_bs + q * p.ldr + ch) * RL::ES;
+        const int64_t ro = p.c_mode == CM_SHUFFLE ? shuffled(q, ch) : bz * p.r_bs + q * p.ldr + ch;
+        const unsigned char* src = (const unsigned char*)p.res + ro * RL::ES;
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                          (__attribute__((address_space(3))) void*)(rslot + c * 1024), 16, 0, 0);
       }

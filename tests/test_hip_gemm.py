@@ -428,6 +428,19 @@ def test_up(dt, hip_bf16, hip_f32):
     check(got.cpu(), ref, f"up {dt}")
 
 
+@pytest.mark.parametrize("k,cq,rdt", [(128, 64, torch.bfloat16), (64, 32, torch.float32), (96, 16, None)])
+def test_up_decoder_shapes(k, cq, rdt, hip_bf16):
+    """1x1 conv + PixelShuffle(2) with the NAFNet decoder's channel split (N = 4 C', K up to 128):
+    the streaming kernels' shuffled store and shuffled residual addressing, two images."""
+    g = gen(10)
+    n, hh, ww = 2, 9, 27
+    x = rnd(g, n, hh, ww, k, dtype=torch.bfloat16)
+    wkn = rnd(g, k, 4 * cq, scale=k ** -0.5, dtype=torch.bfloat16)
+    res = rnd(g, n, 2 * hh, 2 * ww, cq, dtype=rdt) if rdt is not None else None
+    got = hip_bf16.up(*dev(x, wkn), residual=res.cuda() if res is not None else None, out_dtype=torch.float32)
+    assert_fp32(got.cpu(), REF.up(x, wkn, residual=res), rel=1e-5, what=f"up K{k} C'{cq} res {rdt}")
+
+
 # --------------------------------------------------------------------- ln_mul_linear / per image
 def test_ln_mul_linear(hip_bf16):
     """tools/test_kernels.py:251-258: m a channel slice; GELU(m) with fp32 x at 1e4."""
