@@ -237,9 +237,10 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
   int tile_override = 0;
   if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && !run_div) tile_override = 3;
-  // streaming kernel with an LDS ring per wave: rows without prologue, row or pixel-shuffle
-  // output (a lane's channel run inside one quadrant), K <= 128 (bf16 A) / 64 (fp32 A); a
-  // residual needs 16-byte rows and whole 16-byte channel units, and no gate. Automatic for K <= 64 and for K <= 128 without a gate (measured against the
+  // streaming kernel with an LDS ring per wave: rows without prologue or with LN / RMS / a bf16
+  // TLC map (split operands, batch 1), row or pixel-shuffle output (a lane's channel run inside
+  // one quadrant), K <= 128 (bf16 A) / 64 (fp32 A); a residual needs 16-byte rows and whole
+  // 16-byte channel units, and no gate. Automatic for K <= 64 and for K <= 128 without a gate (measured against the
   // register-prefetch streaming kernel and the 64 x 64 tiled kernel on the NAFNet, config-1 and
   // attn . V shapes: faster or equal except a gated K = 128); tile 16 forces it.
   {
@@ -247,8 +248,11 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     const int er = a->res ? esize(a->r_dtype) : 2;
     const bool res_ok = !a->res || (p.vec_res == 2 && a->n % (16 / er) == 0 && !a->gate);
     const int nb = (a->n <= 64 || a->gate) ? 4 : (run_div && run_div % 32 ? 4 : 8);
-    const bool ring_ok = a->a_mode == CLARUS_A_ROWS && a->pro == PRO_NONE && ks && res_ok &&
-                         (opm != OPM_SPLIT || a->a_dtype == DT_F32) &&
+    const bool pro_ok = a->pro == PRO_NONE ||
+                        (opm == OPM_SPLIT && a->batch == 1 &&
+                         (a->pro == PRO_LN || a->pro == PRO_RMS || (a->pro == PRO_MUL && a->s_dtype == DT_BF16)));
+    const bool ring_ok = a->a_mode == CLARUS_A_ROWS && pro_ok && ks && res_ok &&
+                         (opm != OPM_SPLIT || a->a_dtype == DT_F32 || a->pro != PRO_NONE) &&
                          (!run_div || (run_div % (4 * nb) == 0 && a->batch == 1));
     CLARUS_REQUIRE(a->tile != 16 || ring_ok, "gemm: the ring streaming kernel does not take this problem");
     const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || !a->gate);

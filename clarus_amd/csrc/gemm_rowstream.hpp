@@ -1,5 +1,5 @@
-// Streaming fused GEMM with an LDS ring per wave (NHWC rows, short K, no prologue; row or
-// pixel-shuffle output), gfx950.
+// Streaming fused GEMM with an LDS ring per wave (NHWC rows, short K; LN / RMS / TLC map
+// prologues; row or pixel-shuffle output), gfx950.
 //
 // Same math, MFMA mapping and epilogue as gemm_stream_kernel (D[channel][pixel] = W^T . A^T on
 // 16x16 MFMAs, a lane holds 4 * NB consecutive output channels of one pixel, all of W^T for the
@@ -49,26 +49,32 @@ struct RsR {
 template <int U, int RPB>
 __device__ __forceinline__ int rs_slot(int row, int unit) { return unit ^ ((row / RPB) & (U - 1)); }
 
-__host__ __device__ constexpr int rowstream_slot_bytes(int nb, int ks, int ta, int rdt, bool res) {
-  return 16 * ks * 32 * (ta == DT_BF16 ? 2 : 4) + (res ? 16 * nb * 16 * (rdt == DT_BF16 ? 2 : 4) : 0);
+// one ring slot: A rows, the prologue's map rows (bf16, X2), the residual rows
+__host__ __device__ constexpr int rowstream_slot_bytes(int nb, int ks, int ta, int rdt, bool res, bool x2 = false) {
+  return 16 * ks * 32 * (ta == DT_BF16 ? 2 : 4) + (x2 ? 16 * ks * 32 * 2 : 0) +
+         (res ? 16 * nb * 16 * (rdt == DT_BF16 ? 2 : 4) : 0);
 }
 // ring depth (4 waves per workgroup): the deepest ring that still lets two workgroups share a
 // CU (80 KiB each; one workgroup of 4 waves per CU measured slower than two with a shallower
 // ring), else what fits in 160 KiB; below 2 the shape has no kernel
-__host__ __device__ constexpr int rowstream_depth(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res) {
-  const int slot4 = 4 * rowstream_slot_bytes(nb, ks, ta, rdt, res);
+__host__ __device__ constexpr int rowstream_depth(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
+                                                  bool x2 = false) {
+  const int slot4 = 4 * rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
   const int w = stream_lds_bytes(nb, gate, ks, opm);
   const int d2 = (80 * 1024 - w) / slot4;
   const int d = d2 >= 2 ? d2 : (160 * 1024 - w) / slot4;
   return d > RS_MAX_DEPTH ? RS_MAX_DEPTH : d;
 }
-__host__ __device__ constexpr int rowstream_lds_bytes(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res) {
+__host__ __device__ constexpr int rowstream_lds_bytes(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
+                                                      bool x2 = false) {
   return stream_lds_bytes(nb, gate, ks, opm) +
-         4 * rowstream_depth(nb, gate, ks, opm, ta, rdt, res) * rowstream_slot_bytes(nb, ks, ta, rdt, res);
+         4 * rowstream_depth(nb, gate, ks, opm, ta, rdt, res, x2) * rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
 }
 
-// RDT: residual dtype (ignored when RES is false)
-template <int NB, bool GATE, int OPM, int TA, int KS, bool RES, int RDT>
+// RDT: residual dtype (ignored when RES is false). X2: the TLC map multiply prologue (bf16 map
+// rows gathered into the ring); LN / RMS prologues (runtime p.pro) take their statistics from
+// the row in registers. Prologues come with OPM_SPLIT (the fp32 prologue output as hi + lo).
+template <int NB, bool GATE, int OPM, int TA, int KS, bool RES, int RDT, bool X2 = false>
 __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   constexpr int G = GATE ? 2 : 1;
   constexpr int TN = NB * 16;
@@ -79,12 +85,18 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   constexpr int WB = G * TN * ROWB;
   using AL = RsA<KS, TA>;
   using RL = RsR<NB, RDT>;
-  constexpr int SLOT = AL::BYTES + (RES ? RL::BYTES : 0);
+  using ML = RsA<KS, DT_BF16>;                  // map rows (X2): same units as bf16 A rows
+  constexpr int MOFF = AL::BYTES;               // map block offset in a slot
+  constexpr int ROFF = AL::BYTES + (X2 ? ML::BYTES : 0);  // residual block offset
+  constexpr int SLOT = ROFF + (RES ? RL::BYTES : 0);
   constexpr int CA = AL::BYTES / 1024;          // A copies per lane per block
+  constexpr int CM = X2 ? ML::BYTES / 1024 : 0;  // map copies per lane per block
   constexpr int CR = RES ? RL::BYTES / 1024 : 0;  // residual copies per lane per block
-  static_assert(AL::BYTES % 1024 == 0 && (!RES || RL::BYTES % 1024 == 0), "blocks are whole copy instructions");
-  constexpr int C = CA + CR;                    // copy instructions per block
-  constexpr int RS_DEPTH = rowstream_depth(NB, GATE, KS, OPM, TA, RDT, RES);
+  static_assert(AL::BYTES % 1024 == 0 && (!RES || RL::BYTES % 1024 == 0) && (!X2 || ML::BYTES % 1024 == 0),
+                "blocks are whole copy instructions");
+  static_assert(!X2 || OPM == OPM_SPLIT, "a prologue output is split into hi + lo");
+  constexpr int C = CA + CM + CR;               // copy instructions per block
+  constexpr int RS_DEPTH = rowstream_depth(NB, GATE, KS, OPM, TA, RDT, RES, X2);
   static_assert(RS_DEPTH >= 2 && RS_DEPTH <= 4, "ring depth");
   static_assert(2 * C < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -136,6 +148,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
   const int64_t nmine = wid < nblk ? (nblk - 1 - wid) / stride + 1 : 0;  // blocks of this wave
   const int ua_valid = (int)(K * AL::ES / 16);  // A units per row that hold k < K
+  const int ua_map = (int)(K * 2 / 16);         // map units per row that hold k < K
 
   // element offset of (pixel q, channel c of the N space) in the output, which the residual
   // shares under the pixel shuffle (N = (dy, dx, c'), output [*, 2h, 2w, N / 4])
@@ -176,8 +189,30 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(slot + c * 1024), 16, 0, 0);
     }
+    if constexpr (X2) {  // map row of each pixel: S[clamp(y - pt), clamp(x - pl)], all K channels
+      unsigned char* mslot = slot + MOFF;
+#pragma unroll
+      for (int c = 0; c < CM; ++c) {
+        const int idx = c * 64 + lane;
+        const int row = idx / ML::U, s = idx - row * ML::U;
+        int u = rs_slot<ML::U, ML::RPB>(row, s);
+        if (u > ua_map - 1) u = ua_map - 1;
+        int64_t q = blk * 16 + row;
+        if (q > p.m - 1) q = p.m - 1;
+        const int hwi = p.h * p.w;
+        const int64_t im = q / hwi;
+        const int rr = (int)(q - im * hwi);
+        const int yq = rr / p.w;
+        int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
+        sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
+        sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
+        const unsigned char* src = (const unsigned char*)p.small + (((im * p.oh + sy) * p.ow + sx) * K) * 2 + u * 16;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(mslot + c * 1024), 16, 0, 0);
+      }
+    }
     if constexpr (RES) {
-      unsigned char* rslot = slot + AL::BYTES;
+      unsigned char* rslot = slot + ROFF;
 #pragma unroll
       for (int c = 0; c < CR; ++c) {
         const int idx = c * 64 + lane;
@@ -205,29 +240,78 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
       acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (GATE) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // this lane's 8 consecutive k of pixel lc per k-step, from the ring (k >= K read as 0)
+    RawFrag<TA> raw[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int64_t k = ks * 32 + lg * 8;
       const bool kok = k < K;
-      // this lane's 8 consecutive k of pixel lc, from the ring
-      RawFrag<TA> raw;
       if constexpr (TA == DT_BF16) {
         const int u = (int)(k / 8);
-        raw.q = kok ? *reinterpret_cast<const u32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
-                    : u32x4{0u, 0u, 0u, 0u};
+        raw[ks].q = kok ? *reinterpret_cast<const u32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
+                        : u32x4{0u, 0u, 0u, 0u};
       } else {
         const int u = (int)(k / 4);
-        raw.a = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
-                    : f32x4{0.f, 0.f, 0.f, 0.f};
-        raw.b = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u + 1) * 16)
-                    : f32x4{0.f, 0.f, 0.f, 0.f};
+        raw[ks].a = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+        raw[ks].b = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u + 1) * 16)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
       }
+    }
+    // LN / RMS statistics over the row: this lane's fragments, then the 4 lanes of the pixel
+    // (exact two-pass, fixed order)
+    float mean = 0.f, rstd = 1.f;
+    const bool stats = OPM == OPM_SPLIT && (p.pro == PRO_LN || p.pro == PRO_RMS);
+    if (stats) {
+      const float invk = 1.0f / (float)K;
+      if (p.pro == PRO_LN) {
+        float sum = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const f32x8 t = raw_f32<TA>(raw[ks]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sum += t.v[i];
+        }
+        mean = sum_col4(sum) * invk;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks * 32 + lg * 8 >= K) continue;
+        const f32x8 t = raw_f32<TA>(raw[ks]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float d = t.v[i] - mean;
+          ss += d * d;
+        }
+      }
+      rstd = rsqrtf(sum_col4(ss) * invk + p.ln_eps);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int64_t k = ks * 32 + lg * 8;
+      const bool kok = k < K;
       bf16x8 hi, lo;
       f32x8 a;
       if constexpr (OPM == OPM_BF16) {
-        hi = __builtin_bit_cast(bf16x8, raw.q);
+        hi = __builtin_bit_cast(bf16x8, raw[ks].q);
       } else {
-        a = raw_f32<TA>(raw);
+        a = raw_f32<TA>(raw[ks]);
+        if (stats) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a.v[i] = (a.v[i] - mean) * rstd;
+        }
+        if constexpr (X2) {
+          const u32x4 mq = kok ? *reinterpret_cast<const u32x4*>(slot + MOFF + lc * ML::RB +
+                                                                  rs_slot<ML::U, ML::RPB>(lc, (int)(k / 8)) * 16)
+                               : u32x4{0u, 0u, 0u, 0u};
+          RawFrag<DT_BF16> mr;
+          mr.q = mq;
+          const f32x8 mv = raw_f32<DT_BF16>(mr);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a.v[i] *= mv.v[i];
+        }
+        if (!kok) a = zero8();
         if constexpr (OPM == OPM_SPLIT) split_bf16(a, hi, lo);
       }
 #pragma unroll
@@ -284,7 +368,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
     out_offsets(q, oo, ro);
     if (fast) {
       if constexpr (RES) {  // the lane's RUN residual channels from the ring
-        const unsigned char* rrow = slot + AL::BYTES + lc * RL::RB;
+        const unsigned char* rrow = slot + ROFF + lc * RL::RB;
         constexpr int PER = 16 / RL::ES;  // channels per unit
 #pragma unroll
         for (int u0 = 0; u0 < RUN / PER; ++u0) {

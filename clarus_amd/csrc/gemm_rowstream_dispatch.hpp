@@ -8,7 +8,8 @@ namespace clarus {
 // k-steps of 32 per row for the ring kernel (0: K too long for it)
 int rowstream_ks_for(int64_t k, int ta);
 
-// Launches the kernel for p (AM_ROWS, no prologue, row output; p.ptiles unused). nb: channel
+// Launches the kernel for p (AM_ROWS; no prologue, or LN / RMS / the bf16 TLC map multiply on
+// split operands with batch 1; row or pixel-shuffle output; p.ptiles unused). nb: channel
 // blocks of 16 per workgroup (4 or 8); res / rdt: a residual of that dtype (not with gate; the
 // host checks 16-byte rows and n % (16 / residual element size) == 0). Returns false when no
 // instantiation matches.
