@@ -259,8 +259,11 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     if (a->tile == 16 || ring_auto) {
       GemmP q = p;
       q.ptiles = 0;
+      // 8 channel blocks when the ring still fits next to W^T, else 4
       if (launch_gemm_rowstream(q, nb, a->gate != 0, opm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
-                                (hipStream_t)stream))
+                                (hipStream_t)stream) ||
+          (nb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, opm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
+                                            a->batch, (hipStream_t)stream)))
         return check_launch("gemm");
       CLARUS_REQUIRE(a->tile == 0, "gemm: no ring streaming kernel for operand mode %d A dtype %d K=%lld", opm,
                      a->a_dtype, (long long)a->k);

@@ -10,26 +10,28 @@ namespace {
 template <int NB, bool GATE, int OPM, int TA, int KS, bool RES, int RDT, bool X2>
 void launch_one(const GemmP& p, unsigned ny, unsigned nz, hipStream_t s) {
   constexpr int lds = rowstream_lds_bytes(NB, GATE, KS, OPM, TA, RDT, RES, X2);
+  constexpr int nw = rowstream_waves(NB, GATE, KS, OPM, TA, RDT, RES, X2);
   static_assert(lds <= 160 * 1024, "LDS budget");
   auto fn = &gemm_rowstream_kernel<NB, GATE, OPM, TA, KS, RES, RDT, X2>;
   static const int per_cu = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024);
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), 256, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), 64 * nw, lds) !=
+            hipSuccess ||
         n < 1)
       n = 1;
     return n;
   }();
   // every workgroup resident: 256 CUs x per_cu, split over the channel tiles and batch; a
   // multiple of 8 keeps the channel tiles of a pixel range on one XCD
-  const int64_t blocks16 = cdiv(p.m, 16);
+  const int64_t blocks = cdiv(p.m, RS_BP);
   int64_t gx = (256LL * per_cu) / ((int64_t)ny * nz);
   if (gx < 1) gx = 1;
-  const int64_t need = cdiv(blocks16, 4);
+  const int64_t need = cdiv(blocks, nw);
   if (gx > need) gx = need;
   if (gx > 8) gx = gx / 8 * 8;
-  hipLaunchKernelGGL(fn, dim3((unsigned)gx, ny, nz), dim3(256), lds, s, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)gx, ny, nz), dim3(64 * nw), lds, s, p);
 }
 
 using RsLaunch = void (*)(const GemmP&, unsigned, unsigned, hipStream_t);

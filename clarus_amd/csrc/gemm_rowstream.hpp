@@ -27,13 +27,18 @@ namespace clarus {
 
 constexpr int RS_MAX_DEPTH = 4;  // ring blocks per wave, at most
 
+// pixels per ring block (16 or 32; with 32 two 16-pixel MFMA halves share each W^T fragment
+// read, which halves W^T LDS traffic but doubles the slot: measured slower on every NAFNet,
+// config-1 and attn . V shape but the widest, e.g. attn . V fp32 l0 137 vs 124 us)
+constexpr int RS_BP = 16;
+
 template <int KS, int TA>
 struct RsA {
   static constexpr int ES = TA == DT_BF16 ? 2 : 4;
   static constexpr int RB = KS * 32 * ES;       // bytes per A row in the ring
   static constexpr int U = RB / 16;             // 16-byte units per row
   static constexpr int RPB = RB >= 256 ? 1 : 256 / RB;  // rows per 256-byte bank row
-  static constexpr int BYTES = 16 * RB;         // one block of A
+  static constexpr int BYTES = RS_BP * RB;      // one block of A
 };
 
 // residual bytes per block row: the workgroup's TN channels
@@ -43,7 +48,7 @@ struct RsR {
   static constexpr int RB = NB * 16 * ES;
   static constexpr int U = RB / 16;
   static constexpr int RPB = RB >= 256 ? 1 : 256 / RB;
-  static constexpr int BYTES = 16 * RB;
+  static constexpr int BYTES = RS_BP * RB;
 };
 
 template <int U, int RPB>
@@ -51,31 +56,55 @@ __device__ __forceinline__ int rs_slot(int row, int unit) { return unit ^ ((row 
 
 // one ring slot: A rows, the prologue's map rows (bf16, X2), the residual rows
 __host__ __device__ constexpr int rowstream_slot_bytes(int nb, int ks, int ta, int rdt, bool res, bool x2 = false) {
-  return 16 * ks * 32 * (ta == DT_BF16 ? 2 : 4) + (x2 ? 16 * ks * 32 * 2 : 0) +
-         (res ? 16 * nb * 16 * (rdt == DT_BF16 ? 2 : 4) : 0);
+  return RS_BP * (ks * 32 * (ta == DT_BF16 ? 2 : 4) + (x2 ? ks * 32 * 2 : 0) + (res ? nb * 16 * (rdt == DT_BF16 ? 2 : 4) : 0));
 }
-// ring depth (4 waves per workgroup): the deepest ring that still lets two workgroups share a
-// CU (80 KiB each; one workgroup of 4 waves per CU measured slower than two with a shallower
-// ring), else what fits in 160 KiB; below 2 the shape has no kernel
+// Shape of the workgroup: NW waves sharing one copy of W^T, each with a ring of depth D, chosen
+// for the most blocks in flight per CU:
+//   * 4 waves with a ring of at least 3 while two workgroups still share a CU (80 KiB each);
+//   * else 8 waves with a ring of at least 3 in one workgroup per CU (160 KiB): a large W^T
+//     tile (K = 128 with a gate: 35 KiB) is then staged once for 8 waves instead of twice;
+//   * else 4 waves with a ring of 2 in two workgroups per CU, or one workgroup with what fits.
+// One workgroup of 4 waves with a deeper ring measured slower than two with a ring of 2
+// (c128 expand 51.8 vs 38.6 us). Below a depth of 2 the shape has no kernel.
+struct RsShape {
+  int nw, depth;
+};
+__host__ __device__ constexpr RsShape rowstream_shape(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
+                                                      bool x2 = false) {
+  const int slot = rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
+  const int w = stream_lds_bytes(nb, gate, ks, opm);
+  auto cap = [](int d) { return d > RS_MAX_DEPTH ? RS_MAX_DEPTH : d; };
+  const int d4 = cap((80 * 1024 - w) / (4 * slot));
+  if (d4 >= 3) return RsShape{4, d4};
+  const int d8 = cap((160 * 1024 - w) / (8 * slot));
+  if (d8 >= 3) return RsShape{8, d8};
+  if (d4 >= 2) return RsShape{4, d4};
+  return RsShape{4, cap((160 * 1024 - w) / (4 * slot))};
+}
 __host__ __device__ constexpr int rowstream_depth(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
                                                   bool x2 = false) {
-  const int slot4 = 4 * rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
-  const int w = stream_lds_bytes(nb, gate, ks, opm);
-  const int d2 = (80 * 1024 - w) / slot4;
-  const int d = d2 >= 2 ? d2 : (160 * 1024 - w) / slot4;
-  return d > RS_MAX_DEPTH ? RS_MAX_DEPTH : d;
+  return rowstream_shape(nb, gate, ks, opm, ta, rdt, res, x2).depth;
+}
+__host__ __device__ constexpr int rowstream_waves(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
+                                                  bool x2 = false) {
+  return rowstream_shape(nb, gate, ks, opm, ta, rdt, res, x2).nw;
 }
 __host__ __device__ constexpr int rowstream_lds_bytes(int nb, bool gate, int ks, int opm, int ta, int rdt, bool res,
                                                       bool x2 = false) {
-  return stream_lds_bytes(nb, gate, ks, opm) +
-         4 * rowstream_depth(nb, gate, ks, opm, ta, rdt, res, x2) * rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
+  const RsShape sh = rowstream_shape(nb, gate, ks, opm, ta, rdt, res, x2);
+  return stream_lds_bytes(nb, gate, ks, opm) + sh.nw * sh.depth * rowstream_slot_bytes(nb, ks, ta, rdt, res, x2);
 }
 
 // RDT: residual dtype (ignored when RES is false). X2: the TLC map multiply prologue (bf16 map
 // rows gathered into the ring); LN / RMS prologues (runtime p.pro) take their statistics from
 // the row in registers. Prologues come with OPM_SPLIT (the fp32 prologue output as hi + lo).
 template <int NB, bool GATE, int OPM, int TA, int KS, bool RES, int RDT, bool X2 = false>
-__global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
+__global__ void __launch_bounds__(64 * rowstream_waves(NB, GATE, KS, OPM, TA, RDT, RES, X2))
+gemm_rowstream_kernel(const GemmP p) {
+  constexpr int NW = rowstream_waves(NB, GATE, KS, OPM, TA, RDT, RES, X2);  // waves per workgroup
+  constexpr int NT = 64 * NW;
+  constexpr int BP = RS_BP;
+  constexpr int HB = BP / 16;  // 16-pixel MFMA halves per ring block
   constexpr int G = GATE ? 2 : 1;
   constexpr int TN = NB * 16;
   constexpr int RUN = 4 * NB;
@@ -114,7 +143,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   unsigned char* ring = wlds + WB + wave * (RS_DEPTH * SLOT);
 
   // ---- epilogue vectors and W^T rows (all of K) -> LDS, once (as gemm_stream_kernel)
-  for (int i = tid; i < (G + 1) * TN; i += 256) {
+  for (int i = tid; i < (G + 1) * TN; i += NT) {
     const int part = i / TN;
     const int64_t c = n0 + (i - part * TN);
     float v;
@@ -122,7 +151,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
     else v = ((p.scale && c < p.n) ? p.scale[c] : 1.f) * p.out_scale;
     epi[i] = v;
   }
-  for (int base = wave * 1024; base < WB; base += 4 * 1024) {
+  for (int base = wave * 1024; base < WB; base += NW * 1024) {
     const int pos = base + lane * 16;
     if (pos < WB) {
       const int r = pos / ROWB;
@@ -143,9 +172,9 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   __syncthreads();
 
   const bool lane_full = run0 + RUN <= p.n;
-  const int64_t nblk = cdiv(p.m, 16);
-  const int64_t stride = (int64_t)gridDim.x * 4;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t nblk = cdiv(p.m, BP);
+  const int64_t stride = (int64_t)gridDim.x * NW;
+  const int64_t wid = (int64_t)blockIdx.x * NW + wave;
   const int64_t nmine = wid < nblk ? (nblk - 1 - wid) / stride + 1 : 0;  // blocks of this wave
   const int ua_valid = (int)(K * AL::ES / 16);  // A units per row that hold k < K
   const int ua_map = (int)(K * 2 / 16);         // map units per row that hold k < K
@@ -183,7 +212,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
       const int row = idx / AL::U, s = idx - row * AL::U;
       int u = rs_slot<AL::U, AL::RPB>(row, s);
       if (u > ua_valid - 1) u = ua_valid - 1;  // past K: any valid unit (masked when read)
-      int64_t q = blk * 16 + row;
+      int64_t q = blk * BP + row;
       if (q > p.m - 1) q = p.m - 1;            // past M: any valid row (not stored)
       const unsigned char* src = A + (q * p.lda) * AL::ES + u * 16;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -197,7 +226,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
         const int row = idx / ML::U, s = idx - row * ML::U;
         int u = rs_slot<ML::U, ML::RPB>(row, s);
         if (u > ua_map - 1) u = ua_map - 1;
-        int64_t q = blk * 16 + row;
+        int64_t q = blk * BP + row;
         if (q > p.m - 1) q = p.m - 1;
         const int hwi = p.h * p.w;
         const int64_t im = q / hwi;
@@ -218,7 +247,7 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
         const int idx = c * 64 + lane;
         const int row = idx / RL::U, s = idx - row * RL::U;
         const int u = rs_slot<RL::U, RL::RPB>(row, s);
-        int64_t q = blk * 16 + row;
+        int64_t q = blk * BP + row;
         if (q > p.m - 1) q = p.m - 1;
         int64_t ch = n0 + u * (16 / RL::ES);
         if (ch > p.n - 16 / RL::ES) ch = p.n - 16 / RL::ES;  // channels past N: not stored
@@ -233,187 +262,217 @@ __global__ void __launch_bounds__(256) gemm_rowstream_kernel(const GemmP p) {
   auto compute_block = [&](int64_t j) __attribute__((always_inline)) {
     const int64_t blk = wid + j * stride;
     const unsigned char* slot = ring + (int)(j % RS_DEPTH) * SLOT;
-    const int64_t q = blk * 16 + lc;
-    f32x4 acc[NB], acc2[GATE ? NB : 1];
+    f32x4 acc[HB][NB], acc2[HB][GATE ? NB : 1];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (GATE) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    // this lane's 8 consecutive k of pixel lc per k-step, from the ring (k >= K read as 0)
-    RawFrag<TA> raw[KS];
+    for (int h = 0; h < HB; ++h)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int64_t k = ks * 32 + lg * 8;
-      const bool kok = k < K;
-      if constexpr (TA == DT_BF16) {
-        const int u = (int)(k / 8);
-        raw[ks].q = kok ? *reinterpret_cast<const u32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
-                        : u32x4{0u, 0u, 0u, 0u};
-      } else {
-        const int u = (int)(k / 4);
-        raw[ks].a = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u) * 16)
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
-        raw[ks].b = kok ? *reinterpret_cast<const f32x4*>(slot + lc * AL::RB + rs_slot<AL::U, AL::RPB>(lc, u + 1) * 16)
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < NB; ++i) {
+        acc[h][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (GATE) acc2[h][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    // this lane's 8 consecutive k of pixel 16 h + lc per k-step, from the ring (k >= K read as 0)
+    RawFrag<TA> raw[HB][KS];
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      const int row = 16 * h + lc;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int64_t k = ks * 32 + lg * 8;
+        const bool kok = k < K;
+        if constexpr (TA == DT_BF16) {
+          const int u = (int)(k / 8);
+          raw[h][ks].q = kok ? *reinterpret_cast<const u32x4*>(slot + row * AL::RB + rs_slot<AL::U, AL::RPB>(row, u) * 16)
+                             : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          const int u = (int)(k / 4);
+          raw[h][ks].a = kok ? *reinterpret_cast<const f32x4*>(slot + row * AL::RB + rs_slot<AL::U, AL::RPB>(row, u) * 16)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+          raw[h][ks].b = kok ? *reinterpret_cast<const f32x4*>(slot + row * AL::RB +
+                                                                 rs_slot<AL::U, AL::RPB>(row, u + 1) * 16)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
-    // LN / RMS statistics over the row: this lane's fragments, then the 4 lanes of the pixel
+    // LN / RMS statistics over each row: this lane's fragments, then the 4 lanes of the pixel
     // (exact two-pass, fixed order)
-    float mean = 0.f, rstd = 1.f;
+    float mean[HB], rstd[HB];
     const bool stats = OPM == OPM_SPLIT && (p.pro == PRO_LN || p.pro == PRO_RMS);
-    if (stats) {
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      mean[h] = 0.f;
+      rstd[h] = 1.f;
+      if (!stats) continue;
       const float invk = 1.0f / (float)K;
       if (p.pro == PRO_LN) {
         float sum = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const f32x8 t = raw_f32<TA>(raw[ks]);
+          const f32x8 t = raw_f32<TA>(raw[h][ks]);
 #pragma unroll
           for (int i = 0; i < 8; ++i) sum += t.v[i];
         }
-        mean = sum_col4(sum) * invk;
+        mean[h] = sum_col4(sum) * invk;
       }
       float ss = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         if (ks * 32 + lg * 8 >= K) continue;
-        const f32x8 t = raw_f32<TA>(raw[ks]);
+        const f32x8 t = raw_f32<TA>(raw[h][ks]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float d = t.v[i] - mean;
+          const float d = t.v[i] - mean[h];
           ss += d * d;
         }
       }
-      rstd = rsqrtf(sum_col4(ss) * invk + p.ln_eps);
+      rstd[h] = rsqrtf(sum_col4(ss) * invk + p.ln_eps);
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int64_t k = ks * 32 + lg * 8;
       const bool kok = k < K;
-      bf16x8 hi, lo;
-      f32x8 a;
-      if constexpr (OPM == OPM_BF16) {
-        hi = __builtin_bit_cast(bf16x8, raw[ks].q);
-      } else {
-        a = raw_f32<TA>(raw[ks]);
-        if (stats) {
+      bf16x8 hi[HB], lo[HB];
+      f32x8 a[HB];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) a.v[i] = (a.v[i] - mean) * rstd;
-        }
-        if constexpr (X2) {
-          const u32x4 mq = kok ? *reinterpret_cast<const u32x4*>(slot + MOFF + lc * ML::RB +
-                                                                  rs_slot<ML::U, ML::RPB>(lc, (int)(k / 8)) * 16)
-                               : u32x4{0u, 0u, 0u, 0u};
-          RawFrag<DT_BF16> mr;
-          mr.q = mq;
-          const f32x8 mv = raw_f32<DT_BF16>(mr);
+      for (int h = 0; h < HB; ++h) {
+        if constexpr (OPM == OPM_BF16) {
+          hi[h] = __builtin_bit_cast(bf16x8, raw[h][ks].q);
+        } else {
+          a[h] = raw_f32<TA>(raw[h][ks]);
+          if (stats) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) a.v[i] *= mv.v[i];
+            for (int i = 0; i < 8; ++i) a[h].v[i] = (a[h].v[i] - mean[h]) * rstd[h];
+          }
+          if constexpr (X2) {
+            const int row = 16 * h + lc;
+            const u32x4 mq = kok ? *reinterpret_cast<const u32x4*>(slot + MOFF + row * ML::RB +
+                                                                    rs_slot<ML::U, ML::RPB>(row, (int)(k / 8)) * 16)
+                                 : u32x4{0u, 0u, 0u, 0u};
+            RawFrag<DT_BF16> mr;
+            mr.q = mq;
+            const f32x8 mv = raw_f32<DT_BF16>(mr);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[h].v[i] *= mv.v[i];
+          }
+          if (!kok) a[h] = zero8();
+          if constexpr (OPM == OPM_SPLIT) split_bf16(a[h], hi[h], lo[h]);
         }
-        if (!kok) a = zero8();
-        if constexpr (OPM == OPM_SPLIT) split_bf16(a, hi, lo);
       }
+      // each W^T fragment is read from LDS once for all HB pixel halves
 #pragma unroll
       for (int jb = 0; jb < NB; ++jb) {
 #pragma unroll
         for (int hf = 0; hf < G; ++hf) {
           const unsigned char* wp = wlds + (size_t)(hf * TN + jb * 16 + lc) * ROWB + (ks * 32 + lg * 8) * WES;
-          f32x4 t = hf ? acc2[GATE ? jb : 0] : acc[jb];
-          if constexpr (OPM == OPM_F32) {
+          if constexpr (OPM == OPM_F32) {  // fp32 products: mfma i contracts k = ks * 32 + 8 lg + i over lg
             const f32x4 w0 = *reinterpret_cast<const f32x4*>(wp);
             const f32x4 w1 = *reinterpret_cast<const f32x4*>(wp + 16);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t = mfma_f32(w0[i], a.v[i], t);
+            for (int h = 0; h < HB; ++h) {
+              f32x4 t = hf ? acc2[h][GATE ? jb : 0] : acc[h][jb];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t = mfma_f32(w1[i], a.v[4 + i], t);
-          } else {
-            const bf16x8 wv = *reinterpret_cast<const bf16x8*>(wp);
-            t = mfma_bf16(wv, hi, t);
-            if constexpr (OPM == OPM_SPLIT) t = mfma_bf16(wv, lo, t);
-          }
-          if (hf) acc2[GATE ? jb : 0] = t; else acc[jb] = t;
-        }
-      }
-    }
-    if (q >= p.m) return;
-    float v[RUN];
-    const int e0 = lg * RUN;
+              for (int i = 0; i < 4; ++i) t = mfma_f32(w0[i], a[h].v[i], t);
 #pragma unroll
-    for (int jb = 0; jb < NB; ++jb) {
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(epi + e0 + jb * 4);
-      f32x4 b2 = b1;
-      if constexpr (GATE) b2 = *reinterpret_cast<const f32x4*>(epi + TN + e0 + jb * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = acc[jb][i] + b1[i];
-        if constexpr (GATE) x = x * (acc2[jb][i] + b2[i]);
-        v[jb * 4 + i] = x;
-      }
-    }
-    if (p.act == ACT_GELU) {
-#pragma unroll
-      for (int i = 0; i < RUN; ++i) v[i] = gelu_erf(v[i]);
-    } else if (p.act == ACT_LRELU) {
-#pragma unroll
-      for (int i = 0; i < RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
-    }
-#pragma unroll
-    for (int jb = 0; jb < NB; ++jb) {
-      const f32x4 sc = *reinterpret_cast<const f32x4*>(epi + G * TN + e0 + jb * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[jb * 4 + i] *= sc[i];
-    }
-    int64_t oo, ro;
-    out_offsets(q, oo, ro);
-    if (fast) {
-      if constexpr (RES) {  // the lane's RUN residual channels from the ring
-        const unsigned char* rrow = slot + ROFF + lc * RL::RB;
-        constexpr int PER = 16 / RL::ES;  // channels per unit
-#pragma unroll
-        for (int u0 = 0; u0 < RUN / PER; ++u0) {
-          const int u = (lg * RUN) / PER + u0;
-          const u32x4 r = *reinterpret_cast<const u32x4*>(rrow + rs_slot<RL::U, RL::RPB>(lc, u) * 16);
-          if constexpr (RDT == DT_BF16) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              v[u0 * 8 + 2 * i] += __uint_as_float(r[i] << 16);
-              v[u0 * 8 + 2 * i + 1] += __uint_as_float(r[i] & 0xffff0000u);
+              for (int i = 0; i < 4; ++i) t = mfma_f32(w1[i], a[h].v[4 + i], t);
+              if (hf) acc2[h][GATE ? jb : 0] = t; else acc[h][jb] = t;
             }
           } else {
+            const bf16x8 wv = *reinterpret_cast<const bf16x8*>(wp);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[u0 * 4 + i] += __uint_as_float(r[i]);
+            for (int h = 0; h < HB; ++h) {
+              f32x4 t = hf ? acc2[h][GATE ? jb : 0] : acc[h][jb];
+              t = mfma_bf16(wv, hi[h], t);
+              if constexpr (OPM == OPM_SPLIT) t = mfma_bf16(wv, lo[h], t);
+              if (hf) acc2[h][GATE ? jb : 0] = t; else acc[h][jb] = t;
+            }
           }
         }
       }
-      if (p.c_dt == DT_BF16) {
-        unsigned short* op = (unsigned short*)p.c + oo;
+    }
+    // ---- epilogue per pixel half
 #pragma unroll
-        for (int jj = 0; jj < RUN / 8; ++jj) {
-          u32x4 o;
+    for (int h = 0; h < HB; ++h) {
+      const int row = 16 * h + lc;
+      const int64_t q = blk * BP + row;
+      if (q >= p.m) continue;
+      float v[RUN];
+      const int e0 = lg * RUN;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            o[i] = (unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i]) | ((unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i + 1]) << 16);
-          if (p.vec_out == 2) {
-            *reinterpret_cast<u32x4*>(op + 8 * jj) = o;
-          } else {
-            *reinterpret_cast<u32x2*>(op + 8 * jj) = u32x2{o[0], o[1]};
-            *reinterpret_cast<u32x2*>(op + 8 * jj + 4) = u32x2{o[2], o[3]};
+      for (int jb = 0; jb < NB; ++jb) {
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(epi + e0 + jb * 4);
+        f32x4 b2 = b1;
+        if constexpr (GATE) b2 = *reinterpret_cast<const f32x4*>(epi + TN + e0 + jb * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = acc[h][jb][i] + b1[i];
+          if constexpr (GATE) x = x * (acc2[h][jb][i] + b2[i]);
+          v[jb * 4 + i] = x;
+        }
+      }
+      if (p.act == ACT_GELU) {
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) v[i] = gelu_erf(v[i]);
+      } else if (p.act == ACT_LRELU) {
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * p.slope;
+      }
+#pragma unroll
+      for (int jb = 0; jb < NB; ++jb) {
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(epi + G * TN + e0 + jb * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[jb * 4 + i] *= sc[i];
+      }
+      int64_t oo, ro;
+      out_offsets(q, oo, ro);
+      if (fast) {
+        if constexpr (RES) {  // the lane's RUN residual channels from the ring
+          const unsigned char* rrow = slot + ROFF + row * RL::RB;
+          constexpr int PER = 16 / RL::ES;  // channels per unit
+#pragma unroll
+          for (int u0 = 0; u0 < RUN / PER; ++u0) {
+            const int u = (lg * RUN) / PER + u0;
+            const u32x4 r = *reinterpret_cast<const u32x4*>(rrow + rs_slot<RL::U, RL::RPB>(row, u) * 16);
+            if constexpr (RDT == DT_BF16) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                v[u0 * 8 + 2 * i] += __uint_as_float(r[i] << 16);
+                v[u0 * 8 + 2 * i + 1] += __uint_as_float(r[i] & 0xffff0000u);
+              }
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) v[u0 * 4 + i] += __uint_as_float(r[i]);
+            }
           }
         }
-      } else {
-        float* op = (float*)p.c + oo;
+        if (p.c_dt == DT_BF16) {
+          unsigned short* op = (unsigned short*)p.c + oo;
 #pragma unroll
-        for (int jj = 0; jj < RUN / 4; ++jj)
-          *reinterpret_cast<f32x4*>(op + 4 * jj) = f32x4{v[4 * jj], v[4 * jj + 1], v[4 * jj + 2], v[4 * jj + 3]};
-      }
-    } else {  // partial channel tile / unaligned output: element-wise
+          for (int jj = 0; jj < RUN / 8; ++jj) {
+            u32x4 o;
 #pragma unroll
-      for (int i = 0; i < RUN; ++i) {
-        if (run0 + i >= p.n) continue;
-        float x = v[i];
-        if constexpr (RES) x += load1(p.res, p.r_dt, ro + i);
-        store1(p.c, p.c_dt, oo + i, x);
+            for (int i = 0; i < 4; ++i)
+              o[i] = (unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i]) |
+                     ((unsigned)f32_to_bf16_bits(v[8 * jj + 2 * i + 1]) << 16);
+            if (p.vec_out == 2) {
+              *reinterpret_cast<u32x4*>(op + 8 * jj) = o;
+            } else {
+              *reinterpret_cast<u32x2*>(op + 8 * jj) = u32x2{o[0], o[1]};
+              *reinterpret_cast<u32x2*>(op + 8 * jj + 4) = u32x2{o[2], o[3]};
+            }
+          }
+        } else {
+          float* op = (float*)p.c + oo;
+#pragma unroll
+          for (int jj = 0; jj < RUN / 4; ++jj)
+            *reinterpret_cast<f32x4*>(op + 4 * jj) = f32x4{v[4 * jj], v[4 * jj + 1], v[4 * jj + 2], v[4 * jj + 3]};
+        }
+      } else {  // partial channel tile / unaligned output: element-wise
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) {
+          if (run0 + i >= p.n) continue;
+          float x = v[i];
+          if constexpr (RES) x += load1(p.res, p.r_dt, ro + i);
+          store1(p.c, p.c_dt, oo + i, x);
+        }
       }
     }
   };
