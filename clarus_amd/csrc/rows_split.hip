@@ -1,4 +1,4 @@
-// Prologue pass of the split-operand GEMM path: clarus_hip_rows_split.
+// Prologue passes of the long-K GEMMs: clarus_hip_rows_split and clarus_hip_rows_prologue.
 //
 // A GEMM whose A operand goes through a prologue (LayerNorm, RMS norm, the TLC local-mean map
 // multiply) has fp32 values after the prologue, which bf16 MFMAs take as hi + lo bf16 pairs
@@ -9,6 +9,12 @@
 // prologue kernel. Prologue semantics: ops/torch_ref.py:94-100 (_ln, two-pass statistics, eps
 // inside the square root), :85-91 and :18-41 (the TLC map expanded over the image with clamped
 // coordinates), applied in fp32.
+//
+// clarus_hip_rows_prologue writes the prologue output rounded once to bf16 (RNE), a row of K
+// elements, for a plain bf16 GEMM with the original K: the reference's GPU path for bf16 models
+// (kernels/spatial.py:312 ln_rows with out_dtype = the compute dtype, :342 mul_small; used at
+// ops/triton_cuda.py:104-110), which rounds the prologue output to the operand dtype before the
+// tensor-core product (kernels/gemm.py:164, :175, :186).
 //
 // Work split: G lanes share a row (G = 16, 32 or 64, the power of two covering K / 8 up to 64),
 // each holding FR fragments of 8 consecutive elements in registers; row statistics are exact
@@ -38,7 +44,7 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <int TA, int G, int FR>
+template <int TA, int G, int FR, bool SPLIT>
 __global__ void __launch_bounds__(256) rows_split_kernel(const SplitP p) {
   constexpr int ES = TA == DT_BF16 ? 2 : 4;
   constexpr int R = 64 / G;  // rows per wave
@@ -99,58 +105,59 @@ __global__ void __launch_bounds__(256) rows_split_kernel(const SplitP p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[f].v[i] = (x[f].v[i] - mean) * rstd;
     }
-    unsigned short* dst = (unsigned short*)p.out + row * 2 * K;
+    unsigned short* dst = (unsigned short*)p.out + row * (SPLIT ? 2 : 1) * K;
 #pragma unroll
     for (int f = 0; f < FR; ++f) {
       const int64_t kk = (int64_t)(f * G + gl) * 8;
       if (kk >= K) continue;
-      bf16x8 hi, lo;
-      split_bf16(x[f], hi, lo);
-      *reinterpret_cast<bf16x8*>(dst + kk) = hi;
-      *reinterpret_cast<bf16x8*>(dst + K + kk) = lo;
+      if constexpr (SPLIT) {
+        bf16x8 hi, lo;
+        split_bf16(x[f], hi, lo);
+        *reinterpret_cast<bf16x8*>(dst + kk) = hi;
+        *reinterpret_cast<bf16x8*>(dst + K + kk) = lo;
+      } else {
+        *reinterpret_cast<bf16x8*>(dst + kk) = pack_bf16(x[f]);
+      }
     }
   }
 }
 
-template <int TA, int G, int FR>
+template <int TA, int G, int FR, bool SPLIT>
 static void launch_split(const SplitP& p, hipStream_t s) {
   constexpr int rows_per_block = 4 * (64 / G);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(p.m, rows_per_block), 4096);
-  hipLaunchKernelGGL((rows_split_kernel<TA, G, FR>), dim3(blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((rows_split_kernel<TA, G, FR, SPLIT>), dim3(blocks), dim3(256), 0, s, p);
 }
 
-template <int TA>
+template <int TA, bool SPLIT>
 static void launch_split_ta(const SplitP& p, hipStream_t s) {
   const int64_t frags = p.k / 8;  // 8-element fragments per row
-  if (frags <= 16) launch_split<TA, 16, 1>(p, s);
-  else if (frags <= 32) launch_split<TA, 32, 1>(p, s);
-  else if (frags <= 64) launch_split<TA, 64, 1>(p, s);
-  else if (frags <= 128) launch_split<TA, 64, 2>(p, s);
-  else launch_split<TA, 64, 4>(p, s);
+  if (frags <= 16) launch_split<TA, 16, 1, SPLIT>(p, s);
+  else if (frags <= 32) launch_split<TA, 32, 1, SPLIT>(p, s);
+  else if (frags <= 64) launch_split<TA, 64, 1, SPLIT>(p, s);
+  else if (frags <= 128) launch_split<TA, 64, 2, SPLIT>(p, s);
+  else launch_split<TA, 64, 4, SPLIT>(p, s);
 }
 
-}  // namespace clarus
-
-using namespace clarus;
-
-extern "C" int clarus_hip_rows_split(const ClarusGemmArgs* a, void* out, void* stream) {
+// shared argument checks and launch of both entry points
+static int rows_pass(const ClarusGemmArgs* a, void* out, void* stream, bool split, const char* what) {
   clear_error();
-  CLARUS_REQUIRE(a != nullptr && a->a && out, "rows_split: null operand");
-  CLARUS_REQUIRE(a->m > 0 && a->k > 0, "rows_split: empty problem");
+  CLARUS_REQUIRE(a != nullptr && a->a && out, "%s: null operand", what);
+  CLARUS_REQUIRE(a->m > 0 && a->k > 0, "%s: empty problem", what);
   CLARUS_REQUIRE(a->pro == PRO_LN || a->pro == PRO_RMS || a->pro == PRO_MUL,
-                 "rows_split: prologue %d is not LN, RMS or the map multiply", a->pro);
-  CLARUS_REQUIRE(a->a_dtype == DT_F32 || a->a_dtype == DT_BF16, "rows_split: bad A dtype");
-  CLARUS_REQUIRE(a->k % 8 == 0 && a->k <= 2048, "rows_split: K=%lld must be a multiple of 8, at most 2048",
+                 "%s: prologue %d is not LN, RMS or the map multiply", what, a->pro);
+  CLARUS_REQUIRE(a->a_dtype == DT_F32 || a->a_dtype == DT_BF16, "%s: bad A dtype", what);
+  CLARUS_REQUIRE(a->k % 8 == 0 && a->k <= 2048, "%s: K=%lld must be a multiple of 8, at most 2048", what,
                  (long long)a->k);
   const int ea = a->a_dtype == DT_BF16 ? 2 : 4;
   CLARUS_REQUIRE(aligned(a->a, 16) && aligned(out, 16) && (a->lda * ea) % 16 == 0 && a->lda >= a->k,
-                 "rows_split: A rows and the output must be 16-byte aligned");
-  CLARUS_REQUIRE(a->batch == 1, "rows_split: rows of one batch entry (fold images into m)");
+                 "%s: A rows and the output must be 16-byte aligned", what);
+  CLARUS_REQUIRE(a->batch == 1, "%s: rows of one batch entry (fold images into m)", what);
   if (a->pro == PRO_MUL) {
     CLARUS_REQUIRE(a->small && (a->s_dtype == DT_F32 || a->s_dtype == DT_BF16) && aligned(a->small, 16),
-                   "rows_split: the map multiply needs an aligned map");
+                   "%s: the map multiply needs an aligned map", what);
     CLARUS_REQUIRE(a->h > 0 && a->w > 0 && a->oh > 0 && a->ow > 0 && a->m % ((int64_t)a->h * a->w) == 0,
-                   "rows_split: map geometry");
+                   "%s: map geometry", what);
   }
   SplitP p{};
   p.a = a->a; p.out = out; p.small = a->small;
@@ -158,7 +165,20 @@ extern "C" int clarus_hip_rows_split(const ClarusGemmArgs* a, void* out, void* s
   p.pro = a->pro; p.s_dt = a->s_dtype;
   p.h = a->h; p.w = a->w; p.oh = a->oh; p.ow = a->ow; p.pt = a->pt; p.pl = a->pl;
   p.eps = a->ln_eps;
-  if (a->a_dtype == DT_BF16) launch_split_ta<DT_BF16>(p, (hipStream_t)stream);
-  else launch_split_ta<DT_F32>(p, (hipStream_t)stream);
-  return check_launch("rows_split");
+  hipStream_t s = (hipStream_t)stream;
+  if (a->a_dtype == DT_BF16) split ? launch_split_ta<DT_BF16, true>(p, s) : launch_split_ta<DT_BF16, false>(p, s);
+  else split ? launch_split_ta<DT_F32, true>(p, s) : launch_split_ta<DT_F32, false>(p, s);
+  return check_launch(what);
+}
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" int clarus_hip_rows_split(const ClarusGemmArgs* a, void* out, void* stream) {
+  return rows_pass(a, out, stream, true, "rows_split");
+}
+
+extern "C" int clarus_hip_rows_prologue(const ClarusGemmArgs* a, void* out, void* stream) {
+  return rows_pass(a, out, stream, false, "rows_prologue");
 }

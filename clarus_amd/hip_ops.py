@@ -66,6 +66,12 @@ class HipOps(Backend):
     # this K on; shorter rows keep the prologue inside the streaming kernels (NAFNet-w64 720p
     # forward measured at thresholds 128 / 256 / 512: 10.68 / 10.51 / 10.60 ms)
     split_min_k = 256
+    # From split_min_k on, the prologue output of a bf16-weight GEMM is rounded once to bf16
+    # (clarus_hip_rows_prologue, then a plain GEMM with K) as in the reference's GPU path
+    # (ops/triton_cuda.py:104-110, kernels/gemm.py:164-186). True keeps it as [hi | lo]
+    # (clarus_hip_rows_split, K' = 2K): fp32-accurate products at twice the MFMA work and A bytes.
+    # NAFNet-w64 720p bf16 forward: split 10.77 ms.
+    prologue_split = False
 
     def __init__(self, dtype, device):
         super().__init__(dtype, device)
@@ -193,17 +199,19 @@ class HipOps(Backend):
                    act=_lib.ACT_GELU if act == "gelu" else 0)
         m = n * h * wd
         if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0:
-            # split-operand path (the fp32-accurate form of triton_cuda.py:101-108's separate
-            # ln_rows / mul_small passes): prologue rows as [hi | lo], then K' = 2K
-            rows = torch.empty((m, 2 * k), device=x.device, dtype=torch.bfloat16)
+            # the separate prologue pass of triton_cuda.py:104-110 (ln_rows / mul_small), then a
+            # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K)
+            kk = 2 * k if self.prologue_split else k
+            rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
             hh, ww, oh, ow, pt, pl = geom
             args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
                                  pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
                                  s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
                                  h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
-            _lib.check(self.lib.clarus_hip_rows_split(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
-            return self._gemm("linear", a=rows, wt=self._wt2(w), c=out, m=m, n=nout, k=2 * k, lda=2 * k, ldc=nout,
-                              **epi)
+            fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
+            _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
+            wt = self._wt2(w) if self.prologue_split else self._wt(w)
+            return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, **epi)
         return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                           small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
 

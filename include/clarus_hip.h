@@ -102,7 +102,9 @@ typedef struct ClarusGemmArgs {
   int32_t tile;       /* 0 = library's choice; else a kernel / tile id for sweeps: 1-7 tiled
                          shapes, 8 / 9 W-resident streaming (4 / 8 channel blocks), 10 pipelined
                          LDS tile, 11 DMA-pipelined tile (bf16 A, no prologue, K % 32 == 0),
-                         13 DMA-pipelined 32x32-MFMA tile (bf16 A, no prologue, K % 64 == 0) */
+                         13 DMA-pipelined 32x32-MFMA tile (bf16 A, no prologue, K % 64 == 0),
+                         14 / 15 the same with 256 / 128 pixels x 256 channels per tile,
+                         16 streaming with a per-wave LDS ring (K <= 128 bf16 / 64 fp32) */
 } ClarusGemmArgs;
 
 /* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */
@@ -120,6 +122,17 @@ int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
  * ops/triton_cuda.py:101-108 (which round the prologue's output to the compute dtype instead)
  */
 int clarus_hip_rows_split(const ClarusGemmArgs* args, void* out, void* stream);
+
+/*
+ * Prologue pass rounded once: the same prologue as clarus_hip_rows_split, written as one bf16
+ * row of k elements, out[r] = bf16(v) (round to nearest even), out dense [m][k]. A plain bf16
+ * clarus_hip_gemm on out with the original k then computes what the reference's GPU path
+ * computes for a bf16 model: the prologue output rounded to the operand dtype, then a
+ * tensor-core product with fp32 accumulation. Same argument rules as clarus_hip_rows_split.
+ * replaces kernels/spatial.py:312 ln_rows (out_dtype = the compute dtype) and :342 mul_small,
+ * as called at ops/triton_cuda.py:104-110
+ */
+int clarus_hip_rows_prologue(const ClarusGemmArgs* args, void* out, void* stream);
 
 /*
  * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:

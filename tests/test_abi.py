@@ -56,5 +56,7 @@ def test_validation_rejects_before_launch(lib):
     a = _lib.GemmArgs(a=16, m=10, k=64, batch=1, lda=64, pro=0)
     assert lib.clarus_hip_rows_split(ctypes.byref(a), 16, None) == _lib.EINVAL  # no prologue
     assert b"prologue" in lib.clarus_hip_last_error()
+    assert lib.clarus_hip_rows_prologue(ctypes.byref(a), 16, None) == _lib.EINVAL  # no prologue
+    assert b"rows_prologue" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
