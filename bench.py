@@ -78,8 +78,8 @@ def summarize_trace(directory: str) -> None:
 
 def summarize_e2e(directory: str, top: int = 40) -> None:
     """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: launches from
-    the first intro_kernel (the NAFNet stem) on, grouped by (kernel, grid), divided by the number
-    of forwards in the trace (one intro_kernel each)."""
+    the first intro kernel (intro_mfma_kernel / intro_kernel, the NAFNet stem) on, grouped by
+    (kernel, grid), divided by the number of forwards in the trace (one intro kernel each)."""
     files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {directory}")
@@ -88,11 +88,14 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
         with open(f) as fh:
             rows += list(csv.DictReader(fh))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    first = next((i for i, r in enumerate(rows) if "intro_kernel" in r.get("Kernel_Name", "")), None)
+    def is_intro(r):
+        name = r.get("Kernel_Name", "")
+        return "intro_kernel" in name or "intro_mfma_kernel" in name
+    first = next((i for i, r in enumerate(rows) if is_intro(r)), None)
     if first is None:
-        raise SystemExit("no NAFNet forward (intro_kernel) in the trace")
+        raise SystemExit("no NAFNet forward (intro kernel) in the trace")
     e2e = rows[first:]
-    nfwd = sum(1 for r in e2e if "intro_kernel" in r.get("Kernel_Name", ""))
+    nfwd = sum(1 for r in e2e if is_intro(r))
     groups: dict = {}
     for r in e2e:
         name = r.get("Kernel_Name", "?").split("(")[0].replace("void ", "")

@@ -45,9 +45,10 @@ bool launch_conv_halo(GemmP& p, hipStream_t s) {
   // chunk offsets must stay inside the 1 KiB zero page: (cin / 32 - 1) * 64 + 64 <= 1024
   if (p.cin % CH_KC != 0 || p.cin > 448) return false;
   const bool up2 = p.up2 != 0;
-  // 64-channel tiles where the resident weights fit, else 32
+  // 64-channel tiles where the resident weights fit, else 32 (16 for at most 16 channels)
   const bool tr64 = p.n >= 64 && conv_halo_lds_bytes(64, p.cin, up2, 2) <= kLdsMax;
   if (tr64) return up2 ? launch_tr<64, true>(p, s) : launch_tr<64, false>(p, s);
+  if (p.n <= 16 && !up2) return launch_tr<16, false>(p, s);  // narrow outputs: half the MFMA work of 32
   return up2 ? launch_tr<32, true>(p, s) : launch_tr<32, false>(p, s);
 }
 

@@ -14,7 +14,9 @@
 //     block, 16 channels); two waves per SIMD hide each other's LDS latency.
 // The K loop of a tile is one chunk per step with a single barrier; the epilogue (bias,
 // LeakyReLU, out_scale, residual, 16-byte stores into a channel slice of the output) runs once
-// per tile outside it, and the next tile's first halo is already in flight by then.
+// per tile outside it, and the next tile's first halo is already in flight by then. NCHW fp32
+// output (c_mode NCHW, the NAFNet ending conv with its global residual) is stored per channel
+// plane; TR = 16 serves narrow outputs (cout <= 16, e.g. 3 image channels).
 #pragma once
 
 #include "gemm_lds.hpp"
@@ -211,6 +213,19 @@ __global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
         }
 #pragma unroll
         for (int i = 0; i < RUN; ++i) v[i] *= p.out_scale;
+        if (p.c_mode == CM_NCHW) {
+          // channel planes [img][n][H][W] (output and residual): the 16 lanes of a channel store
+          // 16 consecutive pixels of one row
+          const int64_t hw = (int64_t)H * W;
+          const int64_t o0 = ((int64_t)img * p.n + run0) * hw + (int64_t)oy * W + ox;
+#pragma unroll
+          for (int i = 0; i < RUN; ++i) {
+            if (run0 + i >= p.n) continue;
+            const int64_t o = o0 + i * hw;
+            store1(p.c, p.c_dt, o, p.has_res ? v[i] + load1(p.res, p.r_dt, o) : v[i]);
+          }
+          continue;
+        }
         const int64_t q = ((int64_t)img * H + oy) * W + ox;
         store_run<RUN>(p, v, q * p.ldc + run0, q * p.ldr + run0, run0, full_n);
       }

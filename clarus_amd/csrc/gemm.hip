@@ -311,8 +311,19 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                       cdiv(a->m, 128) * cdiv(a->n, 64) < ((int64_t)1 << 31);  // tile index in 31 bits
   const bool m32_ok = dma_ok && a->k % 64 == 0 && (!run_div || run_div % kGemmM32Run == 0) &&
                       epi32_tables_fit(a->n, a->gate != 0);  // bias / scale tables in LDS
+  // 2x2 stride-2 down conv with bf16 operands: space-to-depth rows on the 32x32 DMA-pipelined
+  // kernel (tile 13 or auto; tiles 1-7 keep the register-staged tiled kernel)
+  const bool s2d_m32 = a->a_mode == CLARUS_A_S2D && opm == OPM_BF16 && a->pro == PRO_NONE && a->batch == 1 &&
+                       p.cin % 32 == 0 && !run_div && epi32_tables_fit(a->n, a->gate != 0) &&
+                       cdiv(a->m, 128) * cdiv(a->n, 64) < ((int64_t)1 << 31);
   CLARUS_REQUIRE(a->tile != 11 || dma_ok, "gemm: the DMA-pipelined kernel does not take this problem");
-  CLARUS_REQUIRE(a->tile != 13 || m32_ok, "gemm: the 32x32 DMA-pipelined kernel does not take this problem");
+  CLARUS_REQUIRE(a->tile != 13 || m32_ok || s2d_m32,
+                 "gemm: the 32x32 DMA-pipelined kernel does not take this problem");
+  if (s2d_m32 && (a->tile == 0 || a->tile == 13)) {
+    p.s2d = 1;
+    launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
+    return check_launch("gemm");
+  }
   CLARUS_REQUIRE((a->tile != 14 && a->tile != 15) || m32_ok,
                  "gemm: the big-tile DMA-pipelined kernel does not take this problem");
   if (a->tile == 14 || a->tile == 15) {
@@ -380,8 +391,8 @@ extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
   const int opm = operand_mode(a->x_dtype, a->w_dtype, false);
   // output tiles with an LDS halo and resident weights (tile 0 = auto, 12 = force); the
   // implicit GEMM otherwise (tiles 1..7)
-  const bool halo_ok = opm == OPM_BF16 && a->c_mode == CLARUS_C_ROWS && a->cin % 32 == 0 &&
-                       a->batch * H * W < ((int64_t)1 << 31);
+  const bool halo_ok = opm == OPM_BF16 && (a->c_mode == CLARUS_C_ROWS || (a->c_mode == CLARUS_C_NCHW && !a->up2)) &&
+                       a->cin % 32 == 0 && a->batch * H * W < ((int64_t)1 << 31);
   CLARUS_REQUIRE(a->tile != 12 || halo_ok, "conv3x3: the halo-tile kernel does not take this problem");
   if (halo_ok && (a->tile == 0 || a->tile == 12)) {
     if (launch_conv_halo(p, (hipStream_t)stream)) return check_launch("conv3x3");
@@ -453,6 +464,95 @@ __global__ void __launch_bounds__(256) intro_kernel(const float* __restrict__ in
   }
 }
 
+// MFMA form for cout % 64 == 0: the 3 x 3 x 3 taps are K = 27 (padded to 28) of an fp32
+// 16x16x4 MFMA product D[channel][pixel] = W^T[channel][k] . A[k][pixel], fp32 products and
+// fp32 accumulation like the FMA kernel above (only the summation order differs). A wave takes
+// 16 consecutive pixels x 64 channels per step: lane l loads the 7 input values k = 4 s + l / 16
+// (s < 7) of pixel l % 16 straight from the NCHW planes (16 consecutive floats per tap row and
+// channel), holds its 28 W^T operands for the whole kernel, and issues 7 x 4 MFMAs. W^T rows are
+// permuted so lane group g = l / 16 ends with channels 8 g .. 8 g + 7 and 32 + 8 g .. 32 + 8 g + 7
+// of its pixel: each 16-byte store of the four groups covers 64 contiguous bytes of a pixel row.
+template <int ODT>
+__global__ void __launch_bounds__(256) intro_mfma_kernel(const float* __restrict__ inp, const float* __restrict__ wt,
+                                                         const float* __restrict__ bias, void* out, int m, int h,
+                                                         int w, int cout) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int hw = h * w;
+  const int ncg = cout >> 6;                  // 64-channel groups
+  const int nblk = (m + 15) >> 4;             // 16-pixel blocks
+  const int units = nblk * ncg;
+  int kc[7], koff[7], kdy[7], kdx[7];         // this lane's k of each step: channel plane, tap offsets
+#pragma unroll
+  for (int s = 0; s < 7; ++s) {
+    const int k = 4 * s + g;
+    const int kk = k < 27 ? k : 0;
+    const int tap = kk / 3, c = kk - 3 * tap;
+    kc[s] = k < 27 ? c : -1;
+    kdy[s] = tap / 3 - 1;
+    kdx[s] = tap - 3 * (tap / 3) - 1;
+    koff[s] = c * hw + kdy[s] * w + kdx[s];
+  }
+  int cg_cur = -1;
+  float wv[4][7], bv[16];
+  for (int u = blockIdx.x * 4 + wave; u < units; u += gridDim.x * 4) {
+    const int cg = u / nblk, blk = u - cg * nblk;
+    if (cg != cg_cur) {  // W^T operands and bias of the channel group (once per wave when ncg == 1)
+      cg_cur = cg;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const int ch = cg * 64 + (cb >> 1) * 32 + 8 * (j >> 2) + 4 * (cb & 1) + (j & 3);
+#pragma unroll
+        for (int s = 0; s < 7; ++s) wv[cb][s] = kc[s] >= 0 ? wt[(4 * s + g) * cout + ch] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bv[i] = bias[cg * 64 + (i >> 3) * 32 + 8 * g + (i & 7)];
+    }
+    const int q = blk * 16 + j;
+    const bool qok = q < m;
+    const int qq = qok ? q : m - 1;
+    const int img = qq / hw;
+    const int rr = qq - img * hw;
+    const int y = rr / w, x = rr - (rr / w) * w;
+    const float* plane = inp + (int64_t)img * 3 * hw + rr;
+    float a[7];
+#pragma unroll
+    for (int s = 0; s < 7; ++s) {
+      const int yy = y + kdy[s], xx = x + kdx[s];
+      const bool ok = kc[s] >= 0 && yy >= 0 && yy < h && xx >= 0 && xx < w;
+      a[s] = ok ? plane[koff[s]] : 0.f;
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 7; ++s) acc[cb] = mfma_f32(wv[cb][s], a[s], acc[cb]);
+    }
+    if (!qok) continue;
+    float v[16];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[(cb >> 1) * 8 + (cb & 1) * 4 + i] = acc[cb][i] + bv[(cb >> 1) * 8 + (cb & 1) * 4 + i];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int64_t oo = (int64_t)q * cout + cg * 64 + hf * 32 + 8 * g;
+      if constexpr (ODT == DT_BF16) {
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          r[i] = (unsigned)f32_to_bf16_bits(v[hf * 8 + 2 * i]) | ((unsigned)f32_to_bf16_bits(v[hf * 8 + 2 * i + 1]) << 16);
+        *reinterpret_cast<u32x4*>((unsigned short*)out + oo) = r;
+      } else {
+        *reinterpret_cast<f32x4*>((float*)out + oo) = f32x4{v[hf * 8], v[hf * 8 + 1], v[hf * 8 + 2], v[hf * 8 + 3]};
+        *reinterpret_cast<f32x4*>((float*)out + oo + 4) =
+            f32x4{v[hf * 8 + 4], v[hf * 8 + 5], v[hf * 8 + 6], v[hf * 8 + 7]};
+      }
+    }
+  }
+}
+
 extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, void* out,
                                    int32_t out_dtype, int64_t batch, int64_t h, int64_t w, int64_t cout,
                                    void* stream) {
@@ -464,6 +564,17 @@ extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const floa
   CLARUS_REQUIRE(batch * h * w * (cout / 8) < ((int64_t)1 << 31), "intro3x3: problem too large for 32-bit indexing");
   CLARUS_REQUIRE(aligned(out, 16) && aligned(wt, 16) && aligned(bias, 16), "intro3x3: 16-byte alignment");
   const int64_t m = batch * h * w;
+  if (cout % 64 == 0 && batch * h * w * 3 < ((int64_t)1 << 31)) {
+    const int64_t units = cdiv(m, 16) * (cout / 64);
+    const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(units, 4), 2048);
+    if (out_dtype == DT_BF16)
+      hipLaunchKernelGGL(intro_mfma_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, inp, wt, bias,
+                         out, (int)m, (int)h, (int)w, (int)cout);
+    else
+      hipLaunchKernelGGL(intro_mfma_kernel<DT_F32>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, inp, wt, bias,
+                         out, (int)m, (int)h, (int)w, (int)cout);
+    return check_launch("intro3x3");
+  }
   const int64_t work = m * (cout / 8);
   const size_t lds = (size_t)28 * cout * sizeof(float);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(work, 256), 2048);

@@ -53,6 +53,7 @@ struct GemmP {
   int h, w;          // AM_S2D / CM_SHUFFLE / AM_CONV3: input size; PRO_MUL: image size
   int oh, ow, pt, pl;
   int cin;           // AM_S2D / AM_CONV3 input channels
+  int s2d;           // gemm_mfma32_kernel: A rows are 2x2 stride-2 windows of an NHWC image (h, w, cin)
   int up2;           // AM_CONV3: nearest x2 input
   int pro, c_mode, act, m2_act;
   int has_res;

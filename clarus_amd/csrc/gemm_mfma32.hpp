@@ -29,6 +29,11 @@
 // channel 16 (l / 32) + j of its 32-row block: every lane owns 16 consecutive channels.
 // Memory waits are explicit: with two stages the chunk waited for is always the newest copy
 // group, so every wait is vmcnt(0) (it also covers an epilogue's loads and stores).
+// Space-to-depth rows (p.s2d, the 2x2 stride-2 down conv): A row q is the window of output
+// pixel q, k = (2 dy + dx) cin + c. Its first 2 cin elements are input row 2y at pixels 2x, 2x + 1
+// and its last 2 cin are input row 2y + 1 at the same pixels, each contiguous: a lane's copy
+// source starts at (2y, 2x) and jumps by (w - 2) cin elements once k reaches 2 cin (a chunk
+// boundary, since cin % 32 == 0).
 #pragma once
 
 #include "gemm_epi32.hpp"
@@ -47,6 +52,7 @@ constexpr int M32_RUN = 16;                       // consecutive output channels
 constexpr int M32_STAGES = 2;                     // LDS ring depth
 constexpr int M32_RING = M32_STAGES * M32_STAGE;  // 64 KiB
 constexpr int M32_LDS = M32_RING + EPI32_TABLE_FLOATS * 4;  // + epilogue tables: 80 KiB, two workgroups per CU
+static_assert(M32_ABYTES / 1024 == 4 * 4, "copies j < 4 of a lane are the A KiBs (4 waves)");
 
 __device__ __forceinline__ int m32_swz(int row, int unit) { return unit ^ ((row >> 1) & 7); }
 
@@ -103,7 +109,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       if (kib < 16) {
         int64_t q = (int64_t)pt * M32_P + row;
         if (q > p.m - 1) q = p.m - 1;  // rows past M: any valid row, its outputs are not stored
-        src_base[j] = A + (q * p.lda + unit * 8) * 2;
+        if (p.s2d) {
+          const int wo = p.w >> 1, hwo = (p.h >> 1) * wo;
+          const int64_t img = q / hwo;
+          const int r = (int)(q - img * hwo);
+          const int py = r / wo, px = r - py * wo;
+          src_base[j] = A + ((((img * p.h + 2 * py) * p.w + 2 * px) * p.cin) + unit * 8) * 2;
+        } else {
+          src_base[j] = A + (q * p.lda + unit * 8) * 2;
+        }
       } else {
         // W^T row `row` = wave-row wr, block rb, block row rr = 8 g + 4 h + i holds channel
         // 16 h + 4 g + i of its 32-channel run (gate: block rb is the SimpleGate half)
@@ -117,12 +131,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
   };
+  // space-to-depth: the A source jumps to input row 2y + 1 from chunk s2d_kc on
+  const int s2d_kc = p.s2d ? (2 * p.cin) / M32_KC : nch;
+  const int64_t s2d_jump = p.s2d ? (int64_t)(p.w - 2) * p.cin * 2 : 0;
   auto issue = [&]() __attribute__((always_inline)) {
     const int kb = is_chunk * (M32_KC * 2);
+    const int64_t ka = kb + (is_chunk >= s2d_kc ? s2d_jump : 0);  // A copies (j < 4: KiBs 0-15)
     unsigned char* st = ring + is_stage * M32_STAGE;
 #pragma unroll
     for (int j = 0; j < M32_COPIES; ++j)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src_base[j] + kb),
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src_base[j] + (j < 4 ? ka : kb)),
                                        (__attribute__((address_space(3))) void*)(st + (wave + 4 * j) * 1024), 16, 0,
                                        0);
     is_stage = is_stage + 1 == STAGES ? 0 : is_stage + 1;

@@ -10,6 +10,9 @@
 // inside the square root), :85-91 and :18-41 (the TLC map expanded over the image with clamped
 // coordinates), applied in fp32.
 //
+// Without a prologue (pro = none, fp32 rows) both passes only convert: the reference's fp32 A
+// operand rounded to the bf16 weights' dtype before the product (kernels/gemm.py:187-193).
+//
 // clarus_hip_rows_prologue writes the prologue output rounded once to bf16 (RNE), a row of K
 // elements, for a plain bf16 GEMM with the original K: the reference's GPU path for bf16 models
 // (kernels/spatial.py:312 ln_rows with out_dtype = the compute dtype, :342 mul_small; used at
@@ -79,7 +82,7 @@ __global__ void __launch_bounds__(256) rows_split_kernel(const SplitP p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[f].v[i] *= s.v[i];
       }
-    } else {  // LayerNorm (two-pass mean / variance) or RMS norm
+    } else if (p.pro != PRO_NONE) {  // LayerNorm (two-pass mean / variance) or RMS norm
       float mean = 0.f;
       if (p.pro == PRO_LN) {
         float s = 0.f;
@@ -144,8 +147,9 @@ static int rows_pass(const ClarusGemmArgs* a, void* out, void* stream, bool spli
   clear_error();
   CLARUS_REQUIRE(a != nullptr && a->a && out, "%s: null operand", what);
   CLARUS_REQUIRE(a->m > 0 && a->k > 0, "%s: empty problem", what);
-  CLARUS_REQUIRE(a->pro == PRO_LN || a->pro == PRO_RMS || a->pro == PRO_MUL,
-                 "%s: prologue %d is not LN, RMS or the map multiply", what, a->pro);
+  CLARUS_REQUIRE(a->pro == PRO_NONE || a->pro == PRO_LN || a->pro == PRO_RMS || a->pro == PRO_MUL,
+                 "%s: prologue %d is not none, LN, RMS or the map multiply", what, a->pro);
+  CLARUS_REQUIRE(a->pro != PRO_NONE || a->a_dtype == DT_F32, "%s: rows without a prologue must be fp32", what);
   CLARUS_REQUIRE(a->a_dtype == DT_F32 || a->a_dtype == DT_BF16, "%s: bad A dtype", what);
   CLARUS_REQUIRE(a->k % 8 == 0 && a->k <= 2048, "%s: K=%lld must be a multiple of 8, at most 2048", what,
                  (long long)a->k);

@@ -61,16 +61,15 @@ def _vec16(t: torch.Tensor, *strides: int) -> bool:
 @register_backend("hip")
 class HipOps(Backend):
     name = "hip"
-    # linear with a prologue (LN / RMS / TLC map) and bf16 weights takes the split-operand path
-    # (one prologue pass writing [hi | lo] bf16 rows, then a plain bf16 GEMM with K' = 2K) from
-    # this K on; shorter rows keep the prologue inside the streaming kernels (NAFNet-w64 720p
-    # forward measured at thresholds 128 / 256 / 512: 10.68 / 10.51 / 10.60 ms)
-    split_min_k = 256
-    # From split_min_k on, the prologue output of a bf16-weight GEMM is rounded once to bf16
-    # (clarus_hip_rows_prologue, then a plain GEMM with K) as in the reference's GPU path
-    # (ops/triton_cuda.py:104-110, kernels/gemm.py:164-186). True keeps it as [hi | lo]
-    # (clarus_hip_rows_split, K' = 2K): fp32-accurate products at twice the MFMA work and A bytes.
-    # NAFNet-w64 720p bf16 forward: split 10.77 ms.
+    # linear with a prologue (LN / RMS / TLC map) and bf16 weights runs the prologue as a
+    # separate pass from this K on, then a plain bf16 GEMM; shorter rows keep the prologue inside
+    # the streaming kernels. NAFNet-w64 720p bf16 forward at thresholds 128 / 256: 9.17-9.22 /
+    # 9.29-9.30 ms (rounded rows); 10.68 / 10.51 ms with split rows.
+    split_min_k = 128
+    # The pass rounds the prologue output once to bf16 (clarus_hip_rows_prologue, then the GEMM
+    # with K), as the reference's GPU path does (ops/triton_cuda.py:104-110, kernels/gemm.py:
+    # 164-186). True writes [hi | lo] rows instead (clarus_hip_rows_split, K' = 2K on [W | W]):
+    # fp32-accurate products at twice the MFMA work and A bytes (forward 10.88 vs 9.27 ms).
     prologue_split = False
 
     def __init__(self, dtype, device):
@@ -226,6 +225,14 @@ class HipOps(Backend):
             raise Unsupported("down: bf16 / fp32, cin % 8 == 0, at least 2x2 input")
         wt = self.cached(w4d, "s2d", lambda t: t.permute(0, 2, 3, 1).reshape(t.shape[0], -1).contiguous())
         out = torch.empty((n, h // 2, wd // 2, cout), device=x.device, dtype=odt)
+        if x.dtype == torch.float32 and wt.dtype == torch.bfloat16 and not self.prologue_split:
+            # fp32 activations with bf16 weights: rounded once to bf16 like the reference's fp32 A
+            # operand (kernels/gemm.py:187-193), then the bf16 space-to-depth GEMM
+            xb = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+            args = _lib.GemmArgs(a=x.data_ptr(), m=n * h * wd, k=c, batch=1, lda=c, a_dtype=_lib.F32,
+                                 pro=_lib.PRO_NONE)
+            _lib.check(self.lib.clarus_hip_rows_prologue(ctypes.byref(args), xb.data_ptr(), self._stream(x)), "down")
+            x = xb
         return self._gemm("down", a=x, wt=wt, c=out, m=n * (h // 2) * (wd // 2), n=cout, k=4 * c, lda=c, ldc=cout,
                           bias=self._bias(b), a_mode=_lib.A_S2D, geom=(h, wd, 0, 0, 0, 0))
 

@@ -128,7 +128,9 @@ int clarus_hip_rows_split(const ClarusGemmArgs* args, void* out, void* stream);
  * row of k elements, out[r] = bf16(v) (round to nearest even), out dense [m][k]. A plain bf16
  * clarus_hip_gemm on out with the original k then computes what the reference's GPU path
  * computes for a bf16 model: the prologue output rounded to the operand dtype, then a
- * tensor-core product with fp32 accumulation. Same argument rules as clarus_hip_rows_split.
+ * tensor-core product with fp32 accumulation. Same argument rules as clarus_hip_rows_split;
+ * both also take pro = none on fp32 rows (a plain conversion, the reference's fp32 A operand
+ * rounded to the weights' dtype, kernels/gemm.py:187-193).
  * replaces kernels/spatial.py:312 ln_rows (out_dtype = the compute dtype) and :342 mul_small,
  * as called at ops/triton_cuda.py:104-110
  */

@@ -53,10 +53,11 @@ def test_validation_rejects_before_launch(lib):
     assert lib.clarus_hip_conv3x3(ctypes.byref(cv), None) == _lib.EINVAL  # cin % 8 != 0
     assert lib.clarus_hip_channel_attention(16, 1, 16, 16, 1, 64, 30, 2, 16, 0, None) == _lib.EINVAL
     assert lib.clarus_hip_patch_corr(16, 0, 0, 0, 0, 16, 16, 16, 1, 12, 16, 8, None) == _lib.EINVAL  # h % 8
-    a = _lib.GemmArgs(a=16, m=10, k=64, batch=1, lda=64, pro=0)
-    assert lib.clarus_hip_rows_split(ctypes.byref(a), 16, None) == _lib.EINVAL  # no prologue
-    assert b"prologue" in lib.clarus_hip_last_error()
-    assert lib.clarus_hip_rows_prologue(ctypes.byref(a), 16, None) == _lib.EINVAL  # no prologue
+    a = _lib.GemmArgs(a=16, m=10, k=64, batch=1, lda=64, pro=0, a_dtype=_lib.BF16)
+    assert lib.clarus_hip_rows_split(ctypes.byref(a), 16, None) == _lib.EINVAL  # bf16 rows, no prologue
+    assert b"fp32" in lib.clarus_hip_last_error()
+    a.pro = 9
+    assert lib.clarus_hip_rows_prologue(ctypes.byref(a), 16, None) == _lib.EINVAL  # unknown prologue
     assert b"rows_prologue" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0

@@ -116,7 +116,12 @@ def test_config3_patch_filter(c, h, w, hip_f32):
 @pytest.mark.parametrize("h,w,k,nout,ln,res", [(64, 96, 48, 288, True, False), (40, 64, 192, 256, True, False),
                                                (90, 45, 144, 48, False, True), (52, 76, 96, 96, "rms", True)])
 def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
-    """tools/test_kernels.py:237-245 cases."""
+    """tools/test_kernels.py:237-245 cases. With LN over K >= HipOps.split_min_k the normalised
+    rows are rounded once to bf16, as the reference's GPU path does (ops/triton_cuda.py:269-271):
+    then the bf16 rule holds against that rounding emulated on the oracle, and the fp32 oracle is
+    met within the reference's own bound for this op, 2e-2 of the output scale
+    (tools/test_kernels.py:28-32, :242)."""
+    from clarus_amd.hip_ops import HipOps
     g = gen(4)
     x, f = rnd(g, 1, h, w, k).bfloat16(), rnd(g, nout, 8, 5)
     wl, b = rnd(g, k, nout, scale=k ** -0.5).bfloat16(), rnd(g, nout)
@@ -124,7 +129,15 @@ def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
     got = hip_bf16.linear_patch_filter(x.cuda(), wl.cuda(), b.cuda(), f.cuda(), ln=ln, ln_eps=1e-5,
                                        residual=rr.cuda() if res else None)
     ref = REF.linear_patch_filter(x, wl, b, f, ln=ln, ln_eps=1e-5, residual=rr)
-    assert_bf16(got.cpu(), ref, f"linear_patch_filter {h}x{w} k{k} ln={ln}")
+    what = f"linear_patch_filter {h}x{w} k{k} ln={ln}"
+    rounded = (ln and not HipOps.prologue_split and HipOps.split_min_k <= k <= 2048 and k % 32 == 0)
+    if not rounded:
+        assert_bf16(got.cpu(), ref, what)
+        return
+    xr = REF.ln(x.float(), 1e-5, rms=(ln == "rms")).to(torch.bfloat16)  # the rows the GPU path rounds
+    assert_bf16(got.cpu(), REF.linear_patch_filter(xr, wl, b, f, ln=False, residual=rr), what + " (rounded rows)")
+    err = (got.cpu().double() - ref.double()).abs().max().item() / ref.abs().max().item()
+    assert err < 2e-2, f"{what}: {err:.3e} of the output scale against the fp32 oracle"
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])

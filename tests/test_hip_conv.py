@@ -123,18 +123,23 @@ def test_conv3x3_kernels_agree(tile, hip_bf16):
 
 
 def test_ending_and_intro(hip_bf16):
-    """ending: fp32 input at |x| ~ 300, NCHW fp32 output + global residual; intro 3 -> 64 / 48."""
+    """ending: fp32 input at |x| ~ 300 (implicit GEMM) and bf16 input (halo-tile kernel, 16-channel
+    tile, NCHW fp32 stores), NCHW fp32 output + global residual; intro 3 -> 64 / 128 (fp32 MFMA
+    kernel) and 48 (FMA kernel)."""
     g = gen(4)
     n, h, w = 2, 19, 27
     x3 = torch.rand(n, 3, h, w, generator=g)
-    xe = rnd(g, n, h, w, 64, scale=300.0)
-    we, be = rnd(g, 3, 64, 3, 3, scale=0.1, dtype=torch.bfloat16), rnd(g, 3)
-    got = hip_bf16.ending(xe.cuda(), we.cuda(), be.cuda(), x3.cuda())
-    assert_fp32(got.cpu(), REF.ending(xe, we, be, x3), what="ending fp32-in NCHW + res")
-    for c in (64, 48):
+    for xdt, mag in ((torch.float32, 300.0), (torch.bfloat16, 1.0)):
+        xe = rnd(g, n, h, w, 64, scale=mag).to(xdt)
+        we, be = rnd(g, 3, 64, 3, 3, scale=0.1, dtype=torch.bfloat16), rnd(g, 3)
+        got = hip_bf16.ending(xe.cuda(), we.cuda(), be.cuda(), x3.cuda())
+        assert_fp32(got.cpu(), REF.ending(xe, we, be, x3), what=f"ending {xdt} NCHW + res")
+    for c in (64, 128, 48):
         wi, bi = rnd(g, c, 3, 3, 3, scale=0.3), rnd(g, c)
         got = hip_bf16.intro(x3.cuda(), wi.cuda(), bi.cuda(), out_dtype=torch.float32)
         assert_fp32(got.cpu(), REF.intro(x3, wi, bi, out_dtype=torch.float32), what=f"intro 3->{c}")
+        got = hip_bf16.intro(x3.cuda(), wi.cuda(), bi.cuda())
+        check(got.cpu(), REF.intro(x3, wi, bi, out_dtype=torch.float32), what=f"intro 3->{c} bf16")
 
 
 @pytest.mark.parametrize("mag", [2.0 ** -18, 1.0, 6e4, 1e7])

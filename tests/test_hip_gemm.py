@@ -7,7 +7,7 @@ configs 1 (fp32 NAFNet pointwise chain) and 2 (NAFNet-w64 720p pointwise GEMMs, 
 Tolerances: tests/_tol.py (fp32: 1e-5 relative; bf16: 2e-2 absolute up to rounding flips).
 bf16-weight GEMMs whose prologue (LN / RMS / TLC map) runs over K >= HipOps.split_min_k round the
 prologue output once to bf16 by default, as the reference's GPU path does
-(ops/triton_cuda.py:104-110): those results are held to 5e-4 relative against that rounding
+(ops/triton_cuda.py:104-110): those results are held to 2e-3 relative against that rounding
 emulated on the oracle, and against the fp32 oracle to the bound one bf16 rounding of each
 prologue element allows (check_prologue); with HipOps.prologue_split they keep the fp32 tolerance.
 """
@@ -85,14 +85,16 @@ def rounding_bound(a, wt, b=None, gate=False, act=None, scale=None):
 
 def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6, rel=1e-5, **kw):
     """fp32-output prologue GEMM against the oracle. With the prologue rounded once to bf16
-    (rounds_prologue): within 5e-4 relative of that rounding emulated on the oracle (the
-    reference GPU path's numerics, kernels/gemm.py:164-186), and within rounding_bound (+ 1e-5
+    (rounds_prologue): within 2e-3 relative of that rounding emulated on the oracle (the
+    reference GPU path's numerics, kernels/gemm.py:164-186; elements whose fp32 prologue value
+    sits at a rounding midpoint may round the other way, each moving an output by 2^-8 |a_i w_ij|;
+    the rounding itself is pinned by test_rows_prologue_abi), and within rounding_bound (+ 1e-5
     of the output scale for summation order) of the fp32 oracle. Otherwise the fp32 rule."""
     ref = REF.linear(x, wt, b, ln=ln, mul=mul, ln_eps=ln_eps, **kw)
     if not rounds_prologue(k):
         return assert_fp32(got, ref, rel=rel, what=what)
     a = _prologue_rows(x, mul, ln, ln_eps)
-    assert_fp32(got, REF.linear(a.to(torch.bfloat16), wt, b, **kw), rel=5e-4,
+    assert_fp32(got, REF.linear(a.to(torch.bfloat16), wt, b, **kw), rel=2e-3,
                 what=what + " (vs the bf16-rounded prologue)")
     bound = rounding_bound(a, wt, b, kw.get("gate", False), kw.get("act"), kw.get("scale"))
     d = (got.double() - ref.double()).abs()
@@ -503,22 +505,63 @@ def test_linear_fp32_input_range(mag, hip_bf16):
 
 # --------------------------------------------------------------------- down / up
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hh,ww", [(14, 22), (15, 23)])
-def test_down(dt, hh, ww, hip_bf16, hip_f32):
-    """2x2 stride-2 conv as GEMM with space-to-depth A (tools/test_kernels.py:79-88); odd sizes floor."""
+@pytest.mark.parametrize("hh,ww,cin", [(14, 22, 32), (15, 23, 32), (15, 23, 96), (9, 41, 64)])
+def test_down(dt, hh, ww, cin, hip_bf16, hip_f32):
+    """2x2 stride-2 conv as GEMM with space-to-depth A (tools/test_kernels.py:79-88); odd sizes floor.
+    bf16 takes the 32x32 DMA-pipelined kernel (A source jumping to row 2y + 1 at k = 2 cin)."""
     hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
     g = gen(7)
-    x, w4, b = rnd(g, 2, hh, ww, 32, dtype=dt), rnd(g, 64, 32, 2, 2, scale=0.1, dtype=dt), rnd(g, 64)
+    x, w4, b = rnd(g, 2, hh, ww, cin, dtype=dt), rnd(g, 64, cin, 2, 2, scale=0.1, dtype=dt), rnd(g, 64)
     got = hip.down(*dev(x, w4, b))
-    check(got.cpu(), REF.down(x, w4, b), f"down {hh}x{ww} {dt}")
+    check(got.cpu(), REF.down(x, w4, b), f"down {hh}x{ww} cin {cin} {dt}")
 
 
-def test_down_fp32_input(hip_bf16):
-    """fp32 activations into a bf16-weight down conv (tools/test_kernels.py:154-163)."""
+@pytest.mark.parametrize("tile", [0, 1, 13])
+def test_down_kernels_agree(tile, hip_bf16):
+    """A NAFNet-like down conv (many 128-pixel tiles, output rows not a multiple of the tile)
+    through the C ABI: the space-to-depth DMA kernel (0 = auto, 13) and the tiled kernel (1)."""
+    import ctypes
+
+    from clarus_amd import _lib
+    g = gen(71)
+    n, hh, ww, cin, cout = 1, 46, 82, 128, 256
+    x, w4, b = rnd(g, n, hh, ww, cin, dtype=torch.bfloat16), rnd(g, cout, cin, 2, 2, scale=0.05, dtype=torch.bfloat16), rnd(g, cout)
+    ref = REF.down(x, w4, b)
+    wt = w4.permute(0, 2, 3, 1).reshape(cout, -1).contiguous().cuda()
+    xd, bd = x.cuda(), b.cuda()
+    out = torch.empty(n, hh // 2, ww // 2, cout, device="cuda", dtype=torch.float32)
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=wt.data_ptr(), c=out.data_ptr(), bias=bd.data_ptr(),
+                         m=n * (hh // 2) * (ww // 2), n=cout, k=4 * cin, batch=1, lda=cin, ldc=cout,
+                         a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.F32, a_mode=_lib.A_S2D,
+                         h=hh, w=ww, out_scale=1.0, tile=tile)
+    _lib.check(_lib.load().clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "gemm")
+    assert_fp32(out.cpu(), ref, rel=1e-5, what=f"down tile {tile}")
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_down_fp32_input(split, hip_bf16):
+    """fp32 activations into a bf16-weight down conv (tools/test_kernels.py:154-163). By default
+    they are rounded once to bf16 like the reference's fp32 A operand (kernels/gemm.py:187-193):
+    within 1e-5 of that rounding emulated on the oracle (bf16 products are exact in fp32), and
+    within 2^-9 sum |x||w| of the fp32 oracle; with prologue_split, the fp32 rule."""
+    from clarus_amd.hip_ops import HipOps
     g = gen(8)
     x, w4, b = rnd(g, 2, 18, 26, 32, scale=1000.0), rnd(g, 64, 32, 2, 2, scale=0.1, dtype=torch.bfloat16), rnd(g, 64)
-    got = hip_bf16.down(*dev(x, w4, b), out_dtype=torch.float32)
-    assert_fp32(got.cpu(), REF.down(x, w4, b), rel=1e-5, what="down fp32-in")
+    saved = HipOps.prologue_split
+    try:
+        HipOps.prologue_split = split
+        got = hip_bf16.down(*dev(x, w4, b), out_dtype=torch.float32).cpu()
+    finally:
+        HipOps.prologue_split = saved
+    ref = REF.down(x, w4, b)
+    if split:
+        assert_fp32(got, ref, rel=1e-5, what="down fp32-in split")
+        return
+    assert_fp32(got, REF.down(x.to(torch.bfloat16), w4, b), rel=1e-5, what="down fp32-in vs rounded x")
+    bound = (2.0 ** -9) * (1 + 2.0 ** -7) * REF.down(x.abs(), w4.abs(), None).double()
+    d = (got.double() - ref.double()).abs()
+    assert bool((d <= bound + 1e-5 * ref.abs().max().item()).all()), f"down fp32-in: max|d| {d.max().item():.3e}"
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
