@@ -199,8 +199,10 @@ __global__ void __launch_bounds__(256) box_pass_kernel(const BoxPass p) {
   double sa[E], sb[E];
 #pragma unroll
   for (int c = 0; c < E; ++c) sa[c] = sb[c] = 0.0;
+  // rows of the last batch stay in registers; when the thread's positions fit one batch
+  // (k <= BOX_BATCH T) the recurrence below reuses them instead of reloading
+  u32x4 va[BOX_BATCH], vb[BOX_BATCH];
   for (int j0 = 0; j0 < nj; j0 += BOX_BATCH) {
-    u32x4 va[BOX_BATCH], vb[BOX_BATCH];
     load_rows(j0, va, vb);
 #pragma unroll
     for (int j = 0; j < BOX_BATCH; ++j)
@@ -226,10 +228,9 @@ __global__ void __launch_bounds__(256) box_pass_kernel(const BoxPass p) {
   }
   if (!live) return;
   unsigned char* yp = (unsigned char*)p.y + (plane * p.y_plane + e0) * YES;
-  // the recurrence over this thread's positions (rows re-read: L1 / L2 hits)
+  // the recurrence over this thread's positions (more than one batch: rows re-read, L1 / L2 hits)
   for (int j0 = 0; j0 < nj; j0 += BOX_BATCH) {
-    u32x4 va[BOX_BATCH], vb[BOX_BATCH];
-    load_rows(j0, va, vb);
+    if (nj > BOX_BATCH) load_rows(j0, va, vb);
 #pragma unroll
     for (int j = 0; j < BOX_BATCH; ++j) {
       const int64_t i = r0 + j0 + j;
