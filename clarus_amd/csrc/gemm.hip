@@ -330,7 +330,10 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     launch_gemm_big(p, a->gate != 0, a->tile == 14 ? 2 : 1, (hipStream_t)stream);
     return check_launch("gemm");
   }
-  if (a->tile == 13 || (m32_ok && a->tile == 0 && (auto_dma || use_lds))) {
+  // K <= 256 with a residual stays on the 16x16 DMA kernel (c256 c->c+scale+res: 31.2 vs 35.6 us
+  // and 31.2 vs 32.4 in two runs; K = 512 with an fp32 residual: 25.2 vs 28.6 on 32x32)
+  const bool m32_auto = m32_ok && a->tile == 0 && (auto_dma || use_lds) && !(a->res && a->k <= 256);
+  if (a->tile == 13 || m32_auto) {
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
   }
