@@ -247,18 +247,19 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     const int ks = rowstream_ks_for(a->k, a->a_dtype);
     const int er = a->res ? esize(a->r_dtype) : 2;
     const bool res_ok = !a->res || (p.vec_res == 2 && a->n % (16 / er) == 0 && !a->gate);
-    const int nb = (a->n <= 64 || a->gate) ? 4 : (run_div && run_div % 32 ? 4 : 8);
+    const int nb = (a->n <= 64 || a->gate || a->tile == 17) ? 4 : (run_div && run_div % 32 ? 4 : 8);
     const bool pro_ok = a->pro == PRO_NONE ||
                         (opm == OPM_SPLIT && a->batch == 1 &&
                          (a->pro == PRO_LN || a->pro == PRO_RMS || (a->pro == PRO_MUL && a->s_dtype == DT_BF16)));
     const bool ring_ok = a->a_mode == CLARUS_A_ROWS && pro_ok && ks && res_ok &&
                          (opm != OPM_SPLIT || a->a_dtype == DT_F32 || a->pro != PRO_NONE) &&
                          (!run_div || (run_div % (4 * nb) == 0 && a->batch == 1));
-    CLARUS_REQUIRE(a->tile != 16 || ring_ok, "gemm: the ring streaming kernel does not take this problem");
+    CLARUS_REQUIRE((a->tile != 16 && a->tile != 17) || ring_ok,
+                   "gemm: the ring streaming kernel does not take this problem");
     // K <= 128 with a gate, or with a row-layout residual (twice the ring slot: one 4-wave
     // workgroup per CU) stays on the other kernels (c128 c->c: 52 vs 46 us on the 64 x 64 tiles)
     const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || (!a->gate && (!a->res || run_div)));
-    if (a->tile == 16 || ring_auto) {
+    if (a->tile == 16 || a->tile == 17 || ring_auto) {
       GemmP q = p;
       q.ptiles = 0;
       // 8 channel blocks when the ring still fits next to W^T, else 4

@@ -71,6 +71,12 @@ class HipOps(Backend):
     # 164-186). True writes [hi | lo] rows instead (clarus_hip_rows_split, K' = 2K on [W | W]):
     # fp32-accurate products at twice the MFMA work and A bytes (forward 10.88 vs 9.27 ms).
     prologue_split = False
+    # A plain bf16 GEMM with a residual and N = 512 (NAFNet level 3: conv3 and conv5, whose
+    # outputs the next linear normalises) also writes the normalised bf16 rows of its output in
+    # its epilogue (clarus_hip_gemm_ln_rows), with the eps / mode of the last LayerNorm prologue
+    # this backend ran; a linear(ln=...) on exactly that output (same tensor and version, same
+    # eps and mode) takes those rows instead of running the prologue pass.
+    fuse_ln_rows = True
 
     def __init__(self, dtype, device):
         super().__init__(dtype, device)
@@ -93,6 +99,8 @@ class HipOps(Backend):
         except (OSError, RuntimeError) as exc:
             raise BackendUnavailable(f"libclarus_hip.so: {exc}") from exc
         self.dev = dev
+        self._ln_hint = None  # (eps, rms) of the last LN / RMS prologue
+        self._ln_next = None  # (output, version, data_ptr, eps, rms, rows) from clarus_hip_gemm_ln_rows
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -197,22 +205,61 @@ class HipOps(Backend):
         epi = dict(bias=self._bias(bias), scale=self._bias(scale), res=residual, ldr=nout, gate=gate,
                    act=_lib.ACT_GELU if act == "gelu" else 0)
         m = n * h * wd
+        if ln:
+            self._ln_hint = (float(ln_eps), ln == "rms")
         if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0:
             # the separate prologue pass of triton_cuda.py:104-110 (ln_rows / mul_small), then a
-            # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K)
+            # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K); LN rows
+            # the producing GEMM already wrote are taken as they are
             kk = 2 * k if self.prologue_split else k
-            rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
-            hh, ww, oh, ow, pt, pl = geom
-            args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
-                                 pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
-                                 s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
-                                 h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
-            fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
-            _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
+            rows = self._take_ln_rows(x, ln, ln_eps) if (ln and not self.prologue_split) else None
+            if rows is None:
+                rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
+                hh, ww, oh, ow, pt, pl = geom
+                args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
+                                     pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
+                                     s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
+                                     h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
+                fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
+                _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
             wt = self._wt2(w) if self.prologue_split else self._wt(w)
+            if self._ln_rows_ok(rows, wt, nout, kk, gate, act, residual):
+                return self._gemm_ln_rows(a=rows, wt=wt, c=out, m=m, k=kk, **epi)
             return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, **epi)
-        return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
+        wt = self._wt(w)
+        if pro == _lib.PRO_NONE and self._ln_rows_ok(x, wt, nout, k, gate, act, residual):
+            return self._gemm_ln_rows(a=x, wt=wt, c=out, m=m, k=k, **epi)
+        return self._gemm("linear", a=x, wt=wt, c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                           small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
+
+    # ---- GEMMs that also write the normalised rows of their output (clarus_hip_gemm_ln_rows)
+    def _ln_rows_ok(self, a, wt, nout, k, gate, act, residual) -> bool:
+        return (self.fuse_ln_rows and not self.prologue_split and self._ln_hint is not None
+                and residual is not None and not gate and act is None and nout == 512 and k % 64 == 0
+                and a.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16 and a.is_contiguous())
+
+    def _gemm_ln_rows(self, *, a, wt, c, m, k, bias, scale, res, ldr, gate, act):
+        eps, rms = self._ln_hint
+        n = c.shape[-1]
+        rows = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
+        args = _lib.GemmArgs(
+            a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
+            res=_lib.ptr(res), m=m, n=n, k=k, batch=1, lda=k, ldc=n, ldr=ldr,
+            a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(c.dtype),
+            r_dtype=_lib.dtype_code(res.dtype) if res is not None else 0, out_scale=1.0)
+        _lib.check(self.lib.clarus_hip_gemm_ln_rows(ctypes.byref(args), rows.data_ptr(), eps, int(rms),
+                                                    self._stream(a)), "linear")
+        self._ln_next = (c, c._version, c.data_ptr(), eps, rms, rows)
+        return c
+
+    def _take_ln_rows(self, x, ln, ln_eps):
+        e = self._ln_next
+        if e is None or e[0] is not x or x._version != e[1] or x.data_ptr() != e[2]:
+            return None
+        if e[3] != float(ln_eps) or e[4] != (ln == "rms"):
+            return None
+        self._ln_next = None
+        return e[5]
 
     def down(self, x, w4d, b, out_dtype=None):
         if tuple(w4d.shape[-2:]) != (2, 2) or not _dense(x, b):

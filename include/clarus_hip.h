@@ -104,7 +104,8 @@ typedef struct ClarusGemmArgs {
                          LDS tile, 11 DMA-pipelined tile (bf16 A, no prologue, K % 32 == 0),
                          13 DMA-pipelined 32x32-MFMA tile (bf16 A, no prologue, K % 64 == 0),
                          14 / 15 the same with 256 / 128 pixels x 256 channels per tile,
-                         16 streaming with a per-wave LDS ring (K <= 128 bf16 / 64 fp32) */
+                         16 / 17 streaming with a per-wave LDS ring (K <= 128 bf16 / 64 fp32;
+                         17: 4 channel blocks per workgroup) */
 } ClarusGemmArgs;
 
 /* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */
@@ -135,6 +136,18 @@ int clarus_hip_rows_split(const ClarusGemmArgs* args, void* out, void* stream);
  * as called at ops/triton_cuda.py:104-110
  */
 int clarus_hip_rows_prologue(const ClarusGemmArgs* args, void* out, void* stream);
+
+/*
+ * clarus_hip_gemm (plain bf16 rows: no prologue, gate, activation, batch or pixel shuffle,
+ * N = 512, K % 64 == 0; bias, scale, residual and the output as in clarus_hip_gemm) whose
+ * epilogue also writes ln_out[m][512] (bf16, dense): the output rows normalised with two-pass
+ * LayerNorm (rms = 0) or RMS norm (rms = 1), eps inside the square root, rounded once to bf16;
+ * what clarus_hip_rows_prologue would write for those rows. A tile covers whole rows.
+ * No counterpart in the reference: it fuses its fused_gemm (kernels/gemm.py:353-400) with the
+ * ln_rows pass of the next GEMM (kernels/spatial.py:312, ops/triton_cuda.py:104) for callers
+ * that normalise a GEMM's output next (NAFNet conv3 -> conv4, conv5 -> conv1).
+ */
+int clarus_hip_gemm_ln_rows(const ClarusGemmArgs* args, void* ln_out, float eps, int32_t rms, void* stream);
 
 /*
  * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:

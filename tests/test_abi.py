@@ -59,5 +59,9 @@ def test_validation_rejects_before_launch(lib):
     a.pro = 9
     assert lib.clarus_hip_rows_prologue(ctypes.byref(a), 16, None) == _lib.EINVAL  # unknown prologue
     assert b"rows_prologue" in lib.clarus_hip_last_error()
+    a = _lib.GemmArgs(a=16, wt=16, c=16, m=10, n=256, k=64, batch=1, lda=64, ldc=256,
+                      a_dtype=_lib.BF16, w_dtype=_lib.BF16)
+    assert lib.clarus_hip_gemm_ln_rows(ctypes.byref(a), 16, 1e-6, 0, None) == _lib.EINVAL  # N != 512
+    assert b"512" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0

@@ -453,6 +453,92 @@ def test_rows_prologue_abi(k, pro, hip_bf16):
     assert differ <= max(2, 1e-3 * o.numel()), f"{differ} elements differ from RNE(v)"
 
 
+@pytest.mark.parametrize("m,k,odt,rdt,rms", [(1000, 512, torch.float32, torch.float32, 0),
+                                              (4859, 512, torch.float32, torch.float32, 1),
+                                              (777, 64, torch.bfloat16, torch.bfloat16, 0),
+                                              (130, 1024, torch.float32, None, 0)])
+def test_gemm_ln_rows_abi(m, k, odt, rdt, rms, hip_bf16):
+    """Through the C ABI: clarus_hip_gemm_ln_rows writes the same output as clarus_hip_gemm (bias,
+    scale, residual; row tiles of 64 pixels, M tails), and its normalised rows are correct roundings
+    of the fp64 LayerNorm / RMS of that output (every element within half a bf16 ulp plus fp32
+    noise, all but a few equal to the RNE rounding, as clarus_hip_rows_prologue's)."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(44)
+    n = 512
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    wt = rnd(g, n, k, scale=k ** -0.5, dtype=torch.bfloat16)  # W^T [N][K]
+    b, sc = rnd(g, n), rnd(g, n)
+    res = (3 + rnd(g, m, n)).to(rdt) if rdt is not None else None
+    dv = [t.cuda() if t is not None else None for t in (x, wt, b, sc, res)]
+    outs = []
+    for fused in (False, True):
+        out = torch.empty(m, n, device="cuda", dtype=odt)
+        rows = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        args = _lib.GemmArgs(a=dv[0].data_ptr(), wt=dv[1].data_ptr(), c=out.data_ptr(), bias=dv[2].data_ptr(),
+                             scale=dv[3].data_ptr(), res=_lib.ptr(dv[4]), m=m, n=n, k=k, batch=1, lda=k, ldc=n,
+                             ldr=n, a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+                             r_dtype=_lib.dtype_code(rdt) if rdt is not None else 0, out_scale=1.0)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if fused:
+            _lib.check(lib.clarus_hip_gemm_ln_rows(ctypes.byref(args), rows.data_ptr(), 1e-6, rms, st), "gemm_ln_rows")
+        else:
+            _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), st), "gemm")
+        outs.append((out.cpu(), rows.cpu()))
+    (y0, _), (y1, r1) = outs
+    ref = REF.linear(x, wt.t(), b, scale=sc, residual=res.reshape(m, n) if res is not None else None)
+    if odt == torch.float32:
+        assert_fp32(y1, ref, rel=1e-5, what="gemm_ln_rows output")
+    else:
+        assert_bf16(y1, ref, what="gemm_ln_rows output")
+    d = (y1.double() - y0.double()).abs().max().item()
+    assert d <= 1e-6 * y0.double().abs().max().item() + (0 if odt == torch.float32 else 2.0 ** -7 * y0.double().abs().max().item()), d
+    y64 = y1.double()
+    if rms:
+        v = y64 / torch.sqrt(y64.square().mean(-1, keepdim=True) + 1e-6)
+    else:
+        c = y64 - y64.mean(-1, keepdim=True)
+        v = c / torch.sqrt(c.square().mean(-1, keepdim=True) + 1e-6)
+    o = r1.double()
+    slack = 0.5 * bf16_ulp(v) * (1 + 1e-4) + 2e-6 * (1 + v.abs())
+    assert bool(((o - v).abs() <= slack).all()), f"rows not a rounding of LN(y): max {(o - v).abs().max().item():.3e}"
+    differ = int((o != v.to(torch.bfloat16).double()).sum())
+    assert differ <= max(2, 1e-3 * o.numel()), f"{differ} rows elements differ from RNE(LN(y))"
+
+
+def test_linear_fuses_ln_rows(hip_bf16):
+    """HipOps: a residual-stream GEMM with N = 512 followed by a LayerNorm linear on its output
+    (NAFNet level 3) gives the same results with and without the fused normalised rows (the same
+    rounding of the same fp32 rows; the fused rows come from a different summation order of the
+    statistics, so a few elements may round the other way)."""
+    from clarus_amd.hip_ops import HipOps
+    g = gen(45)
+    x = rnd(g, 1, 30, 41, 512, dtype=torch.bfloat16).cuda()
+    w3, b3 = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 512).cuda()
+    w4, b4 = rnd(g, 512, 1024, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 1024).cuda()
+    beta, inp = rnd(g, 512).cuda(), (2 + rnd(g, 1, 30, 41, 512)).cuda()
+    res = []
+    saved = HipOps.fuse_ln_rows
+    try:
+        for fuse in (False, True):
+            HipOps.fuse_ln_rows = fuse
+            hip_bf16._ln_next = None
+            hip_bf16.linear(inp.to(torch.bfloat16), w4, b4, ln=True, gate=True)  # sets the LN hint (eps 1e-6)
+            y = hip_bf16.linear(x, w3, b3, scale=beta, residual=inp, out_dtype=torch.float32)
+            taken = hip_bf16._ln_next is not None
+            z = hip_bf16.linear(y, w4, b4, ln=True, gate=True)
+            assert taken == fuse and hip_bf16._ln_next is None
+            res.append((y.cpu(), z.cpu()))
+    finally:
+        HipOps.fuse_ln_rows = saved
+    (y0, z0), (y1, z1) = res
+    assert torch.equal(y0, y1)
+    d = (z0.float() - z1.float()).abs()
+    assert (d > 2e-2).float().mean().item() <= 1e-3 and d.max().item() <= 0.1, d.max().item()
+
+
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
 def test_linear_range(k, nout, gate, hip_bf16):
     """|x| ~ 400, |w| ~ 200, scale 1e-4 -> fp32 (tools/test_ops_contracts.py:76-86): bf16
