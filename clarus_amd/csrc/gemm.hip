@@ -233,10 +233,16 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   // K > 128 (K % 32 == 0): the DMA-pipelined tile kernel; K <= 128 with a residual: the tiled
   // kernel with 64 x 64 tiles (the streaming kernel's residual prefetch costs it ~25 % there).
   const bool plain_bf16 = a->a_mode == CLARUS_A_ROWS && opm == OPM_BF16 && a->pro == PRO_NONE && a->batch == 1;
+  // few 128 x 128 output tiles (under 192 for 256 CUs): the 64 x 64 tiled kernel fills the GPU
+  // better (NAFNet SCA GEMMs on the TLC map: M = 4859, K = N = 512: 15.9 vs 17.2 us; M = 1254,
+  // K = N = 1024: 20.0 vs 24.0 us; c1024 c -> c with 232 tiles stays: 30.8 vs 28.3 us)
+  const bool few_tiles = a->tile == 0 && plain_bf16 && a->k > 128 && !run_div &&
+                         cdiv(a->m, 128) * cdiv(a->n, a->gate ? 64 : 128) < 192;
   const bool auto_dma = a->tile == 0 && plain_bf16 && a->k > 128 && a->k % 32 == 0 && (a->lda * 2) % 16 == 0 &&
-                        (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
+                        (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0) && !few_tiles;
   int tile_override = 0;
   if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && !run_div) tile_override = 3;
+  if (few_tiles) tile_override = 3;
   // streaming kernel with an LDS ring per wave: rows without prologue or with LN / RMS / a bf16
   // TLC map (split operands, batch 1), row or pixel-shuffle output (a lane's channel run inside
   // one quadrant), K <= 128 (bf16 A) / 64 (fp32 A); a residual needs 16-byte rows and whole
@@ -295,7 +301,8 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const bool ln_like = a->pro == PRO_LN || a->pro == PRO_RMS || a->pro == PRO_LNMUL;
   const bool lds_shape = a->a_mode == CLARUS_A_ROWS && opm != OPM_F32 && a->batch == 1 &&
                          (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0);
-  const bool use_lds = lds_shape && (a->tile == 10 || (a->tile == 0 && a->k > 128)) && (!ln_like || a->stats);
+  const bool use_lds = lds_shape && (a->tile == 10 || (a->tile == 0 && a->k > 128 && !few_tiles)) &&
+                       (!ln_like || a->stats);
   CLARUS_REQUIRE(a->tile != 10 || use_lds, "gemm: the pipelined tile kernel does not take this problem");
   const bool needs_stats = a->a_mode == CLARUS_A_ROWS && ln_like && (use_lds || a->k > kc_for(opm));
   if (needs_stats && a->stats && a->batch == 1) {  // one pass over A instead of one per column tile
