@@ -19,6 +19,7 @@ ABI_VERSION = 2
 OK, EINVAL, ELAUNCH = 0, 1, 2
 F32, BF16 = 0, 1
 PRO_NONE, PRO_LN, PRO_MUL, PRO_RMS, PRO_LNMUL = 0, 1, 2, 3, 5
+PRO_ROUND = 0x100  # or-ed into pro: the prologue output may be rounded once to bf16
 A_ROWS, A_S2D = 0, 1
 C_ROWS, C_SHUFFLE, C_NCHW = 0, 1, 2
 ACT_NONE, ACT_GELU, ACT_LRELU = 0, 1, 2

@@ -158,6 +158,15 @@ using namespace clarus;
 extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   clear_error();
   CLARUS_REQUIRE(a != nullptr, "gemm: null args");
+  // CLARUS_PRO_ROUND: the prologue output may be rounded once to bf16 (the ring streaming
+  // kernel does; the other kernels keep hi + lo pairs)
+  ClarusGemmArgs plain;
+  const bool pro_round = (a->pro & CLARUS_PRO_ROUND) != 0;
+  if (pro_round) {
+    plain = *a;
+    plain.pro &= ~CLARUS_PRO_ROUND;
+    a = &plain;
+  }
   CLARUS_REQUIRE(a->a && a->wt && a->c, "gemm: null operand");
   CLARUS_REQUIRE(a->m > 0 && a->n > 0 && a->k > 0 && a->batch > 0, "gemm: empty problem m=%lld n=%lld k=%lld",
                  (long long)a->m, (long long)a->n, (long long)a->k);
@@ -269,9 +278,10 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
       GemmP q = p;
       q.ptiles = 0;
       // 8 channel blocks when the ring still fits next to W^T, else 4
-      if (launch_gemm_rowstream(q, nb, a->gate != 0, opm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
+      const int ropm = (pro_round && opm == OPM_SPLIT && a->a_dtype == DT_BF16 && a->pro != PRO_NONE) ? OPM_ROUND : opm;
+      if (launch_gemm_rowstream(q, nb, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
                                 (hipStream_t)stream) ||
-          (nb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, opm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
+          (nb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
                                             a->batch, (hipStream_t)stream)))
         return check_launch("gemm");
       CLARUS_REQUIRE(a->tile == 0, "gemm: no ring streaming kernel for operand mode %d A dtype %d K=%lld", opm,

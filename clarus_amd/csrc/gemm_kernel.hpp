@@ -31,7 +31,9 @@ namespace clarus {
 enum : int { PRO_NONE = 0, PRO_LN = 1, PRO_MUL = 2, PRO_RMS = 3, PRO_LNMUL = 5 };
 enum : int { AM_ROWS = 0, AM_S2D = 1, AM_CONV3 = 2 };
 enum : int { CM_ROWS = 0, CM_SHUFFLE = 1, CM_NCHW = 2 };
-enum : int { OPM_BF16 = 0, OPM_SPLIT = 1, OPM_F32 = 2 };
+// operand modes: bf16 products; fp32 A (or a prologue output) as hi + lo bf16 pairs; fp32
+// products; a prologue output rounded once to bf16 (ring streaming kernel)
+enum : int { OPM_BF16 = 0, OPM_SPLIT = 1, OPM_F32 = 2, OPM_ROUND = 3 };
 
 struct GemmP {
   const void* a;

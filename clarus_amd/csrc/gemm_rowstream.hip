@@ -68,7 +68,8 @@ RsLaunch pick_ks(int ks, bool res, int rdt) {
 }
 
 // operand modes: bf16 A without prologue; fp32 A split into hi + lo (bf16 W) or fp32 products
-// (fp32 W); bf16 A with a prologue (LN / RMS, or the map multiply with x2) split into hi + lo
+// (fp32 W); bf16 A with a prologue (LN / RMS, or the map multiply with x2) split into hi + lo or
+// rounded once to bf16
 template <int NB, bool GATE>
 RsLaunch pick_mode(int opm, int ta, int ks, bool res, int rdt, bool pro, bool x2) {
   if (opm == OPM_BF16 && ta == DT_BF16 && !pro) return pick_ks<NB, GATE, OPM_BF16, DT_BF16, false>(ks, res, rdt);
@@ -77,6 +78,9 @@ RsLaunch pick_mode(int opm, int ta, int ks, bool res, int rdt, bool pro, bool x2
   if (opm == OPM_SPLIT && ta == DT_BF16 && pro)
     return x2 ? pick_ks<NB, GATE, OPM_SPLIT, DT_BF16, true>(ks, res, rdt)
               : pick_ks<NB, GATE, OPM_SPLIT, DT_BF16, false>(ks, res, rdt);
+  if (opm == OPM_ROUND && ta == DT_BF16 && pro)
+    return x2 ? pick_ks<NB, GATE, OPM_ROUND, DT_BF16, true>(ks, res, rdt)
+              : pick_ks<NB, GATE, OPM_ROUND, DT_BF16, false>(ks, res, rdt);
   return nullptr;
 }
 

@@ -123,7 +123,7 @@ gemm_rowstream_kernel(const GemmP p) {
   constexpr int CR = RES ? RL::BYTES / 1024 : 0;  // residual copies per lane per block
   static_assert(AL::BYTES % 1024 == 0 && (!RES || RL::BYTES % 1024 == 0) && (!X2 || ML::BYTES % 1024 == 0),
                 "blocks are whole copy instructions");
-  static_assert(!X2 || OPM == OPM_SPLIT, "a prologue output is split into hi + lo");
+  static_assert(!X2 || OPM == OPM_SPLIT || OPM == OPM_ROUND, "a prologue output is split or rounded to bf16");
   constexpr int C = CA + CM + CR;               // copy instructions per block
   constexpr int RS_DEPTH = rowstream_depth(NB, GATE, KS, OPM, TA, RDT, RES, X2);
   static_assert(RS_DEPTH >= 2 && RS_DEPTH <= 4, "ring depth");
@@ -296,7 +296,7 @@ gemm_rowstream_kernel(const GemmP p) {
     // LN / RMS statistics over each row: this lane's fragments, then the 4 lanes of the pixel
     // (exact two-pass, fixed order)
     float mean[HB], rstd[HB];
-    const bool stats = OPM == OPM_SPLIT && (p.pro == PRO_LN || p.pro == PRO_RMS);
+    const bool stats = (OPM == OPM_SPLIT || OPM == OPM_ROUND) && (p.pro == PRO_LN || p.pro == PRO_RMS);
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
       mean[h] = 0.f;
@@ -355,6 +355,7 @@ gemm_rowstream_kernel(const GemmP p) {
           }
           if (!kok) a[h] = zero8();
           if constexpr (OPM == OPM_SPLIT) split_bf16(a[h], hi[h], lo[h]);
+          if constexpr (OPM == OPM_ROUND) hi[h] = pack_bf16(a[h]);  // RNE, as the long-K prologue pass
         }
       }
       // each W^T fragment is read from LDS once for all HB pixel halves

@@ -77,6 +77,9 @@ class HipOps(Backend):
     # this backend ran; a linear(ln=...) on exactly that output (same tensor and version, same
     # eps and mode) takes those rows instead of running the prologue pass.
     fuse_ln_rows = True
+    # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
+    # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
+    round_short_prologue = False
 
     def __init__(self, dtype, device):
         super().__init__(dtype, device)
@@ -153,7 +156,7 @@ class HipOps(Backend):
               ln_eps=1e-6, out_scale=1.0, tile=0):
         h, w, oh, ow, pt, pl = geom
         stats = None
-        if pro in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1:
+        if (pro & 0xff) in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1:
             stats = torch.empty(2 * m, device=a.device, dtype=torch.float32)  # row statistics scratch
         args = _lib.GemmArgs(
             a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
@@ -229,6 +232,8 @@ class HipOps(Backend):
         wt = self._wt(w)
         if pro == _lib.PRO_NONE and self._ln_rows_ok(x, wt, nout, k, gate, act, residual):
             return self._gemm_ln_rows(a=x, wt=wt, c=out, m=m, k=k, **epi)
+        if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.round_short_prologue and not self.prologue_split:
+            pro |= _lib.PRO_ROUND
         return self._gemm("linear", a=x, wt=wt, c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                           small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
 

@@ -45,6 +45,10 @@ extern "C" {
 #define CLARUS_PRO_MUL 2   /* a * S[clamp(y - pt), clamp(x - pl), k] (TLC map)      */
 #define CLARUS_PRO_RMS 3   /* a * rsqrt(mean(a^2) + eps)                            */
 #define CLARUS_PRO_LNMUL 5 /* ((a - mean) * rstd * lnw[k] + lnb[k]) * act(m2[p, k]) */
+/* or-ed into pro (LN / RMS / TLC map with bf16 A and W): the prologue output may be rounded once
+   to bf16 (RNE) before the product, the reference GPU path's arithmetic (kernels/gemm.py:164-186);
+   the ring streaming kernel (K <= 128) does so, the other kernels keep hi + lo bf16 pairs */
+#define CLARUS_PRO_ROUND 0x100
 
 /* A addressing */
 #define CLARUS_A_ROWS 0  /* row p at a + p * lda                                    */

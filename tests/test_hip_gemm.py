@@ -83,7 +83,7 @@ def rounding_bound(a, wt, b=None, gate=False, act=None, scale=None):
     return e
 
 
-def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6, rel=1e-5, **kw):
+def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6, rel=1e-5, rounded=None, **kw):
     """fp32-output prologue GEMM against the oracle. With the prologue rounded once to bf16
     (rounds_prologue): within 2e-3 relative of that rounding emulated on the oracle (the
     reference GPU path's numerics, kernels/gemm.py:164-186; elements whose fp32 prologue value
@@ -91,7 +91,7 @@ def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6,
     the rounding itself is pinned by test_rows_prologue_abi), and within rounding_bound (+ 1e-5
     of the output scale for summation order) of the fp32 oracle. Otherwise the fp32 rule."""
     ref = REF.linear(x, wt, b, ln=ln, mul=mul, ln_eps=ln_eps, **kw)
-    if not rounds_prologue(k):
+    if not (rounds_prologue(k) if rounded is None else rounded):
         return assert_fp32(got, ref, rel=rel, what=what)
     a = _prologue_rows(x, mul, ln, ln_eps)
     assert_fp32(got, REF.linear(a.to(torch.bfloat16), wt, b, **kw), rel=2e-3,
@@ -377,6 +377,40 @@ def test_split_operand_path(pro, adt, split, hip_bf16):
                 check_prologue(got.cpu(), k, what, x, wt, b, ln=mode, **kw)
     finally:
         HipOps.split_min_k, HipOps.prologue_split = saved
+
+
+@pytest.mark.parametrize("pro", ["ln", "rms", "mul"])
+def test_short_prologue_rounded(pro, hip_bf16):
+    """HipOps.round_short_prologue (CLARUS_PRO_ROUND): a K = 64 prologue GEMM on the ring streaming
+    kernel rounds the prologue output once to bf16 (OPM_ROUND) instead of taking hi + lo pairs;
+    held to the same criteria as the long-K pass. Two images (the TLC map is indexed per image),
+    bias + scale + bf16 residual, N = 72."""
+    from clarus_amd.hip_ops import HipOps
+    g = gen(46)
+    n, h, w, k, c = 2, 11, 19, 64, 72
+    x = (3 + rnd(g, n, h, w, k)).to(torch.bfloat16)
+    wt, b = rnd(g, k, c, scale=k ** -0.5, dtype=torch.bfloat16), rnd(g, c)
+    sc, res = rnd(g, c), rnd(g, n, h, w, c, dtype=torch.bfloat16)
+    kw = dict(scale=sc, residual=res)
+    if pro == "mul":
+        k1, k2, oh, ow, pt, pl = box_geometry(h, w, 6)
+        s = Small(rnd(g, n, oh, ow, k, dtype=torch.bfloat16), pt, pl, h, w)
+        kwd, kwr = dict(mul=Small(s.data.cuda(), pt, pl, h, w)), dict(mul=s)
+    else:
+        mode = True if pro == "ln" else "rms"
+        kwd = kwr = dict(ln=mode)
+    saved = HipOps.round_short_prologue
+    try:
+        HipOps.round_short_prologue = True
+        got = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), residual=res.cuda(), out_dtype=torch.float32, **kwd)
+    finally:
+        HipOps.round_short_prologue = saved
+    check_prologue(got.cpu(), k, f"short prologue {pro} rounded", x, wt, b, rounded=True, **kwr, **kw)
+    # the default keeps hi + lo pairs: the fp32 rule; and the rounded run is really rounded (it
+    # differs from the pairs by more than fp32 summation noise)
+    got2 = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), residual=res.cuda(), out_dtype=torch.float32, **kwd)
+    check_prologue(got2.cpu(), k, f"short prologue {pro} split", x, wt, b, rounded=False, **kwr, **kw)
+    assert (got - got2).abs().max().item() > 1e-4 * got2.abs().max().item(), "the rounded mode did not round"
 
 
 @pytest.mark.parametrize("k", [128, 200, 1024, 2048])
