@@ -250,7 +250,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const bool auto_dma = a->tile == 0 && plain_bf16 && a->k > 128 && a->k % 32 == 0 && (a->lda * 2) % 16 == 0 &&
                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0) && !few_tiles;
   int tile_override = 0;
-  if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && !run_div) tile_override = 3;
+  if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && (!run_div || run_div % 16 == 0)) tile_override = 3;
   if (few_tiles) tile_override = 3;
   // streaming kernel with an LDS ring per wave: rows without prologue or with LN / RMS / a bf16
   // TLC map (split operands, batch 1), row or pixel-shuffle output (a lane's channel run inside
@@ -271,9 +271,10 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                          (!run_div || (run_div % (4 * nb) == 0 && a->batch == 1));
     CLARUS_REQUIRE((a->tile != 16 && a->tile != 17) || ring_ok,
                    "gemm: the ring streaming kernel does not take this problem");
-    // K <= 128 with a gate, or with a row-layout residual (twice the ring slot: one 4-wave
-    // workgroup per CU) stays on the other kernels (c128 c->c: 52 vs 46 us on the 64 x 64 tiles)
-    const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || (!a->gate && (!a->res || run_div)));
+    // K = 128 with a gate or a residual (twice the ring slot: one 4-wave workgroup per CU) stays
+    // on the other kernels: c128 c->c 52 vs 46 us, the level-1 -> 0 up-conv with its shuffled
+    // residual 109 vs 77 us on the 64 x 64 tiles
+    const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || (!a->gate && !a->res));
     if (a->tile == 16 || a->tile == 17 || ring_auto) {
       GemmP q = p;
       q.ptiles = 0;
