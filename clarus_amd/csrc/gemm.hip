@@ -271,19 +271,23 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                          (!run_div || (run_div % (4 * nb) == 0 && a->batch == 1));
     CLARUS_REQUIRE((a->tile != 16 && a->tile != 17) || ring_ok,
                    "gemm: the ring streaming kernel does not take this problem");
-    // K = 128 with a gate or a residual (twice the ring slot: one 4-wave workgroup per CU) stays
-    // on the other kernels: c128 c->c 52 vs 46 us, the level-1 -> 0 up-conv with its shuffled
-    // residual 109 vs 77 us on the 64 x 64 tiles
-    const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || (!a->gate && !a->res));
+    // K = 128 (interleaved A/B on the NAFNet shapes, us): a row-layout residual takes the ring
+    // with 4 channel blocks (c128 c->c 37.0 vs 41.3 on the 64 x 64 tiles, 45.0 with 8 blocks);
+    // a pixel-shuffled residual the 64 x 64 tiles (level-1 -> 0 up-conv 76 vs 109); a gate the
+    // register-prefetch streaming kernel (36.6 vs 38.6); neither the streaming kernel with 4
+    // channel blocks (level-1 conv1 46.9 vs 50.9)
+    const bool ring_res128 = a->tile == 0 && ring_ok && ks == 4 && a->res && !run_div && !a->gate;
+    const bool ring_auto = a->tile == 0 && ring_ok && (ks <= 2 || ring_res128);
+    const int rnb = (a->tile == 17 || ring_res128) ? 4 : nb;
     if (a->tile == 16 || a->tile == 17 || ring_auto) {
       GemmP q = p;
       q.ptiles = 0;
       // 8 channel blocks when the ring still fits next to W^T, else 4
       const int ropm = (pro_round && opm == OPM_SPLIT && a->a_dtype == DT_BF16 && a->pro != PRO_NONE) ? OPM_ROUND : opm;
-      if (launch_gemm_rowstream(q, nb, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
+      if (launch_gemm_rowstream(q, rnb, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
                                 (hipStream_t)stream) ||
-          (nb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
-                                            a->batch, (hipStream_t)stream)))
+          (rnb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
+                                             a->batch, (hipStream_t)stream)))
         return check_launch("gemm");
       CLARUS_REQUIRE(a->tile == 0, "gemm: no ring streaming kernel for operand mode %d A dtype %d K=%lld", opm,
                      a->a_dtype, (long long)a->k);
@@ -294,7 +298,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   if (a->a_mode == CLARUS_A_ROWS && stream_opm && !auto_dma && !tile_override &&
       (a->tile == 0 || a->tile == 8 || a->tile == 9)) {
     const int ks = stream_ks_for(a->k, a->a_dtype);
-    int nb = a->tile == 8 ? 4 : a->tile == 9 ? 8 : ((a->n <= 64 || a->gate) ? 4 : 8);
+    int nb = a->tile == 8 ? 4 : a->tile == 9 ? 8 : ((a->n <= 64 || a->gate || a->k > 64) ? 4 : 8);
     if (opm == OPM_F32 && a->gate) nb = 4;  // fp32 gate rows of NB 8 exceed the LDS budget
     if (run_div && run_div % (4 * nb)) nb = 4;
     const bool x2 = a->pro == PRO_MUL || a->pro == PRO_LNMUL;
@@ -345,13 +349,20 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   }
   CLARUS_REQUIRE((a->tile != 14 && a->tile != 15) || m32_ok,
                  "gemm: the big-tile DMA-pipelined kernel does not take this problem");
-  if (a->tile == 14 || a->tile == 15) {
-    launch_gemm_big(p, a->gate != 0, a->tile == 14 ? 2 : 1, (hipStream_t)stream);
+  // Automatic choice among the DMA-pipelined kernels for plain bf16 rows with K > 128
+  // (interleaved A/B on the NAFNet shapes, us):
+  //   * gated, with at least 200 tiles of 256 pixels x 256 W^T rows: gemm_big_kernel (level-3
+  //     conv4 28.8 vs 31.7 on 32x32 / 29.8 on 16x16; level-2 conv4 33.6 vs 37.4 / 35.9);
+  //   * with a residual and K > 256: 32x32 MFMAs (K = 512 with an fp32 residual: 25.2 vs 28.6);
+  //   * otherwise 16x16 MFMAs (level-3 conv1 34.0 vs 36.7; level-2 conv1 41.6 vs 43.8;
+  //     c1024 rows 29.1 vs 32.1; c256 c->c+scale+res 31.2 vs 35.6)
+  const bool long_auto = a->tile == 0 && (auto_dma || use_lds);
+  const bool big_auto = long_auto && m32_ok && a->gate && !a->res && cdiv(a->m, 256) * cdiv(a->n, 128) >= 200;
+  if (a->tile == 14 || a->tile == 15 || big_auto) {
+    launch_gemm_big(p, a->gate != 0, a->tile == 15 ? 1 : 2, (hipStream_t)stream);
     return check_launch("gemm");
   }
-  // K <= 256 with a residual stays on the 16x16 DMA kernel (c256 c->c+scale+res: 31.2 vs 35.6 us
-  // and 31.2 vs 32.4 in two runs; K = 512 with an fp32 residual: 25.2 vs 28.6 on 32x32)
-  const bool m32_auto = m32_ok && a->tile == 0 && (auto_dma || use_lds) && !(a->res && a->k <= 256);
+  const bool m32_auto = m32_ok && long_auto && a->res && a->k > 256;
   if (a->tile == 13 || m32_auto) {
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
