@@ -98,7 +98,8 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
     nfwd = sum(1 for r in e2e if is_intro(r))
     groups: dict = {}
     for r in e2e:
-        name = r.get("Kernel_Name", "?").split("(")[0].replace("void ", "")
+        name = r.get("Kernel_Name", "?").replace("(anonymous namespace)::", "")
+        name = name.split("(")[0].replace("void ", "")
         grid = r.get("Grid_Size_X") or r.get("Grid_Size", "?")
         groups.setdefault((name, grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
     total = sum(sum(v) for v in groups.values()) / nfwd

@@ -52,8 +52,30 @@ struct RowLnP {
   int rms;
 };
 
+// The second GEMM of clarus_hip_gemm_ln_gemm: out2 = gate?((LN rows) . W2 + bias2), K = RL_N.
+// Its A operand (the tile's normalised rows) stays in LDS; its W^T fragments stream straight
+// from global memory into registers, each wave its own 64 W^T rows, so the loop has no barrier.
+// w2p holds them in fragment order: pass P (512 W^T rows), wave w, 16-k step s, block b (32 rows),
+// lane l: the 8 values W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e] (one 1 KiB load
+// per fragment; a wave's 64-k group is 8 KiB contiguous).
+constexpr int L2_ROWS = 512;                     // W^T rows per pass
+constexpr int L2_STEPS = RL_N / 16;              // 16-k steps per pass (32)
+constexpr int L2_GROUPS = L2_STEPS / 4;          // 64-k groups per pass (8)
+constexpr int L2_A = 0;                          // LN rows: 64 rows x 1 KiB, units XOR (row % 16)
+static_assert(RL_P * RL_N * 2 <= RL_RING, "the LN rows reuse the first GEMM's ring");
+
+struct Ln2P {
+  const void* w2p;     // packed W^T rows (above), bf16
+  const float* bias2;  // [n2w] fp32 (W^T row order), or null
+  void* out2;          // [m][ld2] bf16
+  int64_t ld2;
+  int n2w;             // W^T rows: a multiple of 512
+  int gate;            // SimpleGate: out2 channel c = (row c) * (row c + n2w / 2)
+};
+
+template <bool FUSE>
 __global__ void __launch_bounds__(RL_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-gemm_rowln_kernel(const GemmP p, const RowLnP q) {
+gemm_rowln_kernel(const GemmP p, const RowLnP q, const Ln2P r2) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   unsigned char* ring = lds;
   float* tb = reinterpret_cast<float*>(lds + RL_RING);                 // [0, 512) bias, [512, 1024) scale
@@ -322,23 +344,143 @@ gemm_rowln_kernel(const GemmP p, const RowLnP q) {
     }
 
     // ---- normalised rows, rounded once to bf16
+    if constexpr (!FUSE) {
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+      for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-      for (int rd = 0; rd < 4; ++rd) {
-        const int64_t qq = (int64_t)t * RL_P + pb * 32 + rd * 8 + (lane >> 3);
-        if (qq >= p.m) continue;
-        f32x8 o;
+        for (int rd = 0; rd < 4; ++rd) {
+          const int64_t qq = (int64_t)t * RL_P + pb * 32 + rd * 8 + (lane >> 3);
+          if (qq >= p.m) continue;
+          f32x8 o;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o.v[i] = (yv[pb][rd][i] - mean[pb][rd]) * rstd[pb][rd];
-        *reinterpret_cast<bf16x8*>((unsigned short*)q.ln_out + qq * RL_N + wave * 64 + (lane & 7) * 8) = pack_bf16(o);
-      }
+          for (int i = 0; i < 8; ++i) o.v[i] = (yv[pb][rd][i] - mean[pb][rd]) * rstd[pb][rd];
+          *reinterpret_cast<bf16x8*>((unsigned short*)q.ln_out + qq * RL_N + wave * 64 + (lane & 7) * 8) = pack_bf16(o);
+        }
+    }
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+    if constexpr (FUSE) {
+      // ---- second GEMM on the tile's normalised rows, which stay in LDS (a workgroup has one
+      // tile: the host launches one workgroup per tile). Every wave is past its staging reads
+      // (the last statistics barrier above), so the ring is free for the rows (at L2_A). Its 8
+      // waves compute 64 pixels x 64 W^T rows each per 512-row pass, as in the first GEMM, with
+      // the W^T fragments of the next 64-k group in flight while one group is multiplied.
+      // lane and wave indices laundered here, so the compiler cannot hoist this phase's
+      // address arithmetic above the first GEMM (where it would hold registers through its loop)
+      int lane_f = lane, wave_f = wave;
+      asm volatile("" : "+v"(lane_f), "+v"(wave_f));
+      const int l32f = lane_f & 31, hlf = lane_f >> 5;
+      const int npass = r2.n2w / L2_ROWS;
+      const int total = npass * L2_GROUPS;  // 64-k groups
+      const unsigned char* W2 = (const unsigned char*)r2.w2p + ((int64_t)wave_f * L2_STEPS * 2 * 64 + lane_f) * 16;
+      bf16x8 wf2[2][4][2];  // [buffer][16-k step][block]
+      auto load_group = [&](int buf, int g) __attribute__((always_inline)) {
+        // group g = pass g / 8, steps 4 (g % 8) .. + 3
+        const unsigned char* src = W2 + ((int64_t)(g / L2_GROUPS) * RL_WAVES * L2_STEPS * 2 + (g % L2_GROUPS) * 8) * 1024;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            wf2[buf][ks][rb] = *reinterpret_cast<const bf16x8*>(src + (ks * 2 + rb) * 1024);
+      };
+      load_group(0, 0);
+      // rows into LDS: pixel px, 16-byte unit u = 8 wave + lane % 8 of its 64, stored at u ^ (px % 16)
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int rd = 0; rd < 4; ++rd) {
+          const int px = pb * 32 + rd * 8 + (lane_f >> 3);
+          f32x8 o;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o.v[i] = (yv[pb][rd][i] - mean[pb][rd]) * rstd[pb][rd];
+          const int u = wave_f * 8 + (lane_f & 7);
+          *reinterpret_cast<bf16x8*>(lds + L2_A + px * (RL_N * 2) + (u ^ (px & 15)) * 16) = pack_bf16(o);
+        }
+      barrier_keep_vm();  // every wave's rows are in LDS
+      const int64_t q0 = (int64_t)t * RL_P;
+      // one 64-k group: its A fragments from LDS, 16 MFMAs
+      auto group = [&](const int buf, const int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int ua = (g % L2_GROUPS) * 8 + 2 * ks + hlf;  // 16-byte unit of the 1 KiB row
+          bf16x8 af2[2];
+#pragma unroll
+          for (int pb = 0; pb < 2; ++pb) {
+            const int px = pb * 32 + l32f;
+            af2[pb] = *reinterpret_cast<const bf16x8*>(lds + L2_A + px * (RL_N * 2) + (ua ^ (px & 15)) * 16);
+          }
+#pragma unroll
+          for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf2[buf][ks][rb], af2[pb], acc[pb][rb]);
+        }
+      };
+      // pass epilogue: + bias2 (SimpleGate), rounded once to bf16, stored from the MFMA layout
+      // (16 consecutive channels of one pixel per lane and block)
+      auto pass_epilogue = [&](const int pass) __attribute__((always_inline)) {
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+          const int64_t qq = q0 + pb * 32 + l32f;
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            if (r2.gate && rb == 1) continue;
+            const int c0 = r2.gate ? pass * (L2_ROWS / 2) + wave_f * 32 + 16 * hlf
+                                   : pass * L2_ROWS + wave_f * 64 + rb * 32 + 16 * hlf;
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f32x4 b1 = r2.bias2 ? *reinterpret_cast<const f32x4*>(r2.bias2 + c0 + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+              if (r2.gate) {
+                const f32x4 b2 = r2.bias2 ? *reinterpret_cast<const f32x4*>(r2.bias2 + r2.n2w / 2 + c0 + 4 * i)
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+              }
+            }
+            if (qq < p.m) {
+              unsigned char* op = (unsigned char*)r2.out2 + (qq * r2.ld2 + c0) * 2;
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                f32x8 o;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o.v[i] = v[8 * h + i];
+                *reinterpret_cast<bf16x8*>(op + 16 * h) = pack_bf16(o);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+      };
+      // groups in pairs (register buffers 0 / 1 by constant index); total is even (8 per pass).
+      // Loads return in order, so vmcnt(8) (the next group's 8 loads outstanding) means group g
+      // has landed, whatever epilogue stores are still in flight.
+      for (int g = 0; g < total; g += 2) {
+        load_group(1, g + 1);
+        wait_vmcnt<8>();
+        group(0, g);
+        if ((g + 1) % L2_GROUPS == 0) pass_epilogue(g / L2_GROUPS);
+        if (g + 2 < total) {
+          load_group(0, g + 2);
+          wait_vmcnt<8>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        group(1, g + 1);
+        if ((g + 2) % L2_GROUPS == 0) pass_epilogue((g + 1) / L2_GROUPS);
+      }
+    }
   }
 }
 
@@ -348,28 +490,30 @@ gemm_rowln_kernel(const GemmP p, const RowLnP q) {
 
 using namespace clarus;
 
-extern "C" int clarus_hip_gemm_ln_rows(const ClarusGemmArgs* a, void* ln_out, float eps, int32_t rms, void* stream) {
-  clear_error();
-  CLARUS_REQUIRE(a != nullptr && a->a && a->wt && a->c && ln_out, "gemm_ln_rows: null operand");
-  CLARUS_REQUIRE(a->m > 0 && a->k > 0, "gemm_ln_rows: empty problem");
-  CLARUS_REQUIRE(a->n == RL_N, "gemm_ln_rows: N=%lld, the row tile covers exactly %d channels", (long long)a->n, RL_N);
-  CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16, "gemm_ln_rows: bf16 A and W");
-  CLARUS_REQUIRE(a->c_dtype == DT_BF16 || a->c_dtype == DT_F32, "gemm_ln_rows: bad output dtype");
-  CLARUS_REQUIRE(!a->res || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_ln_rows: bad residual dtype");
+namespace {
+
+// checks shared by both entry points; fills the first GEMM's parameters
+int rowln_params(const ClarusGemmArgs* a, const void* ln_out, float eps, int32_t rms, GemmP& p, const char* what) {
+  CLARUS_REQUIRE(a != nullptr && a->a && a->wt && a->c && ln_out, "%s: null operand", what);
+  CLARUS_REQUIRE(a->m > 0 && a->k > 0, "%s: empty problem", what);
+  CLARUS_REQUIRE(a->n == RL_N, "%s: N=%lld, the row tile covers exactly %d channels", what, (long long)a->n, RL_N);
+  CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16, "%s: bf16 A and W", what);
+  CLARUS_REQUIRE(a->c_dtype == DT_BF16 || a->c_dtype == DT_F32, "%s: bad output dtype", what);
+  CLARUS_REQUIRE(!a->res || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "%s: bad residual dtype", what);
   CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
                      !a->gate && a->act == ACT_NONE,
-                 "gemm_ln_rows: plain rows (no prologue, gate, activation, batch or pixel shuffle)");
-  CLARUS_REQUIRE(a->k % M32_KC == 0, "gemm_ln_rows: K=%lld must be a multiple of %d", (long long)a->k, M32_KC);
+                 "%s: plain rows (no prologue, gate, activation, batch or pixel shuffle)", what);
+  CLARUS_REQUIRE(a->k % M32_KC == 0, "%s: K=%lld must be a multiple of %d", what, (long long)a->k, M32_KC);
   CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(a->wt, 16),
-                 "gemm_ln_rows: 16-byte A / W rows");
+                 "%s: 16-byte A / W rows", what);
   const int ec = a->c_dtype == DT_BF16 ? 2 : 4, er = a->r_dtype == DT_BF16 ? 2 : 4;
-  CLARUS_REQUIRE(a->ldc >= a->n && (a->ldc * ec) % 16 == 0 && aligned(a->c, 16), "gemm_ln_rows: 16-byte output rows");
+  CLARUS_REQUIRE(a->ldc >= a->n && (a->ldc * ec) % 16 == 0 && aligned(a->c, 16), "%s: 16-byte output rows", what);
   CLARUS_REQUIRE(!a->res || (a->ldr >= a->n && (a->ldr * er) % 16 == 0 && aligned(a->res, 16)),
-                 "gemm_ln_rows: 16-byte residual rows");
-  CLARUS_REQUIRE(aligned(ln_out, 16), "gemm_ln_rows: 16-byte normalised rows");
-  CLARUS_REQUIRE(eps >= 0.f && (rms == 0 || rms == 1), "gemm_ln_rows: bad eps / mode");
-  CLARUS_REQUIRE(cdiv(a->m, RL_P) < ((int64_t)1 << 31), "gemm_ln_rows: too many tiles");
-  GemmP p{};
+                 "%s: 16-byte residual rows", what);
+  CLARUS_REQUIRE(aligned(ln_out, 16), "%s: 16-byte normalised rows", what);
+  CLARUS_REQUIRE(eps >= 0.f && (rms == 0 || rms == 1), "%s: bad eps / mode", what);
+  CLARUS_REQUIRE(cdiv(a->m, RL_P) < ((int64_t)1 << 31), "%s: too many tiles", what);
+  p = GemmP{};
   p.a = a->a; p.wt = a->wt; p.c = a->c;
   p.bias = a->bias; p.scale = a->scale; p.res = a->res;
   p.m = a->m; p.n = a->n; p.k = a->k;
@@ -378,20 +522,50 @@ extern "C" int clarus_hip_gemm_ln_rows(const ClarusGemmArgs* a, void* ln_out, fl
   p.has_res = a->res != nullptr;
   p.out_scale = a->out_scale;
   p.ptiles = cdiv(a->m, RL_P);
-  RowLnP q{ln_out, eps, rms};
+  return CLARUS_OK;
+}
+
+template <bool FUSE>
+int rowln_launch(const GemmP& p, const RowLnP& q, const Ln2P& r2, void* stream, const char* what) {
   static const int per_cu = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_rowln_kernel),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_rowln_kernel<FUSE>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&gemm_rowln_kernel),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&gemm_rowln_kernel<FUSE>),
                                                      RL_THREADS, RL_LDS) != hipSuccess ||
         n < 1)
       n = 1;
     return n;
   }();
-  int64_t gx = 256LL * per_cu;
+  // one tile per workgroup at most (the fused second GEMM reuses the ring, so a workgroup
+  // cannot prefetch a next tile); without the fusion, persistent up to the resident count
   const int64_t need = cdiv(p.ptiles, 8) * 8;
-  if (gx > need) gx = need;
-  hipLaunchKernelGGL(gemm_rowln_kernel, dim3((unsigned)gx), dim3(RL_THREADS), RL_LDS, (hipStream_t)stream, p, q);
-  return check_launch("gemm_ln_rows");
+  int64_t gx = FUSE ? need : std::min<int64_t>(256LL * per_cu, need);
+  hipLaunchKernelGGL(gemm_rowln_kernel<FUSE>, dim3((unsigned)gx), dim3(RL_THREADS), RL_LDS, (hipStream_t)stream, p,
+                     q, r2);
+  return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int clarus_hip_gemm_ln_rows(const ClarusGemmArgs* a, void* ln_out, float eps, int32_t rms, void* stream) {
+  clear_error();
+  GemmP p;
+  if (int rc = rowln_params(a, ln_out, eps, rms, p, "gemm_ln_rows")) return rc;
+  return rowln_launch<false>(p, RowLnP{ln_out, eps, rms}, Ln2P{}, stream, "gemm_ln_rows");
+}
+
+extern "C" int clarus_hip_gemm_ln_gemm(const ClarusGemmArgs* a, float eps, int32_t rms, const void* w2p,
+                                       const float* bias2, void* out2, int64_t n2w, int32_t gate2, void* stream) {
+  clear_error();
+  GemmP p;
+  if (int rc = rowln_params(a, w2p, eps, rms, p, "gemm_ln_gemm")) return rc;
+  CLARUS_REQUIRE(out2 != nullptr && aligned(out2, 16) && aligned(w2p, 16), "gemm_ln_gemm: 16-byte packed W2 / out2");
+  CLARUS_REQUIRE(n2w > 0 && n2w % L2_ROWS == 0 && n2w <= (1 << 20), "gemm_ln_gemm: n2w=%lld must be a multiple of %d",
+                 (long long)n2w, L2_ROWS);
+  CLARUS_REQUIRE(gate2 == 0 || gate2 == 1, "gemm_ln_gemm: gate2 is 0 or 1");
+  CLARUS_REQUIRE(bias2 == nullptr || aligned(bias2, 16), "gemm_ln_gemm: 16-byte bias2");
+  CLARUS_REQUIRE(cdiv(a->m, RL_P) * 8 < ((int64_t)1 << 31), "gemm_ln_gemm: too many tiles");
+  Ln2P r2{w2p, bias2, out2, gate2 ? n2w / 2 : n2w, (int)n2w, gate2};
+  return rowln_launch<true>(p, RowLnP{nullptr, eps, rms}, r2, stream, "gemm_ln_gemm");
 }

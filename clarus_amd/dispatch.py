@@ -85,6 +85,19 @@ class _Backend:
         return hit
 
 
+def linear_ln_linear_unfused(self, x, w, bias=None, scale=None, residual=None, mul=None, out_dtype=None,
+                      w2=None, bias2=None, gate2=False, ln=True, ln_eps=1e-6):
+    """y = linear(x, w, ...) followed by u = linear(y, w2, bias2, ln=ln, gate=gate2): the
+    residual GEMM and the LayerNorm GEMM that reads its output (NAFNet conv3 -> conv4 at
+    python/clarus/models/nafnet.py's block). Returns (y, u). Backends without a fused kernel
+    run the two ops."""
+    y = self.linear(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype)
+    return y, self.linear(y, w2, bias2, ln=ln, gate=gate2, ln_eps=ln_eps)
+
+
+_Backend.linear_ln_linear = linear_ln_linear_unfused
+
+
 class _Ops:
     """Ordered backend chain; `ops.<op>(...)` runs the first backend that accepts the call."""
 

@@ -23,7 +23,7 @@ import torch
 
 from . import _lib
 from .dft import dft_matrices
-from .dispatch import Backend, BackendUnavailable, Unsupported, register_backend
+from .dispatch import Backend, BackendUnavailable, Unsupported, linear_ln_linear_unfused, register_backend
 from .geometry import box_geometry, is_small, make_small
 
 _KDT = (torch.bfloat16, torch.float32)
@@ -104,6 +104,8 @@ class HipOps(Backend):
         self.dev = dev
         self._ln_hint = None  # (eps, rms) of the last LN / RMS prologue
         self._ln_next = None  # (output, version, data_ptr, eps, rms, rows) from clarus_hip_gemm_ln_rows
+        self._fuse_next = None  # (w2, bias2, gate2) for the next LN-rows GEMM (linear_ln_linear)
+        self._fused_out = None
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -243,9 +245,43 @@ class HipOps(Backend):
                 and residual is not None and not gate and act is None and nout == 512 and k % 64 == 0
                 and a.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16 and a.is_contiguous())
 
+    def _w2p(self, w2: torch.Tensor, gate: bool) -> torch.Tensor:
+        """[512, n2w] weight -> W^T in the MFMA fragment order of clarus_hip_gemm_ln_gemm
+        ([pass][wave][16-k step][block][lane][8], the rows of a block permuted so a lane
+        accumulates 16 consecutive channels)."""
+        def pack(t):
+            wt = t.t().contiguous()  # [n2w, 512]
+            n2w = wt.shape[0]
+            dv = wt.device
+            wv = torch.arange(8, device=dv).view(1, 8, 1, 1)
+            b = torch.arange(2, device=dv).view(1, 1, 2, 1)
+            i = torch.arange(32, device=dv).view(1, 1, 1, 32)
+            j = 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3)
+            pas = torch.arange(n2w // 512, device=dv).view(-1, 1, 1, 1)
+            rows = (b * (n2w // 2) + 256 * pas + 32 * wv + j) if gate else (512 * pas + 64 * wv + 32 * b + j)
+            f = wt[rows]                                          # [pass, w, b, l32, 512]
+            f = f.view(n2w // 512, 8, 2, 32, 32, 2, 8)            # k = 16 s + 8 hl + e
+            return f.permute(0, 1, 4, 2, 5, 3, 6).contiguous()    # [pass, w, s, b, hl, l32, e]
+        return self.cached(w2, "w2p_gate" if gate else "w2p", pack)
+
     def _gemm_ln_rows(self, *, a, wt, c, m, k, bias, scale, res, ldr, gate, act):
         eps, rms = self._ln_hint
         n = c.shape[-1]
+        fuse, self._fuse_next = self._fuse_next, None
+        if fuse is not None:
+            w2, bias2, gate2 = fuse
+            n2w = w2.shape[1]
+            u = torch.empty((m, n2w // 2 if gate2 else n2w), device=a.device, dtype=torch.bfloat16)
+            args = _lib.GemmArgs(
+                a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
+                res=_lib.ptr(res), m=m, n=n, k=k, batch=1, lda=k, ldc=n, ldr=ldr,
+                a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(c.dtype),
+                r_dtype=_lib.dtype_code(res.dtype) if res is not None else 0, out_scale=1.0)
+            _lib.check(self.lib.clarus_hip_gemm_ln_gemm(
+                ctypes.byref(args), eps, int(rms), self._w2p(w2, gate2).data_ptr(), _lib.ptr(self._bias(bias2)),
+                u.data_ptr(), n2w, int(gate2), self._stream(a)), "linear_ln_linear")
+            self._fused_out = u
+            return c
         rows = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
         args = _lib.GemmArgs(
             a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
@@ -256,6 +292,31 @@ class HipOps(Backend):
                                                     self._stream(a)), "linear")
         self._ln_next = (c, c._version, c.data_ptr(), eps, rms, rows)
         return c
+
+    def linear_ln_linear(self, x, w, bias=None, scale=None, residual=None, mul=None, out_dtype=None,
+                         w2=None, bias2=None, gate2=False, ln=True, ln_eps=1e-6):
+        """The residual GEMM and the LayerNorm GEMM on its output in one kernel
+        (clarus_hip_gemm_ln_gemm) when the first one takes the LN-rows path and W2 is a bf16
+        [512, 512 j] weight; otherwise the two ops."""
+        fusable = (self.fuse_ln_rows and not self.prologue_split and ln in (True, "rms") and w2 is not None
+                   and w2.dtype == torch.bfloat16 and w2.dim() == 2 and w2.shape[0] == 512
+                   and w2.shape[1] % 512 == 0 and w2.is_contiguous() and _dense(bias2))
+        if not fusable:
+            return linear_ln_linear_unfused(self, x, w, bias, scale, residual, mul, out_dtype, w2, bias2, gate2,
+                                            ln, ln_eps)
+        hint = self._ln_hint
+        self._ln_hint = (float(ln_eps), ln == "rms")
+        self._fuse_next, self._fused_out = (w2, bias2, bool(gate2)), None
+        try:
+            y = self.linear(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype)
+        finally:
+            self._fuse_next = None
+        u, self._fused_out = self._fused_out, None
+        if u is None:  # the first GEMM did not take the LN-rows kernel
+            self._ln_hint = hint if hint is not None else self._ln_hint
+            return y, self.linear(y, w2, bias2, ln=ln, gate=gate2, ln_eps=ln_eps)
+        n, h, wd, _ = y.shape
+        return y, u.view(n, h, wd, u.shape[-1])
 
     def _take_ln_rows(self, x, ln, ln_eps):
         e = self._ln_next

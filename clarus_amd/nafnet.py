@@ -163,9 +163,11 @@ class NAFNet:
         t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
         t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
         sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
-        y = o.linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,
-                     mul=sca, out_dtype=self._rdt(level))
-        u = o.linear(y, w[f"{p}.conv4.w"], w[f"{p}.conv4.bias"], ln=True, gate=True)
+        # conv3 (+ residual) and conv4 (LayerNorm of its output, SimpleGate) as one op, which a
+        # backend may run as one kernel
+        y, u = o.linear_ln_linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"],
+                                  residual=x, mul=sca, out_dtype=self._rdt(level), w2=w[f"{p}.conv4.w"],
+                                  bias2=w[f"{p}.conv4.bias"], gate2=True, ln=True)
         return o.linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
                         out_dtype=self._rdt(level))
 

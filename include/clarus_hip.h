@@ -154,6 +154,25 @@ int clarus_hip_rows_prologue(const ClarusGemmArgs* args, void* out, void* stream
 int clarus_hip_gemm_ln_rows(const ClarusGemmArgs* args, void* ln_out, float eps, int32_t rms, void* stream);
 
 /*
+ * clarus_hip_gemm_ln_rows whose normalised rows feed a second GEMM in the same kernel instead
+ * of being written: out2 = ln_rows . W2 + bias2 (K = 512, fp32 accumulation, rounded once to
+ * bf16), with SimpleGate when gate2 = 1 (out2 channel c = (row c) * (row c + n2w / 2), dense
+ * [m][n2w / 2]; else dense [m][n2w]). The same values clarus_hip_gemm_ln_rows followed by a
+ * bf16 clarus_hip_gemm on ln_out (bias2, gate2) computes; args->c (the first GEMM's output) is
+ * still written. n2w (W2's columns, the W^T rows) is a multiple of 512; bias2 fp32 [n2w] or
+ * NULL. w2p holds W2^T [n2w][512] bf16 packed in MFMA fragment order: for pass P (512 W^T
+ * rows), wave w (0..7), 16-k step s (0..31), block b (0..1), lane l (0..63): the 8 values
+ * W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e], e = 0..7, where for r = 64 w + 32 b + i
+ * with j = 16 ((i / 4) % 2) + 4 (i / 8) + i % 4: row(P, r) = 512 P + 64 w + 32 b + j, or with
+ * gate2 = 1: b n2w / 2 + 256 P + 32 w + j (n2w * 512 bf16 in all).
+ * No counterpart in the reference: it fuses fused_gemm (kernels/gemm.py:353-400), the ln_rows
+ * pass (kernels/spatial.py:312) and the next fused_gemm, for callers that run a LayerNorm GEMM
+ * right after a residual GEMM of width 512 (NAFNet conv3 -> conv4, conv5 -> conv1).
+ */
+int clarus_hip_gemm_ln_gemm(const ClarusGemmArgs* args, float eps, int32_t rms, const void* w2p, const float* bias2,
+                            void* out2, int64_t n2w, int32_t gate2, void* stream);
+
+/*
  * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:
  *   y = act(conv3x3(up2 ? nearest_x2(x) : x) + bias) * out_scale (+ residual)
  * x [batch, h, w, cin] with pixel stride ldx (h, w = INPUT size); wt [cout][9 * cin] with

@@ -63,5 +63,8 @@ def test_validation_rejects_before_launch(lib):
                       a_dtype=_lib.BF16, w_dtype=_lib.BF16)
     assert lib.clarus_hip_gemm_ln_rows(ctypes.byref(a), 16, 1e-6, 0, None) == _lib.EINVAL  # N != 512
     assert b"512" in lib.clarus_hip_last_error()
+    a.n, a.ldc = 512, 512
+    assert lib.clarus_hip_gemm_ln_gemm(ctypes.byref(a), 1e-6, 0, 16, None, 16, 768, 1, None) == _lib.EINVAL  # n2w
+    assert b"n2w" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0

@@ -573,6 +573,42 @@ def test_linear_fuses_ln_rows(hip_bf16):
     assert (d > 2e-2).float().mean().item() <= 1e-3 and d.max().item() <= 0.1, d.max().item()
 
 
+@pytest.mark.parametrize("gate2,n2w,ln,res_dt", [(True, 1024, True, torch.float32), (False, 1024, True, torch.float32),
+                                                 (True, 512, "rms", torch.bfloat16), (False, 512, True, None)])
+def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
+    """clarus_hip_gemm_ln_gemm (HipOps.linear_ln_linear) against the same two GEMMs run apart
+    (clarus_hip_gemm_ln_rows, then a GEMM on the rows it wrote). The first output is the same
+    kernel code (bit-identical); so are the normalised rows, which the fused kernel keeps in
+    LDS, so the second output differs only by the second GEMM's summation order (another
+    kernel): within one bf16 rounding step. M = 1230 leaves a ragged last 64-pixel tile."""
+    from clarus_amd.hip_ops import HipOps
+    g = gen(47)
+    x = rnd(g, 1, 30, 41, 512, dtype=torch.bfloat16).cuda()
+    w3, b3 = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 512).cuda()
+    w4, b4 = rnd(g, 512, n2w, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, n2w).cuda()
+    beta = rnd(g, 512).cuda()
+    inp = None if res_dt is None else (2 + rnd(g, 1, 30, 41, 512)).to(res_dt).cuda()
+    odt = torch.float32 if res_dt is None else res_dt
+    assert HipOps.fuse_ln_rows
+    y1, u1 = hip_bf16.linear_ln_linear(x, w3, b3, scale=beta, residual=inp, out_dtype=odt, w2=w4, bias2=b4,
+                                       gate2=gate2, ln=ln)
+    hip_bf16._ln_hint, hip_bf16._ln_next = (1e-6, ln == "rms"), None
+    y0 = hip_bf16.linear(x, w3, b3, scale=beta, residual=inp, out_dtype=odt)
+    taken = hip_bf16._ln_next is not None
+    u0 = hip_bf16.linear(y0, w4, b4, ln=ln, gate=gate2)
+    assert u1.shape == u0.shape == (1, 30, 41, n2w // 2 if gate2 else n2w)
+    if inp is None:  # no residual: the first GEMM is not an LN-rows one, so neither path fuses
+        assert not taken
+    else:
+        assert taken
+    assert torch.equal(y0, y1)
+    u0, u1 = u0.float().cpu(), u1.float().cpu()
+    assert torch.isfinite(u1).all()
+    d = (u0 - u1).abs()
+    assert (d <= 2 ** -7 * u0.abs() + 1e-6).all(), d.max().item()
+    assert (d > 0).float().mean().item() <= 0.02
+
+
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
 def test_linear_range(k, nout, gate, hip_bf16):
     """|x| ~ 400, |w| ~ 200, scale 1e-4 -> fp32 (tools/test_ops_contracts.py:76-86): bf16
