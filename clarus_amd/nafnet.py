@@ -158,9 +158,14 @@ class NAFNet:
         return tuple(((t + self.padder - 1) // self.padder * self.padder >> level) * int(t * 1.5) // t
                      for t in self.tlc)
 
-    def _block(self, x, p, level):
+    def _block(self, x, p, level, t=None, nxt=None):
+        """One NAFBlock on x. t: its conv1 output when the previous block's fused op already
+        computed it. nxt: the next block's key at the same width, whose conv1 (LayerNorm of this
+        block's output) is then computed with this block's conv5 as one op. Returns (z, the next
+        block's conv1 output or None)."""
         o, w = self.ops, self.w
-        t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
+        if t is None:
+            t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
         t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
         sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
         # conv3 (+ residual) and conv4 (LayerNorm of its output, SimpleGate) as one op, which a
@@ -168,8 +173,19 @@ class NAFNet:
         y, u = o.linear_ln_linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"],
                                   residual=x, mul=sca, out_dtype=self._rdt(level), w2=w[f"{p}.conv4.w"],
                                   bias2=w[f"{p}.conv4.bias"], gate2=True, ln=True)
-        return o.linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
-                        out_dtype=self._rdt(level))
+        if nxt is None:
+            return o.linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
+                            out_dtype=self._rdt(level)), None
+        return o.linear_ln_linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"],
+                                  residual=y, out_dtype=self._rdt(level), w2=w[f"{nxt}.conv1.w"],
+                                  bias2=w[f"{nxt}.conv1.bias"], gate2=False, ln=True)
+
+    def _stage(self, x, prefix, nb, level):
+        """nb consecutive blocks {prefix}.0 .. {prefix}.{nb - 1} at one width."""
+        t = None
+        for j in range(nb):
+            x, t = self._block(x, f"{prefix}.{j}", level, t, f"{prefix}.{j + 1}" if j + 1 < nb else None)
+        return x
 
     @torch.no_grad()
     def forward(self, inp):
@@ -181,17 +197,14 @@ class NAFNet:
         x = o.intro(inp, w["intro.w"], w["intro.bias"], out_dtype=self._rdt(0))
         skips = []
         for i, nb in enumerate(self.enc):
-            for j in range(nb):
-                x = self._block(x, f"enc{i}.{j}", i)
+            x = self._stage(x, f"enc{i}", nb, i)
             skips.append(x)
             x = o.down(x, w[f"down{i}.w"], w[f"down{i}.bias"], out_dtype=self._rdt(i + 1))
-        for j in range(self.mid):
-            x = self._block(x, f"mid.{j}", len(self.enc))
+        x = self._stage(x, "mid", self.mid, len(self.enc))
         for i, nb in enumerate(self.dec):
             level = len(self.enc) - 1 - i
             x = o.up(x, w[f"up{i}.w"], residual=skips[level], out_dtype=self._rdt(level))
-            for j in range(nb):
-                x = self._block(x, f"dec{i}.{j}", level)
+            x = self._stage(x, f"dec{i}", nb, level)
         out = o.ending(x, w["ending.w"], w["ending.bias"], inp)
         return out[:, :, :h, :wd]
 
