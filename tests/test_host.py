@@ -235,3 +235,49 @@ def test_nafnet_tlc_windows_known_answer():
     # NAFNet-GoPro-w64 at train 256: 384 / 192 / 96 / 48 / 24 per level
     m64 = NAFNet(ops, width=4, enc=[1, 1, 1, 1], mid=1, dec=[1, 1, 1, 1])
     assert [m64.tlc_kernel(level)[0] for level in range(5)] == [384, 192, 96, 48, 24]
+
+
+@pytest.mark.parametrize("gate", [False, True])
+def test_ln_gemm_weight_packing_matches_header(gate):
+    """HipOps._w2p (torch gather / permute) against the fragment order clarus_hip_gemm_ln_gemm
+    documents in include/clarus_hip.h, evaluated element by element at sampled positions:
+    packed[P][w][s][b][l][e] = W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e]."""
+    from clarus_amd.hip_ops import HipOps
+
+    class Stub:
+        def cached(self, t, tag, fn):
+            return fn(t)
+
+    n2w = 1024
+    w = torch.randn(512, n2w, generator=torch.Generator().manual_seed(5))
+    packed = HipOps._w2p(Stub(), w, gate).reshape(-1)
+    assert packed.numel() == n2w * 512
+    wt = w.t()
+    rng = np.random.default_rng(0)
+    for _ in range(3000):
+        P, wv, s, b, l, e = (int(rng.integers(0, m)) for m in (n2w // 512, 8, 32, 2, 64, 8))
+        i = l % 32
+        j = 16 * ((i // 4) % 2) + 4 * (i // 8) + i % 4
+        row = b * (n2w // 2) + 256 * P + 32 * wv + j if gate else 512 * P + 64 * wv + 32 * b + j
+        flat = ((((P * 8 + wv) * 32 + s) * 2 + b) * 64 + l) * 8 + e
+        assert packed[flat].item() == wt[row, 16 * s + 8 * (l // 32) + e].item()
+    # every W^T element lands exactly once
+    assert torch.equal(packed.sort().values, w.reshape(-1).sort().values)
+
+
+def test_linear_ln_linear_unfused_is_two_linears():
+    """Backends without the fused kernel run linear_ln_linear as the two ops."""
+    calls = []
+
+    class B(Backend):
+        name = "rec"
+
+        def linear(self, x, w, bias=None, **kw):
+            calls.append(kw)
+            return x @ w
+
+    b = B(torch.float32, torch.device("cpu"))
+    x, w1, w2 = torch.randn(3, 4), torch.randn(4, 4), torch.randn(4, 6)
+    y, u = b.linear_ln_linear(x, w1, residual=x, w2=w2, gate2=True, ln="rms", ln_eps=1e-5)
+    assert torch.equal(y, x @ w1) and torch.equal(u, (x @ w1) @ w2)
+    assert calls[0]["residual"] is x and calls[1] == {"ln": "rms", "gate": True, "ln_eps": 1e-5}
