@@ -580,7 +580,10 @@ def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
     (clarus_hip_gemm_ln_rows, then a GEMM on the rows it wrote). The first output is the same
     kernel code (bit-identical); so are the normalised rows, which the fused kernel keeps in
     LDS, so the second output differs only by the second GEMM's summation order (another
-    kernel): within one bf16 rounding step. M = 1230 leaves a ragged last 64-pixel tile."""
+    kernel): within one bf16 rounding step. Both outputs are also held to the oracle: y to the
+    bf16 / fp32 rule, u to the fp32 LayerNorm GEMM within rounding_bound (the rows rounded once to
+    bf16, as the reference's ln_rows pass does) plus the output's bf16 rounding. M = 1230 leaves
+    a ragged last 64-pixel tile."""
     from clarus_amd.hip_ops import HipOps
     g = gen(47)
     x = rnd(g, 1, 30, 41, 512, dtype=torch.bfloat16).cuda()
@@ -607,6 +610,18 @@ def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
     d = (u0 - u1).abs()
     assert (d <= 2 ** -7 * u0.abs() + 1e-6).all(), d.max().item()
     assert (d > 0).float().mean().item() <= 0.02
+    # against the oracle: y as the reference's fused_gemm; u as its LayerNorm GEMM on y in fp32,
+    # within the bound that rounding every normalised row element once to bf16 allows (the
+    # reference GPU path's ln_rows pass, rounding_bound) plus the bf16 rounding of the output
+    xc, w3c, b3c, bc = x.cpu(), w3.cpu(), b3.cpu(), beta.cpu()
+    y_ref = REF.linear(xc, w3c, b3c, scale=bc, residual=None if inp is None else inp.cpu())
+    check(y1.cpu(), y_ref, f"linear_ln_linear y gate2={gate2}")
+    yc = y1.cpu().float()
+    u_ref = REF.linear(yc, w4.cpu(), b4.cpu(), ln=ln, gate=gate2).double()
+    bound = (rounding_bound(_prologue_rows(yc, ln=ln), w4.cpu(), b4.cpu(), gate2)
+             + 2 ** -8 * u_ref.abs() + 1e-5 * u_ref.abs().max().item())
+    du = (u1.double() - u_ref).abs()
+    assert bool((du <= bound).all()), f"u vs oracle: {int((du > bound).sum())} beyond the bound, max {du.max():.3e}"
 
 
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
