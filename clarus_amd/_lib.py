@@ -23,6 +23,7 @@ PRO_ROUND = 0x100  # or-ed into pro: the prologue output may be rounded once to 
 A_ROWS, A_S2D = 0, 1
 C_ROWS, C_SHUFFLE, C_NCHW = 0, 1, 2
 ACT_NONE, ACT_GELU, ACT_LRELU = 0, 1, 2
+CHANNEL_ATTENTION_SCRATCH_MAX = 16 << 20  # bytes of clarus_hip_channel_attention_noalloc's static scratch
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -68,6 +69,7 @@ SIGNATURES = {
     "clarus_hip_channel_attention_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "clarus_hip_channel_attention": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp,
                                             ctypes.c_size_t, _vp]),
+    "clarus_hip_channel_attention_noalloc": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "clarus_hip_patch_filter": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _i32,
                                        _i64, _i64, _i64, _i64, _vp]),
     "clarus_hip_patch_corr": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,

@@ -15,6 +15,8 @@
 // Stage 3 (gram_finish_kernel), one workgroup per (image, head): sums the RS slices in order,
 // scales by rsqrt(max(|.|^2, 1e-24)) and the temperature, and applies a row softmax.
 // The result is deterministic (fixed summation order for a given shape).
+#include <mutex>
+
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -337,36 +339,15 @@ static int64_t split_len_for(int64_t batch, int64_t heads, int64_t hw) {
   return len < GP_CHUNK ? GP_CHUNK : len;
 }
 
-}  // namespace clarus
-
-using namespace clarus;
-
-extern "C" size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads) {
-  if (batch <= 0 || hw <= 0 || c <= 0 || heads <= 0 || c % heads) return 0;
+// Launches the three stages with `scratch` as the partials (already checked to be large enough).
+static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,
+                                    int64_t batch, int64_t hw, int64_t c, int64_t heads, void* scratch,
+                                    hipStream_t s) {
   const int64_t ch = c / heads;
-  const int64_t nsplit = cdiv(hw, split_len_for(batch, heads, hw));
-  return (size_t)(batch * heads * (nsplit + GP_RS) * gram_rec_floats(pick_nb(ch)) * sizeof(float));
-}
-
-extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,
-                                            int64_t batch, int64_t hw, int64_t c, int64_t heads, void* scratch,
-                                            size_t scratch_bytes, void* stream) {
-  clear_error();
-  CLARUS_REQUIRE(qkv && temperature && out && scratch, "channel_attention: null operand");
-  CLARUS_REQUIRE(batch > 0 && hw > 0 && c > 0 && heads > 0 && c % heads == 0, "channel_attention: bad sizes");
-  CLARUS_REQUIRE(qkv_dtype == DT_BF16 || qkv_dtype == DT_F32, "channel_attention: bad dtype");
-  const int64_t ch = c / heads;
-  CLARUS_REQUIRE(ch % 8 == 0 && ch <= 64, "channel_attention: head width %lld must be a multiple of 8, <= 64",
-                 (long long)ch);
-  CLARUS_REQUIRE(aligned(qkv, 16) && (c * (qkv_dtype == DT_BF16 ? 2 : 4)) % 16 == 0,
-                 "channel_attention: qkv rows must be 16-byte aligned");
-  const size_t need = clarus_hip_channel_attention_workspace(batch, hw, c, heads);
-  CLARUS_REQUIRE(scratch_bytes >= need, "channel_attention: scratch %zu < %zu bytes", scratch_bytes, need);
   const int64_t len = split_len_for(batch, heads, hw);
   const int nsplit = (int)cdiv(hw, len);
   const int nb = pick_nb(ch);
   const int64_t rec = gram_rec_floats(nb);
-  hipStream_t s = (hipStream_t)stream;
   dim3 g1((unsigned)nsplit, (unsigned)(batch * heads));
   dim3 g2((unsigned)cdiv(rec, 256), (unsigned)(batch * heads), GP_RS);
   float* part = (float*)scratch;
@@ -391,4 +372,90 @@ extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, 
   }
 #undef CLARUS_GRAM
   return check_launch("channel_attention");
+}
+
+static int check_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, const float* out,
+                                   int64_t batch, int64_t hw, int64_t c, int64_t heads) {
+  CLARUS_REQUIRE(qkv && temperature && out, "channel_attention: null operand");
+  CLARUS_REQUIRE(batch > 0 && hw > 0 && c > 0 && heads > 0 && c % heads == 0, "channel_attention: bad sizes");
+  CLARUS_REQUIRE(qkv_dtype == DT_BF16 || qkv_dtype == DT_F32, "channel_attention: bad dtype");
+  const int64_t ch = c / heads;
+  CLARUS_REQUIRE(ch % 8 == 0 && ch <= 64, "channel_attention: head width %lld must be a multiple of 8, <= 64",
+                 (long long)ch);
+  CLARUS_REQUIRE(aligned(qkv, 16) && (c * (qkv_dtype == DT_BF16 ? 2 : 4)) % 16 == 0,
+                 "channel_attention: qkv rows must be 16-byte aligned");
+  return CLARUS_OK;
+}
+
+// The partials of clarus_hip_channel_attention_noalloc: one array per device, resident until the
+// process ends. Host code never passes `scratch` itself (in host code the name is only a stand-in
+// for the symbol); it uses the device address hipGetSymbolAddress returns, looked up once per
+// device with that device current.
+constexpr size_t CA_SCRATCH_BYTES = CLARUS_CHANNEL_ATTENTION_SCRATCH_MAX;
+__device__ __align__(256) unsigned char scratch[CA_SCRATCH_BYTES];
+
+constexpr int CA_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[CA_MAX_DEVICES];
+
+// device address of this device's `scratch` (looked up on the first call per device), or null
+// with the error text set
+static void* device_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= CA_MAX_DEVICES) {
+    set_error("channel_attention_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("channel_attention_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads) {
+  if (batch <= 0 || hw <= 0 || c <= 0 || heads <= 0 || c % heads) return 0;
+  const int64_t ch = c / heads;
+  const int64_t nsplit = cdiv(hw, split_len_for(batch, heads, hw));
+  return (size_t)(batch * heads * (nsplit + GP_RS) * gram_rec_floats(pick_nb(ch)) * sizeof(float));
+}
+
+extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,
+                                            int64_t batch, int64_t hw, int64_t c, int64_t heads, void* scratch,
+                                            size_t scratch_bytes, void* stream) {
+  clear_error();
+  int rc = check_channel_attention(qkv, qkv_dtype, temperature, out, batch, hw, c, heads);
+  if (rc != CLARUS_OK) return rc;
+  CLARUS_REQUIRE(scratch, "channel_attention: null scratch");
+  const size_t need = clarus_hip_channel_attention_workspace(batch, hw, c, heads);
+  CLARUS_REQUIRE(scratch_bytes >= need, "channel_attention: scratch %zu < %zu bytes", scratch_bytes, need);
+  return launch_channel_attention(qkv, qkv_dtype, temperature, out, batch, hw, c, heads, scratch,
+                                  (hipStream_t)stream);
+}
+
+extern "C" int clarus_hip_channel_attention_noalloc(const void* qkv, int32_t qkv_dtype, const float* temperature,
+                                                    float* out, int64_t batch, int64_t hw, int64_t c, int64_t heads,
+                                                    void* stream) {
+  clear_error();
+  int rc = check_channel_attention(qkv, qkv_dtype, temperature, out, batch, hw, c, heads);
+  if (rc != CLARUS_OK) return rc;
+  const size_t need = clarus_hip_channel_attention_workspace(batch, hw, c, heads);
+  CLARUS_REQUIRE(need <= CA_SCRATCH_BYTES,
+                 "channel_attention_noalloc: this shape needs %zu bytes of partials, more than the %zu-byte "
+                 "static scratch; use clarus_hip_channel_attention with a workspace", need, CA_SCRATCH_BYTES);
+  void* ptr = device_scratch();
+  if (ptr == nullptr) return CLARUS_ELAUNCH;
+  return launch_channel_attention(qkv, qkv_dtype, temperature, out, batch, hw, c, heads, ptr, (hipStream_t)stream);
 }

@@ -223,6 +223,23 @@ int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float
                                  void* stream);
 
 /*
+ * clarus_hip_channel_attention without a workspace argument and without allocating: the split-K
+ * partials live in a static device array of CLARUS_CHANNEL_ATTENTION_SCRATCH_MAX bytes, one per
+ * device, held until the process ends (its address is looked up on the first call on each
+ * device, with that device current). Same arguments, results and rules otherwise; shapes whose
+ * clarus_hip_channel_attention_workspace(...) exceeds the maximum return CLARUS_EINVAL. Every
+ * call on a device shares that device's array: calls that overlap in time on one device (other
+ * streams, other threads) race and give wrong results. Calls no hipMalloc / hipFree.
+ * No counterpart in the reference (its attention.py gram allocates its partials through torch);
+ * for callers that cannot allocate device memory: code under HIP graph capture that must not
+ * allocate, tight serving loops, harnesses that forbid allocation.
+ */
+#define CLARUS_CHANNEL_ATTENTION_SCRATCH_MAX (16u << 20)
+int clarus_hip_channel_attention_noalloc(const void* qkv, int32_t qkv_dtype, const float* temperature,
+                                         float* out, int64_t batch, int64_t hw, int64_t c,
+                                         int64_t heads, void* stream);
+
+/*
  * Per 8x8 patch and channel: y = irfft2(rfft2(patch) * g[c]) (+ residual), as the dense
  * real products  y = Inv[64 x 80] . (g_c * (Fwd[80 x 64] . x))  on fp32 MFMA.
  * fwd [80][64] and inv [64][80] fp32 (rows of re/im coefficients, see clarus_amd/dft.py);

@@ -68,3 +68,19 @@ def test_validation_rejects_before_launch(lib):
     assert b"n2w" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
+
+
+def test_noalloc_attention_rejects_oversized_shapes_before_launch(lib):
+    """clarus_hip_channel_attention_noalloc checks the partials' size against its static scratch on
+    the host, before it looks up the device array or launches anything."""
+    big = (64, 64, 512, 8)  # batch, hw, c, heads: 512 (image, head) records of 64 x 64
+    need = lib.clarus_hip_channel_attention_workspace(*big)
+    assert need > _lib.CHANNEL_ATTENTION_SCRATCH_MAX
+    assert lib.clarus_hip_channel_attention_noalloc(16, _lib.BF16, 16, 16, *big, None) == _lib.EINVAL
+    msg = lib.clarus_hip_last_error()
+    assert b"static scratch" in msg and str(need).encode() in msg
+    assert lib.clarus_hip_channel_attention_noalloc(16, 1, 16, 16, 1, 64, 30, 2, None) == _lib.EINVAL  # width 15
+    assert lib.clarus_hip_channel_attention_noalloc(None, 1, 16, 16, 1, 64, 32, 2, None) == _lib.EINVAL
+    # the largest config-4 level needs well under the maximum
+    for hw, c, heads in ((921600, 48, 1), (230400, 96, 2), (57600, 192, 4), (14400, 384, 8)):
+        assert 0 < lib.clarus_hip_channel_attention_workspace(1, hw, c, heads) <= _lib.CHANNEL_ATTENTION_SCRATCH_MAX
