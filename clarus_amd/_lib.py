@@ -83,6 +83,7 @@ SIGNATURES = {
     "clarus_hip_sizeof_gemm_args": (ctypes.c_size_t, []),
     "clarus_hip_sizeof_conv_args": (ctypes.c_size_t, []),
     "clarus_hip_last_error": (ctypes.c_char_p, []),
+    "clarus_hip_last_kernel": (ctypes.c_char_p, []),
 }
 
 _LIB = None
@@ -119,6 +120,11 @@ def check(rc: int, what: str) -> None:
         msg = _LIB.clarus_hip_last_error().decode(errors="replace") if _LIB is not None else ""
         kind = {EINVAL: "invalid arguments", ELAUNCH: "launch failed"}.get(rc, f"error {rc}")
         raise RuntimeError(f"{what}: {kind}: {msg}")
+
+
+def last_kernel() -> str:
+    """Kernel the calling thread's last launching GEMM / conv entry point chose."""
+    return _LIB.clarus_hip_last_kernel().decode() if _LIB is not None else ""
 
 
 def dtype_code(dt: torch.dtype) -> int:

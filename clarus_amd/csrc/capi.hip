@@ -16,6 +16,15 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
+static thread_local char g_kernel[160];
+
+void note_kernel(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_kernel, sizeof(g_kernel), fmt, ap);
+  va_end(ap);
+}
+
 }  // namespace clarus
 
 extern "C" {
@@ -27,5 +36,7 @@ size_t clarus_hip_sizeof_gemm_args(void) { return sizeof(ClarusGemmArgs); }
 size_t clarus_hip_sizeof_conv_args(void) { return sizeof(ClarusConvArgs); }
 
 const char* clarus_hip_last_error(void) { return clarus::g_err; }
+
+const char* clarus_hip_last_kernel(void) { return clarus::g_kernel; }
 
 }  // extern "C"

@@ -13,6 +13,9 @@ namespace clarus {
 // record the calling thread's last failure (read by clarus_hip_last_error)
 void set_error(const char* fmt, ...);
 void clear_error();
+// record the kernel a launching entry point chose for the calling thread's current call (read by
+// clarus_hip_last_kernel); a diagnostic only, never read by the dispatch
+void note_kernel(const char* fmt, ...);
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 

@@ -284,10 +284,14 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
       q.ptiles = 0;
       // 8 channel blocks when the ring still fits next to W^T, else 4
       const int ropm = (pro_round && opm == OPM_SPLIT && a->a_dtype == DT_BF16 && a->pro != PRO_NONE) ? OPM_ROUND : opm;
+      note_kernel("gemm_rowstream_kernel nb=%d gate=%d opm=%d ks=%d res=%d", rnb, a->gate != 0, ropm, ks,
+                  a->res != nullptr);
       if (launch_gemm_rowstream(q, rnb, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype, a->batch,
                                 (hipStream_t)stream) ||
-          (rnb == 8 && launch_gemm_rowstream(q, 4, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
-                                             a->batch, (hipStream_t)stream)))
+          (rnb == 8 && (note_kernel("gemm_rowstream_kernel nb=4 gate=%d opm=%d ks=%d res=%d", a->gate != 0, ropm,
+                                    ks, a->res != nullptr),
+                        launch_gemm_rowstream(q, 4, a->gate != 0, ropm, a->a_dtype, ks, a->res != nullptr, a->r_dtype,
+                                              a->batch, (hipStream_t)stream))))
         return check_launch("gemm");
       CLARUS_REQUIRE(a->tile == 0, "gemm: no ring streaming kernel for operand mode %d A dtype %d K=%lld", opm,
                      a->a_dtype, (long long)a->k);
@@ -306,6 +310,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                                                                 : nullptr;
     if (fn) {
       p.ptiles = 0;
+      note_kernel("gemm_stream_kernel nb=%d gate=%d opm=%d ks=%d", nb, a->gate != 0, opm, ks);
       fn(p, dim3(0, (unsigned)cdiv(a->n, 16 * nb), (unsigned)a->batch), (hipStream_t)stream, 1);
       return check_launch("gemm");
     }
@@ -344,6 +349,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                  "gemm: the 32x32 DMA-pipelined kernel does not take this problem");
   if (s2d_m32 && (a->tile == 0 || a->tile == 13)) {
     p.s2d = 1;
+    note_kernel("gemm_mfma32_kernel s2d=1 gate=%d", a->gate != 0);
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
   }
@@ -359,20 +365,24 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   const bool long_auto = a->tile == 0 && (auto_dma || use_lds);
   const bool big_auto = long_auto && m32_ok && a->gate && !a->res && cdiv(a->m, 256) * cdiv(a->n, 128) >= 200;
   if (a->tile == 14 || a->tile == 15 || big_auto) {
+    note_kernel("gemm_big_kernel gate=%d wp=%d", a->gate != 0, a->tile == 15 ? 1 : 2);
     launch_gemm_big(p, a->gate != 0, a->tile == 15 ? 1 : 2, (hipStream_t)stream);
     return check_launch("gemm");
   }
   const bool m32_auto = m32_ok && long_auto && a->res && a->k > 256;
   if (a->tile == 13 || m32_auto) {
+    note_kernel("gemm_mfma32_kernel gate=%d", a->gate != 0);
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
   }
   if (dma_ok && (a->tile == 11 || auto_dma || (use_lds && a->tile == 0))) {
+    note_kernel("gemm_dma_kernel gate=%d", a->gate != 0);
     launch_gemm_dma(p, a->gate != 0, (hipStream_t)stream);
     return check_launch("gemm");
   }
   if (use_lds) {
     const bool x2 = a->pro == PRO_MUL || a->pro == PRO_LNMUL;
+    note_kernel("gemm_lds_kernel gate=%d opm=%d x2=%d", a->gate != 0, opm, x2);
     CLARUS_REQUIRE(launch_gemm_lds(p, a->gate != 0, opm, a->a_dtype, x2, (hipStream_t)stream),
                    "gemm: no pipelined tile kernel for operand mode %d A dtype %d", opm, a->a_dtype);
     return check_launch("gemm");
@@ -382,6 +392,8 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                                    : auto_tile(a->m, a->n, a->k, a->batch, a->gate != 0, opm, run_div);
   CLARUS_REQUIRE(tile >= 0 && tile < kNumTiles && (!run_div || run_div % (4 * kTileNB[tile]) == 0),
                  "gemm: tile %d does not fit the pixel-shuffle quadrant width", tile + 1);
+  note_kernel("gemm_kernel tile=%d am=%s gate=%d opm=%d", tile + 1, a->a_mode == CLARUS_A_ROWS ? "rows" : "s2d",
+              a->gate != 0, opm);
   return launch(p, a->a_mode == CLARUS_A_ROWS ? AM_ROWS : AM_S2D, a->gate != 0, opm, a->a_dtype, tile, a->batch,
                 (hipStream_t)stream, "gemm");
 }
@@ -428,10 +440,12 @@ extern "C" int clarus_hip_conv3x3(const ClarusConvArgs* a, void* stream) {
                        a->cin % 32 == 0 && a->batch * H * W < ((int64_t)1 << 31);
   CLARUS_REQUIRE(a->tile != 12 || halo_ok, "conv3x3: the halo-tile kernel does not take this problem");
   if (halo_ok && (a->tile == 0 || a->tile == 12)) {
+    note_kernel("conv_halo_kernel up2=%d", p.up2);
     if (launch_conv_halo(p, (hipStream_t)stream)) return check_launch("conv3x3");
     CLARUS_REQUIRE(a->tile == 0, "conv3x3: the halo-tile kernel's weights do not fit in LDS");
   }
   const int tile = a->tile > 0 ? a->tile - 1 : auto_tile(p.m, p.n, p.k, 1, false, opm, 0);
+  note_kernel("gemm_kernel tile=%d am=conv3 opm=%d", tile + 1, opm);
   return launch(p, AM_CONV3, false, opm, a->x_dtype, tile, 1, (hipStream_t)stream, "conv3x3");
 }
 

@@ -95,7 +95,14 @@ def linear_ln_linear_unfused(self, x, w, bias=None, scale=None, residual=None, m
     return y, self.linear(y, w2, bias2, ln=ln, gate=gate2, ln_eps=ln_eps)
 
 
-_Backend.linear_ln_linear = linear_ln_linear_unfused
+def give_pair_default(backend_cls) -> None:
+    """Attach linear_ln_linear_unfused to a backend base class that has no linear_ln_linear, so
+    every backend derived from it answers the op with the two linear calls."""
+    if not callable(getattr(backend_cls, "linear_ln_linear", None)):
+        backend_cls.linear_ln_linear = linear_ln_linear_unfused
+
+
+give_pair_default(_Backend)
 
 
 class _Ops:
@@ -171,6 +178,7 @@ if _host is not None:
     Ops = _host.Ops
     register_backend = _host.register_backend
     register_backend("hip", "clarus_amd.hip_ops:HipOps")
+    give_pair_default(Backend)  # clarus's Backend has no linear_ln_linear of its own
 else:
     Unsupported = _Unsupported
     BackendUnavailable = _BackendUnavailable

@@ -71,11 +71,11 @@ class HipOps(Backend):
     # 164-186). True writes [hi | lo] rows instead (clarus_hip_rows_split, K' = 2K on [W | W]):
     # fp32-accurate products at twice the MFMA work and A bytes (forward 10.88 vs 9.27 ms).
     prologue_split = False
-    # A plain bf16 GEMM with a residual and N = 512 (NAFNet level 3: conv3 and conv5, whose
-    # outputs the next linear normalises) also writes the normalised bf16 rows of its output in
-    # its epilogue (clarus_hip_gemm_ln_rows), with the eps / mode of the last LayerNorm prologue
-    # this backend ran; a linear(ln=...) on exactly that output (same tensor and version, same
-    # eps and mode) takes those rows instead of running the prologue pass.
+    # linear_ln_linear (a residual GEMM and the LayerNorm GEMM on its output, an explicit op the
+    # caller asks for) runs the pair as one kernel (clarus_hip_gemm_ln_gemm) when the first GEMM
+    # has N = 512 and W2 is a bf16 [512, 512 j] weight, or the first GEMM with the LN rows of its
+    # output written by its epilogue (clarus_hip_gemm_ln_rows) and then the second GEMM on those
+    # rows when only the first fits; False runs the two linear ops.
     fuse_ln_rows = True
     # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
     # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
@@ -102,10 +102,9 @@ class HipOps(Backend):
         except (OSError, RuntimeError) as exc:
             raise BackendUnavailable(f"libclarus_hip.so: {exc}") from exc
         self.dev = dev
-        self._ln_hint = None  # (eps, rms) of the last LN / RMS prologue
-        self._ln_next = None  # (output, version, data_ptr, eps, rms, rows) from clarus_hip_gemm_ln_rows
-        self._fuse_next = None  # (w2, bias2, gate2) for the next LN-rows GEMM (linear_ln_linear)
-        self._fused_out = None
+        # launches of the fused pair kernel (clarus_hip_gemm_ln_gemm) and of the LN-rows GEMM
+        # (clarus_hip_gemm_ln_rows) made by linear_ln_linear; counters only, never read by the dispatch
+        self.pair_launches = {"gemm_ln_gemm": 0, "gemm_ln_rows": 0}
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -176,10 +175,9 @@ class HipOps(Backend):
         return c
 
     # ------------------------------------------------------------------ GEMMs
-    def linear(self, x, w, bias=None, ln=False, act=None, gate=False, scale=None,
-               residual=None, mul=None, out_dtype=None, ln_eps=1e-6):
-        if is_small(x):
-            return x.with_data(self.linear(x.data, w, bias, ln, act, gate, scale, residual, mul, out_dtype, ln_eps))
+    def _linear_plan(self, x, w, bias, ln, act, gate, scale, residual, mul, out_dtype):
+        """Acceptance rules of linear (ops/triton_cuda.py:84-112): raises Unsupported, else
+        returns (n, h, wd, k, nout, odt, map tensor, prologue code, map geometry)."""
         if ln and mul is not None:
             raise Unsupported("linear: LayerNorm and mul prologues together")
         if act not in (None, "gelu") or ln not in (False, True, "rms"):
@@ -197,9 +195,6 @@ class HipOps(Backend):
         if not (_kdt(x, w, residual, sm) and odt in _KDT and w.shape[0] == k and k % 8 == 0
                 and _vec16(x) and (sm is None or _vec16(sm))):
             raise Unsupported("linear: bf16 / fp32 operands, K % 8 == 0, 16-byte aligned rows")
-        out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
-        if out.numel() == 0:
-            return out
         pro = _lib.PRO_NONE
         geom = (0, 0, 0, 0, 0, 0)
         if ln:
@@ -207,44 +202,52 @@ class HipOps(Backend):
         elif sm is not None:
             pro = _lib.PRO_MUL
             geom = (h, wd, sm.shape[1], sm.shape[2], mul.pt, mul.pl)
+        return n, h, wd, k, nout, odt, sm, pro, geom
+
+    def _prologue_pass(self, w, pro, k) -> bool:
+        """A prologue over this K with these weights runs as a separate pass over the rows (the
+        reference's ln_rows / mul_small, ops/triton_cuda.py:104-110), then a plain bf16 GEMM."""
+        return pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0
+
+    def _prologue_rows(self, x, pro, sm, geom, ln_eps, m, k):
+        """The prologue applied to every row, rounded once to bf16 ([m, K]), or as [hi | lo] bf16
+        ([m, 2K]) with prologue_split."""
+        kk = 2 * k if self.prologue_split else k
+        rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
+        hh, ww, oh, ow, pt, pl = geom
+        args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
+                             pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
+                             s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
+                             h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
+        fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
+        _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
+        return rows
+
+    def linear(self, x, w, bias=None, ln=False, act=None, gate=False, scale=None,
+               residual=None, mul=None, out_dtype=None, ln_eps=1e-6):
+        if is_small(x):
+            return x.with_data(self.linear(x.data, w, bias, ln, act, gate, scale, residual, mul, out_dtype, ln_eps))
+        n, h, wd, k, nout, odt, sm, pro, geom = self._linear_plan(x, w, bias, ln, act, gate, scale, residual, mul,
+                                                                  out_dtype)
+        out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
+        if out.numel() == 0:
+            return out
         epi = dict(bias=self._bias(bias), scale=self._bias(scale), res=residual, ldr=nout, gate=gate,
                    act=_lib.ACT_GELU if act == "gelu" else 0)
         m = n * h * wd
-        if ln:
-            self._ln_hint = (float(ln_eps), ln == "rms")
-        if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0:
+        if self._prologue_pass(w, pro, k):
             # the separate prologue pass of triton_cuda.py:104-110 (ln_rows / mul_small), then a
-            # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K); LN rows
-            # the producing GEMM already wrote are taken as they are
-            kk = 2 * k if self.prologue_split else k
-            rows = self._take_ln_rows(x, ln, ln_eps) if (ln and not self.prologue_split) else None
-            if rows is None:
-                rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
-                hh, ww, oh, ow, pt, pl = geom
-                args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
-                                     pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
-                                     s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
-                                     h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
-                fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
-                _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
+            # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K)
+            rows = self._prologue_rows(x, pro, sm, geom, ln_eps, m, k)
+            kk = rows.shape[1]
             wt = self._wt2(w) if self.prologue_split else self._wt(w)
-            if self._ln_rows_ok(rows, wt, nout, kk, gate, act, residual):
-                return self._gemm_ln_rows(a=rows, wt=wt, c=out, m=m, k=kk, **epi)
             return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, **epi)
-        wt = self._wt(w)
-        if pro == _lib.PRO_NONE and self._ln_rows_ok(x, wt, nout, k, gate, act, residual):
-            return self._gemm_ln_rows(a=x, wt=wt, c=out, m=m, k=k, **epi)
         if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.round_short_prologue and not self.prologue_split:
             pro |= _lib.PRO_ROUND
-        return self._gemm("linear", a=x, wt=wt, c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
+        return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                           small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
 
-    # ---- GEMMs that also write the normalised rows of their output (clarus_hip_gemm_ln_rows)
-    def _ln_rows_ok(self, a, wt, nout, k, gate, act, residual) -> bool:
-        return (self.fuse_ln_rows and not self.prologue_split and self._ln_hint is not None
-                and residual is not None and not gate and act is None and nout == 512 and k % 64 == 0
-                and a.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16 and a.is_contiguous())
-
+    # ---- a residual GEMM and the LayerNorm GEMM on its output (linear_ln_linear)
     def _w2p(self, w2: torch.Tensor, gate: bool) -> torch.Tensor:
         """[512, n2w] weight -> W^T in the MFMA fragment order of clarus_hip_gemm_ln_gemm
         ([pass][wave][16-k step][block][lane][8], the rows of a block permuted so a lane
@@ -264,68 +267,69 @@ class HipOps(Backend):
             return f.permute(0, 1, 4, 2, 5, 3, 6).contiguous()    # [pass, w, s, b, hl, l32, e]
         return self.cached(w2, "w2p_gate" if gate else "w2p", pack)
 
-    def _gemm_ln_rows(self, *, a, wt, c, m, k, bias, scale, res, ldr, gate, act):
-        eps, rms = self._ln_hint
-        n = c.shape[-1]
-        fuse, self._fuse_next = self._fuse_next, None
-        if fuse is not None:
-            w2, bias2, gate2 = fuse
-            n2w = w2.shape[1]
-            u = torch.empty((m, n2w // 2 if gate2 else n2w), device=a.device, dtype=torch.bfloat16)
-            args = _lib.GemmArgs(
-                a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
-                res=_lib.ptr(res), m=m, n=n, k=k, batch=1, lda=k, ldc=n, ldr=ldr,
-                a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(c.dtype),
-                r_dtype=_lib.dtype_code(res.dtype) if res is not None else 0, out_scale=1.0)
-            _lib.check(self.lib.clarus_hip_gemm_ln_gemm(
-                ctypes.byref(args), eps, int(rms), self._w2p(w2, gate2).data_ptr(), _lib.ptr(self._bias(bias2)),
-                u.data_ptr(), n2w, int(gate2), self._stream(a)), "linear_ln_linear")
-            self._fused_out = u
-            return c
-        rows = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
-        args = _lib.GemmArgs(
-            a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
-            res=_lib.ptr(res), m=m, n=n, k=k, batch=1, lda=k, ldc=n, ldr=ldr,
-            a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(c.dtype),
-            r_dtype=_lib.dtype_code(res.dtype) if res is not None else 0, out_scale=1.0)
-        _lib.check(self.lib.clarus_hip_gemm_ln_rows(ctypes.byref(args), rows.data_ptr(), eps, int(rms),
-                                                    self._stream(a)), "linear")
-        self._ln_next = (c, c._version, c.data_ptr(), eps, rms, rows)
-        return c
+    def _pair_first(self, x, w, bias, scale, residual, mul, out_dtype, ln):
+        """The first GEMM of linear_ln_linear on the LN-rows kernel: (A rows, W^T, output,
+        epilogue, m) when it fits (bf16 backend, plain bf16 rows after any prologue pass, N = 512,
+        K % 64 == 0, a residual, no gate / activation), else None."""
+        if not (self.fuse_ln_rows and not self.prologue_split and self.dtype == torch.bfloat16
+                and ln in (True, "rms") and not is_small(x) and residual is not None):
+            return None
+        try:
+            n, h, wd, k, nout, odt, sm, pro, geom = self._linear_plan(x, w, bias, False, None, False, scale,
+                                                                      residual, mul, out_dtype)
+        except Unsupported:
+            return None
+        if not (nout == 512 and k % 64 == 0 and w.dtype == torch.bfloat16 and n * h * wd > 0):
+            return None
+        m = n * h * wd
+        if pro != _lib.PRO_NONE:
+            if not self._prologue_pass(w, pro, k):
+                return None
+            a = self._prologue_rows(x, pro, sm, geom, 1e-6, m, k)
+        elif x.dtype == torch.bfloat16:
+            a = x
+        else:
+            return None
+        out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
+        epi = _lib.GemmArgs(
+            a=a.data_ptr(), wt=self._wt(w).data_ptr(), c=out.data_ptr(), bias=_lib.ptr(self._bias(bias)),
+            scale=_lib.ptr(self._bias(scale)), res=residual.data_ptr(), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout,
+            ldr=nout, a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+            r_dtype=_lib.dtype_code(residual.dtype), out_scale=1.0)
+        return a, out, epi, m
 
     def linear_ln_linear(self, x, w, bias=None, scale=None, residual=None, mul=None, out_dtype=None,
                          w2=None, bias2=None, gate2=False, ln=True, ln_eps=1e-6):
-        """The residual GEMM and the LayerNorm GEMM on its output in one kernel
-        (clarus_hip_gemm_ln_gemm) when the first one takes the LN-rows path and W2 is a bf16
-        [512, 512 j] weight; otherwise the two ops."""
-        fusable = (self.fuse_ln_rows and not self.prologue_split and ln in (True, "rms") and w2 is not None
-                   and w2.dtype == torch.bfloat16 and w2.dim() == 2 and w2.shape[0] == 512
-                   and w2.shape[1] % 512 == 0 and w2.is_contiguous() and _dense(bias2))
-        if not fusable:
+        """y = linear(x, w, bias, scale=, residual=, mul=, out_dtype=), then u = linear(y, w2,
+        bias2, ln=ln, gate=gate2, ln_eps=ln_eps); returns (y, u). One kernel
+        (clarus_hip_gemm_ln_gemm) when the first GEMM fits the LN-rows kernel and W2 is a bf16
+        [512, 512 j] weight; the first GEMM writing the LN rows of its output and a plain GEMM
+        on them when only the first fits; otherwise the two linear ops."""
+        pairable = w2 is not None and w2.dtype == torch.bfloat16 and w2.dim() == 2 and w2.shape[0] == 512
+        first = self._pair_first(x, w, bias, scale, residual, mul, out_dtype, ln) if pairable else None
+        if first is None:
             return linear_ln_linear_unfused(self, x, w, bias, scale, residual, mul, out_dtype, w2, bias2, gate2,
                                             ln, ln_eps)
-        hint = self._ln_hint
-        self._ln_hint = (float(ln_eps), ln == "rms")
-        self._fuse_next, self._fused_out = (w2, bias2, bool(gate2)), None
-        try:
-            y = self.linear(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype)
-        finally:
-            self._fuse_next = None
-        u, self._fused_out = self._fused_out, None
-        if u is None:  # the first GEMM did not take the LN-rows kernel
-            self._ln_hint = hint if hint is not None else self._ln_hint
-            return y, self.linear(y, w2, bias2, ln=ln, gate=gate2, ln_eps=ln_eps)
+        a, y, args, m = first
+        rms = int(ln == "rms")
+        b2 = self._bias(bias2)
+        fused = (w2.dtype == torch.bfloat16 and w2.dim() == 2 and w2.shape[0] == 512 and w2.shape[1] % 512 == 0
+                 and w2.is_contiguous() and (b2 is None or _vec16(b2)))
         n, h, wd, _ = y.shape
-        return y, u.view(n, h, wd, u.shape[-1])
-
-    def _take_ln_rows(self, x, ln, ln_eps):
-        e = self._ln_next
-        if e is None or e[0] is not x or x._version != e[1] or x.data_ptr() != e[2]:
-            return None
-        if e[3] != float(ln_eps) or e[4] != (ln == "rms"):
-            return None
-        self._ln_next = None
-        return e[5]
+        if fused:
+            n2w = w2.shape[1]
+            u = torch.empty((n, h, wd, n2w // 2 if gate2 else n2w), device=x.device, dtype=torch.bfloat16)
+            _lib.check(self.lib.clarus_hip_gemm_ln_gemm(
+                ctypes.byref(args), float(ln_eps), rms, self._w2p(w2, bool(gate2)).data_ptr(), _lib.ptr(b2),
+                u.data_ptr(), n2w, int(bool(gate2)), self._stream(a)), "linear_ln_linear")
+            self.pair_launches["gemm_ln_gemm"] += 1
+            return y, u
+        rows = torch.empty((n, h, wd, 512), device=x.device, dtype=torch.bfloat16)
+        _lib.check(self.lib.clarus_hip_gemm_ln_rows(ctypes.byref(args), rows.data_ptr(), float(ln_eps), rms,
+                                                    self._stream(a)), "linear_ln_linear")
+        self.pair_launches["gemm_ln_rows"] += 1
+        # the rows are LN(y) rounded once to bf16: what linear(y, ln=...) feeds its GEMM for K = 512
+        return y, self.linear(rows, w2, bias2, gate=gate2)
 
     def down(self, x, w4d, b, out_dtype=None):
         if tuple(w4d.shape[-2:]) != (2, 2) or not _dense(x, b):

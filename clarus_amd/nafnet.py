@@ -89,8 +89,13 @@ class NAFNet:
     """NAFNetLocal (TLC, train_size 256) or plain NAFNet over an `Ops` dispatcher."""
 
     def __init__(self, ops, width=64, enc=(1, 1, 1, 28), mid=1, dec=(1, 1, 1, 1), tlc=(256, 256),
-                 res_fp32_level=3, seed=0, state_dict=None):
+                 res_fp32_level=3, seed=0, state_dict=None, fused_pairs=True):
         self.ops = ops
+        # True: each residual GEMM and the LayerNorm GEMM on its output go to ops.linear_ln_linear
+        # (conv3 -> conv4, and conv5 -> the next block's conv1 within a stage), which a backend may
+        # run as one kernel; False: the reference block's five linear calls
+        # (models/nafnet/__init__.py:152-161), unchanged
+        self.fused_pairs = fused_pairs
         self.dtype = ops.dtype
         self.device = ops.device
         self.width, self.enc, self.mid, self.dec = width, list(enc), mid, list(dec)
@@ -138,7 +143,7 @@ class NAFNet:
         for j in range(self.mid):
             self._fold_block(out, sd, f"middle_blks.{j}", f"mid.{j}")
         for i, n in enumerate(self.dec):
-            w = sd[f"ups.{i}.0.weight"].flatten(1)  # [4C', C], out channel o = c * 4 + dy * 2 + dx
+            w = sd[f"ups.{i}.0.weight"].flatten(1)  # [4C', C]; rows run over (c', dy, dx), dx fastest
             cq = w.shape[0] // 4
             self._put(out, f"up{i}.w", w.view(cq, 2, 2, -1).permute(1, 2, 0, 3).reshape(4 * cq, -1).t())
             for j in range(n):
@@ -158,6 +163,33 @@ class NAFNet:
         return tuple(((t + self.padder - 1) // self.padder * self.padder >> level) * int(t * 1.5) // t
                      for t in self.tlc)
 
+    def _block_reference(self, x, p, level):
+        """One NAFBlock as the reference model calls it: five linear ops, a depthwise conv and the
+        box mean (models/nafnet/__init__.py:152-161)."""
+        o, w = self.ops, self.w
+        t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
+        t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
+        sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
+        y = o.linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,
+                     mul=sca, out_dtype=self._rdt(level))
+        u = o.linear(y, w[f"{p}.conv4.w"], w[f"{p}.conv4.bias"], ln=True, gate=True)
+        return o.linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
+                        out_dtype=self._rdt(level))
+
+    def _pair(self, x, w, bias=None, scale=None, residual=None, mul=None, out_dtype=None, w2=None, bias2=None,
+              gate2=False, ln=True):
+        """ops.linear_ln_linear, or its two linear calls when no backend in the chain has the op."""
+        o = self.ops
+        try:
+            fn = o.linear_ln_linear
+        except AttributeError:
+            fn = None
+        if fn is None:
+            y = o.linear(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype)
+            return y, o.linear(y, w2, bias2, ln=ln, gate=gate2)
+        return fn(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype, w2=w2, bias2=bias2,
+                  gate2=gate2, ln=ln)
+
     def _block(self, x, p, level, t=None, nxt=None):
         """One NAFBlock on x. t: its conv1 output when the previous block's fused op already
         computed it. nxt: the next block's key at the same width, whose conv1 (LayerNorm of this
@@ -170,18 +202,22 @@ class NAFNet:
         sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
         # conv3 (+ residual) and conv4 (LayerNorm of its output, SimpleGate) as one op, which a
         # backend may run as one kernel
-        y, u = o.linear_ln_linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"],
-                                  residual=x, mul=sca, out_dtype=self._rdt(level), w2=w[f"{p}.conv4.w"],
-                                  bias2=w[f"{p}.conv4.bias"], gate2=True, ln=True)
+        y, u = self._pair(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,
+                          mul=sca, out_dtype=self._rdt(level), w2=w[f"{p}.conv4.w"], bias2=w[f"{p}.conv4.bias"],
+                          gate2=True, ln=True)
         if nxt is None:
             return o.linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
                             out_dtype=self._rdt(level)), None
-        return o.linear_ln_linear(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"],
-                                  residual=y, out_dtype=self._rdt(level), w2=w[f"{nxt}.conv1.w"],
-                                  bias2=w[f"{nxt}.conv1.bias"], gate2=False, ln=True)
+        return self._pair(u, w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"], scale=w[f"{p}.conv5.scale"], residual=y,
+                          out_dtype=self._rdt(level), w2=w[f"{nxt}.conv1.w"], bias2=w[f"{nxt}.conv1.bias"],
+                          gate2=False, ln=True)
 
     def _stage(self, x, prefix, nb, level):
         """nb consecutive blocks {prefix}.0 .. {prefix}.{nb - 1} at one width."""
+        if not self.fused_pairs:
+            for j in range(nb):
+                x = self._block_reference(x, f"{prefix}.{j}", level)
+            return x
         t = None
         for j in range(nb):
             x, t = self._block(x, f"{prefix}.{j}", level, t, f"{prefix}.{j + 1}" if j + 1 < nb else None)
@@ -215,17 +251,18 @@ def psnr(pred: torch.Tensor, gt: torch.Tensor, peak: float = 1.0) -> float:
     return float("inf") if mse == 0 else 10.0 * torch.log10(torch.tensor(peak * peak / mse)).item()
 
 
-def bench_forward(dev, reps: int = 20, log=print) -> dict:
+def bench_forward(dev, reps: int = 20, fused_pairs: bool = True, log=print) -> dict:
     """NAFNet-GoPro-w64 (NAFNetLocal, enc [1, 1, 1, 28], mid 1, dec [1, 1, 1, 1]) 720p bf16
     forward: GEMM-family ops, depthwise conv and TLC box mean on `hip`, pixel (un)shuffle and
-    elementwise adds on torch; captured in a HIP graph after an eager
-    warm-up, median of `reps` event-timed replays."""
+    elementwise adds on torch; captured in a HIP graph after an eager warm-up, median of `reps`
+    event-timed replays. fused_pairs: the harness's paired residual GEMM -> LayerNorm GEMM op
+    (one kernel on `hip`), or the reference block's five linear calls."""
     from . import spatial_torch  # noqa: F401  (registers "torch" for the non-GEMM ops)
     from .dispatch import Ops
     ops = Ops(["hip", "torch"], torch.bfloat16, dev, log=lambda *a: None)
     if "hip" not in ops.by_name:
         raise RuntimeError(f"hip backend unavailable: {ops.skipped}")
-    model = NAFNet(ops)
+    model = NAFNet(ops, fused_pairs=fused_pairs)
     g = torch.Generator().manual_seed(1)
     x = torch.rand(1, 3, 720, 1280, generator=g).to(dev)
     stream = torch.cuda.Stream(dev)
@@ -257,6 +294,7 @@ def bench_forward(dev, reps: int = 20, log=print) -> dict:
     res = {"ms": round(statistics.median(times), 3), "eager_ms": round(statistics.median(eager), 3),
            "reps": reps, "input": "1x3x720x1280 fp32 U(0,1), seeded", "dtype": "bf16",
            "model": "NAFNetLocal w64 enc[1,1,1,28] mid1 dec[1,1,1,1], random init",
+           "block": "paired linear_ln_linear ops" if fused_pairs else "reference block: five linear calls",
            "served": served, "finite": bool(torch.isfinite(y).all().item())}
-    log(f"[bench] NAFNet-w64 720p bf16 forward: graph {res['ms']} ms, eager {res['eager_ms']} ms")
+    log(f"[bench] NAFNet-w64 720p bf16 forward ({res['block']}): graph {res['ms']} ms, eager {res['eager_ms']} ms")
     return res

@@ -37,12 +37,22 @@ class OpCase:
     flops: float
     nbytes: float
     run: Callable[[], object]
-    cpu: dict = field(default_factory=dict)  # inputs for a CPU baseline of the same op
+    cpu: dict = field(default_factory=dict)  # the op's inputs on the host
+    # the same op on a CPU backend with the reference's op signatures (the caller passes the
+    # backend, so this package never imports one): cpu_run(backend) runs it once on `cpu`
+    cpu_run: Callable[[object], object] | None = None
 
     def t_bound(self) -> tuple[float, str]:
         tm = self.flops / PEAK_FLOPS[self.dtype]
         tb = self.nbytes / PEAK_HBM
         return (tm, "mfma") if tm >= tb else (tb, "hbm")
+
+
+def kernel_of(case: OpCase) -> str:
+    """Runs the case once and returns the kernel the library chose for its last launch."""
+    from . import _lib
+    case.run()
+    return _lib.last_kernel()
 
 
 def _gen(seed):
@@ -62,10 +72,13 @@ def config2_names() -> list[str]:
     return [n for c, _, _ in CONFIG2_LEVELS for n in (f"c{c} expand+gate", f"c{c} c->c+scale+res")]
 
 
-def config2_cases(hip, device, seed: int = 0) -> list[OpCase]:
-    """Per level: u = linear(x, We, be, gate=True); y = linear(u, Wc, bc, scale=beta, residual=r)."""
+def config2_cases(hip, device, seed: int = 0, levels=None) -> list[OpCase]:
+    """Per level: u = linear(x, We, be, gate=True); y = linear(u, Wc, bc, scale=beta, residual=r).
+    levels: the widths c to build (all five by default)."""
     cases = []
     for c, h, w in CONFIG2_LEVELS:
+        if levels is not None and c not in levels:
+            continue
         g = _gen(seed + c)
         m = h * w
         x = torch.randn(1, h, w, c, generator=g).bfloat16()
@@ -79,6 +92,7 @@ def config2_cases(hip, device, seed: int = 0) -> list[OpCase]:
         cpu = dict(x=x, we=we, be=be, wc=wc, bc=bc, beta=beta, r=r, rdt=rdt)
         d = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in cpu.items()}
         u = hip.linear(d["x"], d["we"], d["be"], gate=True)  # also the c->c input
+        cpu["u"] = u  # the c->c op's input as the device holds it
 
         def expand(d=d):
             return hip.linear(d["x"], d["we"], d["be"], gate=True)
@@ -86,10 +100,14 @@ def config2_cases(hip, device, seed: int = 0) -> list[OpCase]:
         def cc(d=d, u=u):
             return hip.linear(u, d["wc"], d["bc"], scale=d["beta"], residual=d["r"], out_dtype=d["rdt"])
         rb = 2 if c < 512 else 4
+        cpu["u_host"] = u.cpu()
         cases.append(OpCase(f"c{c} expand+gate", 2, "bf16", 4.0 * m * c * c,
-                            2.0 * m * c + 2.0 * m * c + 4.0 * c * c + 8.0 * c, expand, cpu))
+                            2.0 * m * c + 2.0 * m * c + 4.0 * c * c + 8.0 * c, expand, cpu,
+                            lambda r, d=cpu: r.linear(d["x"], d["we"], d["be"], gate=True)))
         cases.append(OpCase(f"c{c} c->c+scale+res", 2, "bf16", 2.0 * m * c * c,
-                            2.0 * m * c + 2.0 * rb * m * c + 2.0 * c * c + 8.0 * c, cc, cpu))
+                            2.0 * m * c + 2.0 * rb * m * c + 2.0 * c * c + 8.0 * c, cc, cpu,
+                            lambda r, d=cpu: r.linear(d["u_host"], d["wc"], d["bc"], scale=d["beta"],
+                                                      residual=d["r"], out_dtype=d["rdt"])))
     return cases
 
 
@@ -102,28 +120,31 @@ def config1_cases(hip32, device, seed: int = 0) -> list[OpCase]:
     w2 = _kaiming_uniform_kn(g, 32, 32)
     b2 = torch.rand(32, generator=g) * 0.2 - 0.1
     beta = torch.randn(32, generator=g) * 0.1
-    d = [t.to(device) for t in (x, w1, b1, w2, b2, beta)]
-    u = hip32.linear(d[0], d[1], d[2], gate=True)
+    host = (x, w1, b1, w2, b2, beta)
+    d = [t.to(device) for t in host]
     m = 256 * 256
 
-    def chain():
-        uu = hip32.linear(d[0], d[1], d[2], gate=True)
-        return hip32.linear(uu, d[3], d[4], scale=d[5], residual=d[0])
-    del u
+    def chain(d=d, r=None):
+        r = r or hip32
+        uu = r.linear(d[0], d[1], d[2], gate=True)
+        return r.linear(uu, d[3], d[4], scale=d[5], residual=d[0])
     return [OpCase("config1 fp32 chain (gate, scale+res)", 1, "fp32", 2.0 * m * 32 * 64 + 2.0 * m * 32 * 32,
-                   4.0 * m * 32 * 2 + 4.0 * m * 32 * 2 + 4.0 * (32 * 64 + 32 * 32) + 4.0 * (64 + 64), chain)]
+                   4.0 * m * 32 * 2 + 4.0 * m * 32 * 2 + 4.0 * (32 * 64 + 32 * 32) + 4.0 * (64 + 64), chain,
+                   {"inputs": host}, lambda r: chain(host, r))]
 
 
 def config3_cases(hip32, device, seed: int = 0) -> list[OpCase]:
     cases = []
     for c, h, w in [(48, 720, 1280), (96, 360, 640), (192, 180, 320)]:
         g = _gen(seed + c)
-        x = torch.randn(1, h, w, c, generator=g).to(device)
-        f = torch.randn(c, 8, 5, generator=g).to(device)
+        xh = torch.randn(1, h, w, c, generator=g)
+        fh = torch.randn(c, 8, 5, generator=g)
+        x, f = xh.to(device), fh.to(device)
         units = (h // 8) * (w // 8) * c
         cases.append(OpCase(f"patch_filter fused C{c} {h}x{w}", 3, "fp32",
                             units * (2.0 * 64 * 80 + 6 * 40 + 2.0 * 80 * 64), units * 4.0 * 128,
-                            lambda x=x, f=f: hip32.patch_filter(x, f)))
+                            lambda x=x, f=f: hip32.patch_filter(x, f), {"x": xh, "f": fh},
+                            lambda r, x=xh, f=fh: r.patch_filter(x, f)))
     return cases
 
 
@@ -136,15 +157,23 @@ def config4_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
             g = _gen(seed + lvl)
             c, heads = 48 * 2 ** lvl, 2 ** lvl
             hw = h * w
-            qkv = torch.randn(1, h, w, 3 * c, generator=g).to(dt).to(device)
-            t = (torch.rand(heads, generator=g) * 1.5 + 0.5).to(device)
+            qkvh = torch.randn(1, h, w, 3 * c, generator=g).to(dt)
+            th = torch.rand(heads, generator=g) * 1.5 + 0.5
+            qkv, t = qkvh.to(device), th.to(device)
             cases.append(OpCase(f"mdta gram+norms+softmax l{lvl} {tag}", 4, tag,
                                 heads * (2.0 * 48 * 48 * hw + 4.0 * 48 * hw), 2.0 * c * hw * e + heads * 48 * 48 * 4,
-                                lambda hip=hip, qkv=qkv, t=t, heads=heads: hip.channel_attention(qkv, heads, t)))
+                                lambda hip=hip, qkv=qkv, t=t, heads=heads: hip.channel_attention(qkv, heads, t),
+                                {"qkv": qkvh, "t": th},
+                                lambda r, q=qkvh, t=th, heads=heads: r.channel_attention(q, heads, t)))
             a = hip.channel_attention(qkv, heads, t)
             wa = a[0].transpose(1, 2).contiguous().to(dt)  # per head A^T [heads, 48, 48]
+            # the reference applies the maps as one per-image matrix blockdiag(A^T) through
+            # linear_per_image (python/clarus/models/restormer/__init__.py:203-210)
+            bd = torch.block_diag(*wa.float().cpu()).unsqueeze(0)
             cases.append(OpCase(f"mdta attn.V l{lvl} {tag}", 4, tag, heads * 2.0 * 48 * 48 * hw, 2.0 * c * hw * e,
-                                lambda hip=hip, qkv=qkv, wa=wa: hip.attention_apply(qkv, wa)))
+                                lambda hip=hip, qkv=qkv, wa=wa: hip.attention_apply(qkv, wa),
+                                {"qkv": qkvh, "blockdiag": bd},
+                                lambda r, q=qkvh, bd=bd, c=c: r.linear_per_image(q[..., 2 * c:], bd)))
     return cases
 
 
@@ -152,27 +181,80 @@ def config5_cases(hip, device, seed: int = 0) -> list[OpCase]:
     g = _gen(seed)
     h, w = 256, 384
     m = h * w
-    buf = torch.randn(1, h, w, 192, generator=g).bfloat16().to(device)
+    bufh = torch.randn(1, h, w, 192, generator=g).bfloat16()
+    buf = bufh.to(device)
     out = torch.empty(1, h, w, 192, dtype=torch.bfloat16, device=device)
+    outh = torch.empty(1, h, w, 192, dtype=torch.bfloat16)
     cases = []
 
     def kn(cout, cin):
-        return ((torch.randn(cout, cin, 3, 3, generator=g) * math.sqrt(2.0 / (cin * 9))) * 0.1).bfloat16().to(device)
+        return ((torch.randn(cout, cin, 3, 3, generator=g) * math.sqrt(2.0 / (cin * 9))) * 0.1).bfloat16()
     for cin in (64, 96, 128, 160):
-        wt, b = kn(32, cin), torch.zeros(32, device=device)
+        wh, bh = kn(32, cin), torch.zeros(32)
+        wt, b = wh.to(device), bh.to(device)
         cases.append(OpCase(f"conv3x3 {cin}->32 +lrelu (slice)", 5, "bf16", 2.0 * m * 9 * cin * 32,
                             2.0 * m * (cin + 32) + 18.0 * cin * 32,
                             lambda cin=cin, wt=wt, b=b: hip.conv3x3(buf[..., :cin], wt, b, act="lrelu",
-                                                                    out=buf[..., cin:cin + 32])))
-    w5, b5 = kn(64, 192), torch.zeros(64, device=device)
+                                                                    out=buf[..., cin:cin + 32]),
+                            {"buf": bufh, "w": wh},
+                            lambda r, cin=cin, wt=wh, b=bh: r.conv3x3(bufh[..., :cin], wt, b, act="lrelu",
+                                                                      out=bufh[..., cin:cin + 32])))
+    w5h, b5h = kn(64, 192), torch.zeros(64)
+    w5, b5 = w5h.to(device), b5h.to(device)
     cases.append(OpCase("conv3x3 192->64 *0.2 +res", 5, "bf16", 2.0 * m * 9 * 192 * 64,
                         2.0 * m * (192 + 64) + 2.0 * m * 64 + 18.0 * 192 * 64,
-                        lambda: hip.conv3x3(buf, w5, b5, out_scale=0.2, residual=buf[..., :64], out=out[..., :64])))
+                        lambda: hip.conv3x3(buf, w5, b5, out_scale=0.2, residual=buf[..., :64], out=out[..., :64]),
+                        {"buf": bufh, "w": w5h},
+                        lambda r: r.conv3x3(bufh, w5h, b5h, out_scale=0.2, residual=bufh[..., :64],
+                                            out=outh[..., :64])))
     for hh, ww in [(256, 384), (512, 768)]:
-        x = torch.randn(1, hh, ww, 64, generator=g).bfloat16().to(device)
-        wt, b = kn(64, 64), torch.zeros(64, device=device)
+        xh = torch.randn(1, hh, ww, 64, generator=g).bfloat16()
+        wh, bh = kn(64, 64), torch.zeros(64)
+        x, wt, b = xh.to(device), wh.to(device), bh.to(device)
         mo = 4 * hh * ww
         cases.append(OpCase(f"up2 + conv3x3 64->64 +lrelu out {2 * hh}x{2 * ww}", 5, "bf16", 2.0 * mo * 9 * 64 * 64,
                             2.0 * hh * ww * 64 + 2.0 * mo * 64 + 18.0 * 64 * 64,
-                            lambda x=x, wt=wt, b=b: hip.conv3x3(x, wt, b, act="lrelu", up2=True)))
+                            lambda x=x, wt=wt, b=b: hip.conv3x3(x, wt, b, act="lrelu", up2=True),
+                            {"x": xh, "w": wh},
+                            lambda r, x=xh, wt=wh, b=bh: r.conv3x3(x, wt, b, act="lrelu", up2=True)))
     return cases
+
+
+def nafnet_pair_case(hip, device, seed: int = 0) -> OpCase:
+    """The NAFNet-w64 720p level-3 residual GEMM and the LayerNorm GEMM on its output as one op
+    (linear_ln_linear: conv3 (+ beta * . + fp32 residual) -> LN -> conv4 + SimpleGate), the
+    forward's most frequent fused kernel (29 of these and 27 conv5 -> conv1 pairs per forward).
+    M = 14400: F = 2 M 512 (512 + 1024); B = 2 M 512 (A) + 4 M 512 (residual) + 4 M 512 (y, fp32)
+    + 2 M 512 (u, bf16) + 2 (512^2 + 512 * 1024) (weights) + 4 (512 + 1024 + 512) (vectors)."""
+    g = _gen(seed + 3)
+    m, k = 90 * 160, 512
+    x = torch.randn(1, 90, 160, k, generator=g).bfloat16()
+    w3 = _kaiming_uniform_kn(g, k, k).bfloat16()
+    b3 = torch.rand(k, generator=g) * 0.2 - 0.1
+    beta = torch.randn(k, generator=g) * 0.1
+    r = torch.randn(1, 90, 160, k, generator=g)
+    w4 = _kaiming_uniform_kn(g, k, 2 * k).bfloat16()
+    b4 = torch.rand(2 * k, generator=g) * 0.2 - 0.1
+    host = dict(x=x, w3=w3, b3=b3, beta=beta, r=r, w4=w4, b4=b4)
+    d = {n: t.to(device) for n, t in host.items()}
+
+    def pair(r_=None, d=d):
+        from .dispatch import linear_ln_linear_unfused
+        be = r_ or hip
+        fn = getattr(be, "linear_ln_linear", None)
+        args = (d["x"], d["w3"], d["b3"])
+        kw = dict(scale=d["beta"], residual=d["r"], out_dtype=torch.float32, w2=d["w4"], bias2=d["b4"], gate2=True,
+                  ln=True)
+        return fn(*args, **kw) if fn is not None else linear_ln_linear_unfused(be, *args, **kw)
+    flops = 2.0 * m * k * (k + 2 * k)
+    nbytes = m * k * (2.0 + 4.0 + 4.0 + 2.0) + 2.0 * (k * k + k * 2 * k) + 4.0 * (k + 2 * k + k)
+    return OpCase("nafnet L3 conv3 -> LN -> conv4 (fused pair)", 0, "bf16", flops, nbytes, pair, host,
+                  lambda r_: pair(r_, host))
+
+
+def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
+    """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5
+    and the fused NAFNet pair."""
+    return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
+            + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
+            + config5_cases(hip_bf16, device, seed) + [nafnet_pair_case(hip_bf16, device, seed)])

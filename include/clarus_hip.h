@@ -297,6 +297,12 @@ size_t clarus_hip_sizeof_conv_args(void);
 /* Text of the calling thread's last failure ("" if none). */
 const char* clarus_hip_last_error(void);
 
+/* Kernel chosen by the calling thread's last clarus_hip_gemm / clarus_hip_gemm_ln_rows /
+   clarus_hip_gemm_ln_gemm / clarus_hip_conv3x3 call that launched ("" before any), e.g.
+   "gemm_mfma32_kernel gate=0". A diagnostic, so that tests and benchmarks can record and
+   compare which kernel served a problem; the dispatch never reads it. */
+const char* clarus_hip_last_kernel(void);
+
 #ifdef __cplusplus
 }
 #endif

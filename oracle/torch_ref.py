@@ -234,11 +234,3 @@ class TorchRef:
         if act == "gelu":
             y = F.gelu(y)
         return y.contiguous().to(self.dtype)
-
-    def add_scaled(self, a, b, alpha, out_dtype=None, out=None):
-        """torch_ref.py:201-207: a * alpha + b."""
-        y = a.float() * alpha + b.float()
-        if out is not None:
-            out.copy_(y)
-            return out
-        return y.to(self._odt(out_dtype))

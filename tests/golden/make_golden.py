@@ -21,6 +21,11 @@ tests/test_oracle.py pin every single GEMM-family op, but not how the reference 
   :178-199 conv3x3 with up2 + act + out_scale + residual, :237-245 linear_per_image with
   bias + residual.
 
+* ops_freq.safetensors: reference TorchOps.linear_patch_filter (torch_ref.py:272-276) calls:
+  LayerNorm / RMS / no prologue, with and without a residual, fp32 and bf16 activations, on an
+  odd 13x22 or 9x16 image (reflect padding) and a 16x16 one; the fp32 intermediate between the GEMM and
+  the filter is what the bf16 cases pin (a rounded intermediate gives other bits).
+
 Inputs are drawn from one torch.Generator seeded per case; the generator is in this file, so the
 fixtures can be rewritten, but the tests read only the stored tensors.
 """
@@ -149,13 +154,51 @@ def ops_fixture(ref_root: str) -> dict:
     return {k: v.contiguous() for k, v in out.items()}
 
 
-def main(ref_root: str = "/root/reference") -> None:
+LPF_CASES = [  # (name, n, h, w, k, c, ln, residual)
+    ("lpf_none_res", 1, 13, 22, 16, 24, False, True),
+    ("lpf_ln", 1, 13, 22, 16, 24, True, False),
+    ("lpf_rms_res", 2, 16, 16, 16, 16, "rms", True),
+    ("lpf_ln_res", 1, 9, 16, 32, 16, True, True),
+]
+
+
+def freq_fixture(ref_root: str) -> dict:
+    from clarus.ops.torch_ref import TorchOps
+
+    out = {}
+    for tag, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        r = TorchOps(dt, torch.device("cpu"))
+        g = torch.Generator().manual_seed(31)
+        for name, n, h, w, k, c, ln, has_res in LPF_CASES:
+            x = torch.randn(n, h, w, k, generator=g).to(dt)
+            wt = (torch.randn(k, c, generator=g) * k ** -0.5).to(dt)
+            b = torch.randn(c, generator=g) * 0.1
+            f = torch.randn(c, 8, 5, generator=g)
+            res = torch.randn(n, h, w, c, generator=g).to(dt) if has_res else None
+            y = r.linear_patch_filter(x, wt, b, f, ln=ln, ln_eps=1e-5, residual=res)
+            key = f"{name}_{tag}"
+            out.update({f"{key}.x": x, f"{key}.w": wt, f"{key}.b": b, f"{key}.f": f, f"{key}.y": y})
+            if res is not None:
+                out[f"{key}.res"] = res
+    return {k: v.contiguous() for k, v in out.items()}
+
+
+def main(ref_root: str = "/root/reference", which: str = "all") -> None:
     sys.path.insert(0, os.path.join(ref_root, "python"))
     torch.manual_seed(0)
-    tensors, meta = nafnet_fixture(ref_root)
-    save_file(tensors, os.path.join(HERE, "nafnet_tiny.safetensors"), metadata=meta)
-    save_file(ops_fixture(ref_root), os.path.join(HERE, "ops_combined.safetensors"))
-    for f in ("nafnet_tiny.safetensors", "ops_combined.safetensors"):
+    written = []
+    if which in ("all", "nafnet"):
+        tensors, meta = nafnet_fixture(ref_root)
+        save_file(tensors, os.path.join(HERE, "nafnet_tiny.safetensors"), metadata=meta)
+        written.append("nafnet_tiny.safetensors")
+    if which in ("all", "ops"):
+        save_file(ops_fixture(ref_root), os.path.join(HERE, "ops_combined.safetensors"))
+        written.append("ops_combined.safetensors")
+    if which in ("all", "freq"):
+        save_file(freq_fixture(ref_root), os.path.join(HERE, "ops_freq.safetensors"),
+                  metadata={"cases": json.dumps(LPF_CASES)})
+        written.append("ops_freq.safetensors")
+    for f in written:
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 

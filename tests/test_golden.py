@@ -8,6 +8,9 @@ CPU: the oracle and the NAFNet harness reproduce the reference's outputs.
     TLC-map multiply or LN prologue and bias + gate + GELU + scale + residual, RMS linear,
     ln_mul_linear, conv3x3 with up2 + LeakyReLU + out_scale + residual, linear_per_image with
     bias + residual.
+  * linear_patch_filter calls of the reference TorchOps (LN / RMS / none, residual or not, fp32
+    and bf16, reflect-padded sizes) through the oracle, bit for bit; an oracle that rounded the
+    GEMM output to the activation dtype before the filter does not reproduce the bf16 cases.
 GPU (tests/test_hip_golden.py): the same fixtures through the `hip` backend.
 """
 from __future__ import annotations
@@ -38,6 +41,29 @@ def load_nafnet_fixture():
 
 def load_ops_fixture():
     return load_file(os.path.join(GOLDEN, "ops_combined.safetensors"))
+
+
+def load_freq_fixture():
+    """{case: (inputs dict, ln mode)} of ops_freq.safetensors."""
+    path = os.path.join(GOLDEN, "ops_freq.safetensors")
+    with safe_open(path, "pt") as f:
+        cases = json.loads(f.metadata()["cases"])
+    t = load_file(path)
+    out = {}
+    for name, *_, ln, _res in cases:
+        for tag in DT:
+            key = f"{name}_{tag}"
+            out[key] = ({k.split(".", 1)[1]: v for k, v in t.items() if k.startswith(key + ".")}, ln)
+    return out
+
+
+def run_linear_patch_filter(r, a, ln, dev, out_fp32=False):
+    """linear_patch_filter of one ops_freq case on backend-like `r` (ln_eps 1e-5, as written)."""
+    g = {k: v.to(dev) for k, v in a.items()}
+    if out_fp32:  # the same chain with the final cast left out (the oracle's value before rounding)
+        y = r.linear(g["x"], g["w"], g["b"], ln=ln, ln_eps=1e-5, out_dtype=torch.float32)
+        return r.patch_filter(y, g["f"], residual=g.get("res"), out_dtype=torch.float32)
+    return r.linear_patch_filter(g["x"], g["w"], g["b"], g["f"], ln=ln, ln_eps=1e-5, residual=g.get("res"))
 
 
 def tiny_nafnet(ops, tiny, sd):
@@ -111,3 +137,31 @@ def test_oracle_combined_ops_match_reference(tag):
         ref = t[f"{case}_{tag}.y"]
         assert y.dtype == ref.dtype and y.shape == ref.shape, case
         assert torch.equal(y, ref), (case, (y.float() - ref.float()).abs().max().item())
+
+
+def test_oracle_linear_patch_filter_matches_reference():
+    cases = load_freq_fixture()
+    assert len(cases) == 8
+    for key, (a, ln) in cases.items():
+        tag = key.rsplit("_", 1)[1]
+        y = run_linear_patch_filter(TorchRef(DT[tag], "cpu"), a, ln, "cpu")
+        assert y.dtype == a["y"].dtype == DT[tag] and y.shape == a["y"].shape, key
+        assert torch.equal(y, a["y"]), (key, (y.float() - a["y"].float()).abs().max().item())
+
+
+class _RoundedIntermediate(TorchRef):
+    """A planted mistake: the GEMM output rounded to the activation dtype before the filter."""
+
+    def linear_patch_filter(self, x, w, bias, f, ln=False, ln_eps=1e-6, residual=None):
+        y = self.linear(x, w, bias, ln=ln, ln_eps=ln_eps)
+        return self.patch_filter(y, f, residual=residual)
+
+
+def test_linear_patch_filter_fixture_catches_a_rounded_intermediate():
+    cases = load_freq_fixture()
+    wrong = 0
+    for key, (a, ln) in cases.items():
+        if key.endswith("_bf16"):
+            y = run_linear_patch_filter(_RoundedIntermediate(torch.bfloat16, "cpu"), a, ln, "cpu")
+            wrong += not torch.equal(y, a["y"])
+    assert wrong == 4

@@ -86,6 +86,92 @@ def test_config4_mdta(lvl, h, w, dt, hip_bf16, hip_f32):
                 what=f"mdta attn.V l{lvl} {dt}")
 
 
+def _blockdiag(blocks):
+    """The block-diagonal [N, C, C] matrix of per-head blocks [N, heads, ch, ch]."""
+    n, heads, ch, _ = blocks.shape
+    bd = torch.zeros(n, heads * ch, heads * ch, dtype=torch.float32)
+    for hh in range(heads):
+        bd[:, hh * ch:(hh + 1) * ch, hh * ch:(hh + 1) * ch] = blocks[:, hh].float()
+    return bd
+
+
+def _blockdiag_t(a):
+    """blockdiag(A_h^T) of an attention map [N, heads, ch, ch]: the per-image matrix the
+    Restormer block applies to v (python/clarus/models/restormer/__init__.py:203-208)."""
+    return _blockdiag(a.transpose(-1, -2))
+
+
+@pytest.mark.parametrize("lvl,h,w", CONFIG4)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_config4_attention_apply(lvl, h, w, dt, hip_bf16, hip_f32):
+    """HipOps.attention_apply (the config-4 attn . V the benchmark times: one batched GEMM launch
+    per image, the heads as the batch, v read from qkv with pixel stride 3C) against the oracle's
+    linear_per_image(v, blockdiag(A^T)), at every config-4 level. As in the benchmark, the maps
+    are passed as A^T per head in the activation dtype; fp32 output, then the backend's own."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(60 + lvl)
+    c, heads = 48 * 2 ** lvl, 2 ** lvl
+    qkv = rnd(g, 1, h, w, 3 * c, dtype=dt)
+    logits = rnd(g, 1, heads, 48, 48, scale=2.0)
+    a = torch.softmax(logits, -1)  # a row-stochastic map like channel_attention's
+    at = a.transpose(-1, -2).contiguous().to(dt)  # A^T per head
+    print(f"[attn.V] l{lvl} {dt}", flush=True)
+    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag(at), out_dtype=torch.float32)
+    got = hip.attention_apply(qkv.cuda(), at.cuda(), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), ref, rel=1e-5, what=f"attention_apply l{lvl} {dt}")
+    got = hip.attention_apply(qkv.cuda(), at.cuda())
+    assert got.dtype == dt
+    if dt == torch.bfloat16:
+        assert_bf16(got.cpu(), ref, what=f"attention_apply l{lvl} bf16 out")
+    else:
+        assert_fp32(got.cpu(), ref, rel=1e-5, what=f"attention_apply l{lvl} fp32 out")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_attention_apply_batch_and_residual(dt, hip_bf16, hip_f32):
+    """Two images (the per-image loop), 4 heads of 24 channels, a residual and a ragged pixel
+    count; attn given as [heads, ch, ch] for one image is rejected for two."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(70)
+    n, h, w, heads, ch = 2, 13, 29, 4, 24
+    c = heads * ch
+    qkv = rnd(g, n, h, w, 3 * c, dtype=dt)
+    at = torch.softmax(rnd(g, n, heads, ch, ch, scale=2.0), -1).transpose(-1, -2).contiguous()
+    res = rnd(g, n, h, w, c, dtype=dt)
+    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag(at), residual=res, out_dtype=torch.float32)
+    got = hip.attention_apply(qkv.cuda(), at.cuda(), residual=res.cuda(), out_dtype=torch.float32)
+    assert_fp32(got.cpu(), ref, rel=1e-5, what=f"attention_apply batch 2 + residual {dt}")
+    from clarus_amd.dispatch import Unsupported
+    with pytest.raises(Unsupported):
+        hip.attention_apply(qkv.cuda(), at[0].cuda())
+
+
+@pytest.mark.parametrize("lvl", [0, 2])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_restormer_mix_fold(lvl, dt, hip_bf16, hip_f32):
+    """The Restormer block's attention output path (python/clarus/models/restormer/__init__.py:
+    203-210): the map from channel_attention, mix = blockdiag(A^T) @ proj.w per image, then
+    linear_per_image(v, mix, residual=x, bias=proj.b), all on `hip`, against the same chain on
+    the oracle. Level 0 at 180x320 (1 head), level 2 (4 heads) at 90x160."""
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(80 + lvl)
+    c, heads = 48 * 2 ** lvl, 2 ** lvl
+    h, w = (180, 320) if lvl == 0 else (90, 160)
+    qkv = rnd(g, 1, h, w, 3 * c, dtype=dt)
+    t = torch.rand(heads, generator=g) * 1.5 + 0.5
+    proj_w, proj_b = rnd(g, c, c, scale=c ** -0.5), rnd(g, c, scale=0.1)
+    x = rnd(g, 1, h, w, c, dtype=dt)
+    a_hip = hip.channel_attention(qkv.cuda(), heads, t.cuda())
+    mix_hip = _blockdiag_t(a_hip.cpu()).cuda() @ proj_w.cuda()
+    got = hip.linear_per_image(qkv.cuda()[..., 2 * c:], mix_hip, residual=x.cuda(), out_dtype=torch.float32,
+                               bias=proj_b.cuda())
+    a_ref = REF.channel_attention(qkv, heads, t)
+    mix_ref = _blockdiag_t(a_ref) @ proj_w
+    ref = REF.linear_per_image(qkv[..., 2 * c:], mix_ref, residual=x, out_dtype=torch.float32, bias=proj_b)
+    # the map carries the attention's own error (1e-4 relative for bf16 q / k, as in test_config4_mdta)
+    assert_fp32(got.cpu(), ref, rel=1e-5 if dt == torch.float32 else 1e-4, what=f"restormer mix l{lvl} {dt}")
+
+
 # ------------------------------------------------------------------ patch DFT ops
 @pytest.mark.parametrize("h,w", [(64, 96), (45, 81), (16, 8)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])

@@ -5,6 +5,8 @@
   clarus_amd.nafnet.NAFNet on `hip`: fp32 activations within 1e-5 of the output scale; bf16
   activations with |dPSNR| <= 1e-3 dB against a synthetic target (north star), and every
   GEMM-family op, the depthwise conv and the box mean served by `hip`.
+* The reference's linear_patch_filter calls on `hip`: fp32 within 1e-5 relative, bf16 outputs by the
+  bf16 rule against the oracle's fp32 value before the final cast (the fixture rounds to it).
 * The reference's combined-epilogue TorchOps calls on `hip`: fp32 backends within 1e-5
   relative, bf16 backends within 1e-5 relative where the reference output is fp32 and by the
   bf16 rule (2e-2 absolute, rounding flips allowed) where it is bf16.
@@ -20,7 +22,8 @@ from clarus_amd.dispatch import Ops, Unsupported
 from clarus_amd.nafnet import psnr
 from oracle.torch_ref import Small, TorchRef
 from tests._tol import assert_bf16, assert_fp32
-from tests.test_golden import DT, load_nafnet_fixture, load_ops_fixture, run_combined, tiny_nafnet
+from tests.test_golden import (DT, load_freq_fixture, load_nafnet_fixture, load_ops_fixture, run_combined,
+                               run_linear_patch_filter, tiny_nafnet)
 
 pytestmark = pytest.mark.gpu
 
@@ -84,3 +87,28 @@ def test_hip_declines_ln_with_mul_like_the_reference(gpu_device):
     g = {k.split(".")[1]: v.to(gpu_device) for k, v in t.items() if k.startswith("lin1_fp32.")}
     with pytest.raises(Unsupported):
         ops.linear(g["x"], g["w"], g["b"], ln=True, gate=True, mul=Small(g["map"], 2, 3, 9, 13))
+
+
+@pytest.mark.parametrize("tag", ["fp32", "bf16"])
+def test_hip_linear_patch_filter_vs_reference(tag, gpu_device):
+    print(f"[golden] linear_patch_filter {tag}", flush=True)
+    ops = Ops(["hip"], DT[tag], gpu_device, log=print)
+    assert "hip" in ops.by_name, ops.skipped
+    for key, (a, ln) in load_freq_fixture().items():
+        if not key.endswith(tag):
+            continue
+        y = run_linear_patch_filter(ops, a, ln, gpu_device).cpu()
+        ref = a["y"]
+        assert y.dtype == ref.dtype and y.shape == ref.shape, key
+        if tag == "fp32":
+            e = assert_fp32(y, ref, what=key)
+            print(f"[golden] {key} rel err {e:.2e}")
+        else:
+            # the oracle's fp32 value before the cast, on this host's CPU: the fixture (written on
+            # another CPU, whose summation order may differ in the last fp32 bits) must be a
+            # rounding of it up to rounding flips; tests/test_golden.py pins it bit for bit
+            r32 = run_linear_patch_filter(TorchRef(DT[tag], "cpu"), a, ln, "cpu", out_fp32=True)
+            assert_bf16(ref, r32, what=key + " (fixture vs this host's oracle)")
+            d, flips = assert_bf16(y, r32, what=key)
+            print(f"[golden] {key} max|d| {d:.2e} flips {flips}")
+    assert list(ops.report()["ops"]["linear_patch_filter"]) == ["hip"]

@@ -3,8 +3,8 @@
 Every kernel here has a fixed reduction order and the library records no memset nodes, so each
 replay must reproduce the eager forward bit for bit; the replays are interleaved with eager work
 and host synchronisations (a graph replayed once can hide state that only a later replay
-exposes). The captured forward includes the GEMMs that hand LayerNorm rows to the next GEMM
-(clarus_hip_gemm_ln_rows), whose buffers the capture must keep alive.
+exposes). The captured forward includes the fused residual GEMM -> LayerNorm -> GEMM pairs
+(clarus_hip_gemm_ln_gemm) and their packed second weights, which the eager warm-up builds.
 """
 from __future__ import annotations
 
@@ -28,7 +28,7 @@ def test_nafnet_graph_replays_match_eager(gpu_device):
     stream = torch.cuda.Stream(dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(stream):
-        eager = model.forward(x).clone()  # warm-up: weight re-layouts, LN hint
+        eager = model.forward(x).clone()  # warm-up: weight re-layouts
         eager2 = model.forward(x).clone()
     torch.cuda.synchronize()
     assert torch.equal(eager, eager2), "eager forwards differ"
@@ -37,7 +37,9 @@ def test_nafnet_graph_replays_match_eager(gpu_device):
         y = model.forward(x)
     torch.cuda.synchronize()
     served = ops.report()["ops"]
-    assert list(served.get("linear", {"hip": 0})) == ["hip"], served.get("linear")
+    for op in ("linear", "linear_ln_linear"):
+        assert list(served.get(op, {})) == ["hip"], (op, served.get(op))
+    assert ops.by_name["hip"].pair_launches["gemm_ln_gemm"] > 0
     for rep in range(4):
         graph.replay()
         torch.cuda.synchronize()

@@ -281,3 +281,53 @@ def test_linear_ln_linear_unfused_is_two_linears():
     y, u = b.linear_ln_linear(x, w1, residual=x, w2=w2, gate2=True, ln="rms", ln_eps=1e-5)
     assert torch.equal(y, x @ w1) and torch.equal(u, (x @ w1) @ w2)
     assert calls[0]["residual"] is x and calls[1] == {"ln": "rms", "gate": True, "ln_eps": 1e-5}
+
+
+def test_pair_default_for_a_host_backend_base():
+    """Inside a clarus installation Backend is clarus's own class, which has no linear_ln_linear:
+    the two-linear default is attached to it, so every backend answers the op."""
+    class HostBase:  # a host's backend base without the op
+        def __init__(self, dtype, device):
+            self.dtype, self.device = dtype, device
+
+    dispatch.give_pair_default(HostBase)
+    assert HostBase.linear_ln_linear is dispatch.linear_ln_linear_unfused
+
+    class Own(HostBase):
+        def linear_ln_linear(self, *a, **k):
+            return "own"
+    dispatch.give_pair_default(Own)  # a class with its own op keeps it
+    assert Own(torch.float32, "cpu").linear_ln_linear() == "own"
+
+
+class _PlainOracle:
+    """A backend that does not derive from Backend and has no linear_ln_linear."""
+    name = "plain_oracle"
+
+    def __init__(self, dtype, device):
+        self.dtype, self.device = dtype, device
+        self._r = TorchRef(dtype, device)
+
+    def __getattr__(self, op):
+        if op.startswith("_") or op == "linear_ln_linear":
+            raise AttributeError(op)
+        return getattr(self._r, op)
+
+
+def test_nafnet_pairs_match_the_reference_call_pattern():
+    """The harness's paired calls (conv3 -> conv4, conv5 -> next conv1 in a stage of two blocks)
+    give exactly the reference block's five-linear result (fused_pairs=False) on the oracle,
+    and the harness falls back to the two linear calls when no backend has the pair op."""
+    from clarus_amd.nafnet import NAFNet, random_state_dict
+    register_backend("plain_oracle")(_PlainOracle)
+    enc, mid, dec = [2, 1], 2, [1, 2]
+    sd = random_state_dict(8, enc, mid, dec, seed=4)
+    x = torch.rand(1, 3, 24, 40, generator=torch.Generator().manual_seed(2))
+    outs = []
+    for backend, fused in (("oracle_by_path", True), ("oracle_by_path", False), ("plain_oracle", True)):
+        ops = Ops([backend], torch.float32, torch.device("cpu"), log=lambda *a: None)
+        model = NAFNet(ops, width=8, enc=enc, mid=mid, dec=dec, tlc=(24, 40), state_dict=sd, fused_pairs=fused)
+        outs.append(model.forward(x))
+        calls = ops.report()["ops"]
+        assert ("linear_ln_linear" in calls) == (fused and backend == "oracle_by_path"), calls
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
