@@ -185,7 +185,8 @@ def summarize_pmc(dirs: list, cases_file: str) -> None:
                 out[f"{cn.lower()}_factor"] = round(COPY_BYTES / (copy[2][cn] * 1024.0), 4)
         for (name, _cfg, flops, nbytes), grp in zip(meta, ops):
             o = out["ops"].setdefault(name, {"algorithmic_bytes": nbytes, "algorithmic_flops": flops})
-            o["kernels"] = sorted({g[1].split("(")[0].replace("void ", "")[:100] for g in grp})
+            o["kernels"] = sorted({g[1].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:100]
+                                   for g in grp})
             for cn in ("FETCH_SIZE", "WRITE_SIZE"):
                 if cn in copy[2]:
                     o[f"{cn.lower()}_bytes"] = round(sum(g[2].get(cn, 0.0) for g in grp) * 1024.0
@@ -262,7 +263,7 @@ def cpu_legs(step, others, e2e_reps: int, log=print) -> dict:
     for c in step + others:
         if c.cpu_run is None:
             continue
-        r = refs[torch.float32 if c.dtype == "fp32" and c.config in (1, 3) else torch.bfloat16]
+        r = refs[torch.float32 if c.dtype == "fp32" else torch.bfloat16]
         if c.config == 4:
             r = refs[torch.float32 if c.name.endswith("fp32") else torch.bfloat16]
         with torch.no_grad():
@@ -343,7 +344,7 @@ def main() -> None:
     log(f"[bench] config-2 step: {len(step)} GEMMs, {flops_step / 1e9:.2f} GFLOP")
     others = [] if args.no_ops else (wl.config1_cases(hip32, dev) + wl.config3_cases(hip32, dev)
                                      + wl.config4_cases(hip, hip32, dev) + wl.config5_cases(hip, dev)
-                                     + [wl.nafnet_pair_case(hip, dev)])
+                                     + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev)])
     if args.pmc_pass:  # the last dispatches: two markers, the copy, then a marker before each op and one after
         cases = wl.all_cases(hip, hip32, dev)
         os.makedirs(os.path.dirname(os.path.abspath(args.pmc_cases)), exist_ok=True)

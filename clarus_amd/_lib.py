@@ -72,6 +72,8 @@ SIGNATURES = {
     "clarus_hip_channel_attention_noalloc": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "clarus_hip_patch_filter": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _i32,
                                        _i64, _i64, _i64, _i64, _vp]),
+    "clarus_hip_linear_patch_filter": (_i32, [_vp, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp,
+                                              _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
     "clarus_hip_patch_corr": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
                                      _i64, _i64, _vp]),
     "clarus_hip_dwconv3x3": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32,

@@ -330,9 +330,10 @@ __global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restric
 static int pick_nb(int64_t ch) { return (int)((ch + 15) / 16); }
 
 static int64_t split_len_for(int64_t batch, int64_t heads, int64_t hw) {
-  // ~512 workgroups in total (two per CU), whole chunks per split: long splits amortise the
-  // per-split reduction epilogue
-  int64_t want = (512 + batch * heads - 1) / (batch * heads);
+  // ~2 workgroups per CU in total, whole chunks per split: long splits amortise the per-split
+  // reduction epilogue
+  const int64_t wgs = 2LL * device_cus();
+  int64_t want = (wgs + batch * heads - 1) / (batch * heads);
   if (want < 1) want = 1;
   int64_t len = (hw + want - 1) / want;
   len = (len + GP_CHUNK - 1) / GP_CHUNK * GP_CHUNK;
@@ -364,6 +365,7 @@ static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const fl
     hipLaunchKernelGGL((gram_finish_kernel<NB>), dim3((unsigned)(batch * heads)), dim3(256), 0, s, part2,     \
                        temperature, out, (int)ch, (int)heads);                                                \
   } while (0)
+  note_kernel("gram_partial_kernel + gram_reduce_kernel + gram_finish_kernel nb=%d", nb);
   switch (nb) {
     case 1: CLARUS_GRAM(1); break;
     case 2: CLARUS_GRAM(2); break;

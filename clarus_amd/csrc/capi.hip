@@ -1,4 +1,5 @@
 // Library-wide C entry points: ABI version, struct sizes, per-thread error text.
+#include <atomic>
 #include <string.h>
 
 #include "capi.hpp"
@@ -15,6 +16,19 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_err[0] = 0; }
+
+static std::atomic<int> g_cus[64];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = g_cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 static thread_local char g_kernel[160];
 

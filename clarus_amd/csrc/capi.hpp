@@ -13,6 +13,10 @@ namespace clarus {
 // record the calling thread's last failure (read by clarus_hip_last_error)
 void set_error(const char* fmt, ...);
 void clear_error();
+// compute units of the calling thread's current device (hipDeviceAttributeMultiprocessorCount,
+// looked up once per device; 256 on a whole MI355X, fewer on a partition); sizes persistent grids
+int device_cus();
+
 // record the kernel a launching entry point chose for the calling thread's current call (read by
 // clarus_hip_last_kernel); a diagnostic only, never read by the dispatch
 void note_kernel(const char* fmt, ...);

@@ -25,7 +25,7 @@ void launch_one(GemmP& p, hipStream_t s) {
   const int64_t H = (int64_t)p.h << (UP2 ? 1 : 0), W = (int64_t)p.w << (UP2 ? 1 : 0);
   const int64_t ptiles = (p.m / (H * W)) * cdiv(H, CH_TH) * cdiv(W, CH_TW);
   const int64_t ncol = cdiv(p.n, TR);
-  int64_t per_col = 256LL * per_cu / ncol;  // persistent: every workgroup resident
+  int64_t per_col = (int64_t)device_cus() * per_cu / ncol;  // persistent: every workgroup resident
   if (per_col < 1) per_col = 1;
   if (per_col > ptiles) per_col = ptiles;
   hipLaunchKernelGGL(fn, dim3((unsigned)(per_col * ncol)), dim3(512), lds, s, p);

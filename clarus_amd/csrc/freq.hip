@@ -47,40 +47,46 @@ constexpr int IBYTES = 64 * IROWB;
 
 __device__ __forceinline__ bf16x8 lds8(const unsigned char* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-template <int XDT, bool CORR>
-__global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
-  __shared__ __attribute__((aligned(16))) unsigned char fw[2 * FBYTES];  // hi, then lo
-  __shared__ __attribute__((aligned(16))) unsigned char iv[2 * IBYTES];
-  // staging with 16-byte loads: 4 consecutive k of one row per step, split into 8-byte hi / lo
-  auto put4 = [](unsigned char* dhi, unsigned char* dlo, const f32x4 f) __attribute__((always_inline)) {
-    bf16_t h[4], l[4];
+// 4 consecutive fp32 values written to LDS as 8-byte bf16 hi / lo runs (x = hi + lo)
+__device__ __forceinline__ void put4_split(unsigned char* dhi, unsigned char* dlo, const f32x4 f) {
+  bf16_t h[4], l[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = (bf16_t)f[i];
-      l[i] = (bf16_t)(f[i] - (float)h[i]);
-    }
-    *reinterpret_cast<u32x2*>(dhi) = u32x2{(unsigned)__builtin_bit_cast(unsigned short, h[0]) |
-                                               ((unsigned)__builtin_bit_cast(unsigned short, h[1]) << 16),
-                                           (unsigned)__builtin_bit_cast(unsigned short, h[2]) |
-                                               ((unsigned)__builtin_bit_cast(unsigned short, h[3]) << 16)};
-    *reinterpret_cast<u32x2*>(dlo) = u32x2{(unsigned)__builtin_bit_cast(unsigned short, l[0]) |
-                                               ((unsigned)__builtin_bit_cast(unsigned short, l[1]) << 16),
-                                           (unsigned)__builtin_bit_cast(unsigned short, l[2]) |
-                                               ((unsigned)__builtin_bit_cast(unsigned short, l[3]) << 16)};
-  };
-  for (int e = threadIdx.x; e < NCOEF * 16; e += 256) {  // Fwd [80][64]: 16 groups of 4 per row
-    const int r = e >> 4, k = (e & 15) * 4;
-    const f32x4 f = *reinterpret_cast<const f32x4*>(p.fwd + r * 64 + k);
-    put4(fw + r * FROWB + k * 2, fw + FBYTES + r * FROWB + k * 2, f);
+  for (int i = 0; i < 4; ++i) {
+    h[i] = (bf16_t)f[i];
+    l[i] = (bf16_t)(f[i] - (float)h[i]);
   }
+  *reinterpret_cast<u32x2*>(dhi) = u32x2{(unsigned)__builtin_bit_cast(unsigned short, h[0]) |
+                                             ((unsigned)__builtin_bit_cast(unsigned short, h[1]) << 16),
+                                         (unsigned)__builtin_bit_cast(unsigned short, h[2]) |
+                                             ((unsigned)__builtin_bit_cast(unsigned short, h[3]) << 16)};
+  *reinterpret_cast<u32x2*>(dlo) = u32x2{(unsigned)__builtin_bit_cast(unsigned short, l[0]) |
+                                             ((unsigned)__builtin_bit_cast(unsigned short, l[1]) << 16),
+                                         (unsigned)__builtin_bit_cast(unsigned short, l[2]) |
+                                             ((unsigned)__builtin_bit_cast(unsigned short, l[3]) << 16)};
+}
+
+// Inv staged as the B-order operand of the inverse product (shared by both kernels)
+__device__ __forceinline__ void stage_inv(unsigned char* iv, const float* inv) {
   for (int e = threadIdx.x; e < 64 * 24; e += 256) {  // Inv [64][96 permuted]: 24 groups of 4 per row
     const int r = e / 24, kk = (e - (e / 24) * 24) * 4;
     const int kb = kk >> 5, g = (kk >> 3) & 3, i = kk & 7;  // i = 0 or 4
     const int coef = 16 * (2 * kb + (i >> 2)) + 4 * g;       // 4 consecutive coefficients
-    const f32x4 f = coef < NCOEF ? *reinterpret_cast<const f32x4*>(p.inv + r * NCOEF + coef)
+    const f32x4 f = coef < NCOEF ? *reinterpret_cast<const f32x4*>(inv + r * NCOEF + coef)
                                  : f32x4{0.f, 0.f, 0.f, 0.f};
-    put4(iv + r * IROWB + kk * 2, iv + IBYTES + r * IROWB + kk * 2, f);
+    put4_split(iv + r * IROWB + kk * 2, iv + IBYTES + r * IROWB + kk * 2, f);
   }
+}
+
+template <int XDT, bool CORR>
+__global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
+  __shared__ __attribute__((aligned(16))) unsigned char fw[2 * FBYTES];  // hi, then lo
+  __shared__ __attribute__((aligned(16))) unsigned char iv[2 * IBYTES];
+  for (int e = threadIdx.x; e < NCOEF * 16; e += 256) {  // Fwd [80][64]: 16 groups of 4 per row
+    const int r = e >> 4, k = (e & 15) * 4;
+    const f32x4 f = *reinterpret_cast<const f32x4*>(p.fwd + r * 64 + k);
+    put4_split(fw + r * FROWB + k * 2, fw + FBYTES + r * FROWB + k * 2, f);
+  }
+  stage_inv(iv, p.inv);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -90,10 +96,16 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
   const int H = (int)p.h, W = (int)p.w;
   constexpr int XES = (XDT == DT_BF16) ? 2 : 4;
 
-  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < p.units; u += (int64_t)gridDim.x * 4) {
-    // compiler-only barrier: re-read the operator fragments from LDS per unit instead of
-    // hoisting all of them into registers (which would cost occupancy)
-    asm volatile("" ::: "memory");
+  // a unit's inputs: this lane's 8 pixels of k-block kb (row 4 kb + lg of the patch, columns
+  // 0..7), reflect padding at the bottom / right edge (torch F.pad mode="reflect"), interior
+  // patches (uniform per wave) addressed with 32-bit offsets from the patch origin; and its
+  // filter gains. The next unit's are loaded before the current one is computed, so their
+  // memory latency overlaps the current unit's products and stores.
+  struct UnitIn {
+    f32x8 x[2], k[CORR ? 2 : 1];
+    f32x4 g[CORR ? 1 : 5];
+  };
+  auto load_unit = [&](int64_t u, UnitIn& in) __attribute__((always_inline)) {
     const int cb = (int)(u % cblocks);
     const int64_t patch = u / cblocks;
     const int64_t n = patch / ((int64_t)ph * pw);
@@ -102,15 +114,9 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
     const int64_t ch = (int64_t)cb * 16 + lc;
     const bool cval = ch < p.c;
     const int64_t chl = cval ? ch : 0;
-
-    // this lane's 8 pixels of k-block kb: row 4 kb + lg (0..7), columns 0..7 of the patch;
-    // reflect padding at the bottom / right edge (torch F.pad mode="reflect"). Interior patches
-    // (uniform per wave) address with 32-bit offsets from the patch origin.
     const bool interior = py * 8 + 8 <= H && px * 8 + 8 <= W;
-    bf16x8 xh[2], xl[2], kh[2], kl[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      f32x8 xv, kv;
       if (interior && p.small_offsets) {
         const unsigned char* o0 = (const unsigned char*)p.x +
                                   (n * p.sn + (int64_t)(py * 8) * p.sh + (int64_t)(px * 8) * p.sw + chl) * XES;
@@ -118,14 +124,14 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const int o = rowo + s * (int)p.sw;
-          xv.v[s] = cval ? (XDT == DT_BF16 ? bf16_to_f32(*reinterpret_cast<const unsigned short*>(o0 + (int64_t)o * 2))
-                                           : *reinterpret_cast<const float*>(o0 + (int64_t)o * 4))
-                         : 0.f;
+          in.x[kb].v[s] = cval ? (XDT == DT_BF16 ? bf16_to_f32(*reinterpret_cast<const unsigned short*>(o0 + (int64_t)o * 2))
+                                                 : *reinterpret_cast<const float*>(o0 + (int64_t)o * 4))
+                               : 0.f;
           if constexpr (CORR)
-            kv.v[s] = cval ? (XDT == DT_BF16
-                                  ? bf16_to_f32(*reinterpret_cast<const unsigned short*>(o0 + ((int64_t)o + p.c) * 2))
-                                  : *reinterpret_cast<const float*>(o0 + ((int64_t)o + p.c) * 4))
-                           : 0.f;
+            in.k[kb].v[s] = cval ? (XDT == DT_BF16
+                                        ? bf16_to_f32(*reinterpret_cast<const unsigned short*>(o0 + ((int64_t)o + p.c) * 2))
+                                        : *reinterpret_cast<const float*>(o0 + ((int64_t)o + p.c) * 4))
+                                 : 0.f;
         }
       } else {
         int yy = py * 8 + kb * 4 + lg;
@@ -136,12 +142,42 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
           int xx = px * 8 + s;
           if (xx >= W) xx = 2 * (W - 1) - xx;
           const int64_t o = rowoff + (int64_t)xx * p.sw;
-          xv.v[s] = cval ? load1(p.x, XDT, o + chl) : 0.f;
-          if constexpr (CORR) kv.v[s] = cval ? load1(p.x, XDT, o + p.c + chl) : 0.f;
+          in.x[kb].v[s] = cval ? load1(p.x, XDT, o + chl) : 0.f;
+          if constexpr (CORR) in.k[kb].v[s] = cval ? load1(p.x, XDT, o + p.c + chl) : 0.f;
         }
       }
-      split_bf16(xv, xh[kb], xl[kb]);
-      if constexpr (CORR) split_bf16(kv, kh[kb], kl[kb]);
+    }
+    if constexpr (!CORR) {
+#pragma unroll
+      for (int rb = 0; rb < 5; ++rb)
+        in.g[rb] = cval ? *reinterpret_cast<const f32x4*>(p.gain + chl * NCOEF + rb * 16 + lg * 4)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  const int64_t ustride = (int64_t)gridDim.x * 4;
+  UnitIn nxt;
+  int64_t u = (int64_t)blockIdx.x * 4 + wave;
+  if (u < p.units) load_unit(u, nxt);
+  for (; u < p.units; u += ustride) {
+    // compiler-only barrier: re-read the operator fragments from LDS per unit instead of
+    // hoisting all of them into registers (which would cost occupancy)
+    asm volatile("" ::: "memory");
+    const UnitIn cur = nxt;
+    if (u + ustride < p.units) load_unit(u + ustride, nxt);
+    const int cb = (int)(u % cblocks);
+    const int64_t patch = u / cblocks;
+    const int64_t n = patch / ((int64_t)ph * pw);
+    const int rem = (int)(patch - n * ph * pw);
+    const int py = rem / pw, px = rem - (rem / pw) * pw;
+    const int64_t ch = (int64_t)cb * 16 + lc;
+    const bool cval = ch < p.c;
+
+    bf16x8 xh[2], xl[2], kh[2], kl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      split_bf16(cur.x[kb], xh[kb], xl[kb]);
+      if constexpr (CORR) split_bf16(cur.k[kb], kh[kb], kl[kb]);
     }
 
     // ---- forward: d1[rb] rows = coefficients 16 rb + 4 lg + j, column = channel lc
@@ -175,10 +211,8 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
         d1[rb][2] = cr * dr - ci * di;
         d1[rb][3] = cr * di + ci * dr;
       } else {
-        const f32x4 g = cval ? *reinterpret_cast<const f32x4*>(p.gain + chl * NCOEF + rb * 16 + lg * 4)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d1[rb][j] *= g[j];
+        for (int j = 0; j < 4; ++j) d1[rb][j] *= cur.g[rb][j];
       }
     }
     // the B operand of the inverse: k-block kb2 = coefficient row blocks 2 kb2, 2 kb2 + 1
@@ -222,6 +256,253 @@ __global__ void __launch_bounds__(256) patch_kernel(const FreqP p) {
   }
 }
 
+// ---------------------------------------------------------------- fused (LN) GEMM + patch filter
+// out = patch_filter(prologue(x) . W + bias) (+ residual), the GEMM output never leaving the
+// wave. Unit = (8x8 patch, CB blocks of 16 output channels), one wave:
+//   GEMM  D[pb] (16 patch pixels 16 pb .. 16 pb + 15 as MFMA rows x the 16 channels) =
+//         A[pixels][K] . W[K][channels] on 16x16x32 bf16 MFMAs; A rows are read straight from
+//         the NHWC input (reflected coordinates past the bottom / right edge, which is the
+//         reference's reflect padding of the GEMM output, since the GEMM is per pixel), with the
+//         LayerNorm / RMS prologue applied in fp32 from the row values held in registers (the 4
+//         lanes of a pixel row hold all K) and the normalised values entered as bf16 hi + lo
+//         pairs (fp32 A too); with fp32 weights the GEMM runs on fp32 16x16x4 MFMAs instead.
+//   lane (channel lc, group lg) then holds D[pb][j] = pixel 16 pb + 4 lg + j. The forward DFT
+//   takes those registers as its B operand unchanged: its k slot (lg, i) of k-block kb stands
+//   for pixel 32 kb + 16 (i / 4) + 4 lg + i % 4, and Fwd's columns are staged in that order.
+//   Then gain, inverse, residual and store as patch_kernel. Each operator fragment read from LDS
+//   and each A row read and normalised serves all CB channel blocks of the unit.
+struct LpfP {
+  const void* x;    // [batch, h, w, k] contiguous
+  const void* wt;   // W^T [n][k]
+  const float* bias;
+  const float* fwd;
+  const float* inv;
+  const float* gain;  // [n][80]
+  const void* res;
+  void* out;          // [batch, h, w, n] contiguous
+  int64_t batch, h, w, k, n;
+  int64_t units;
+  float eps;
+  int r_dt, o_dt;
+};
+
+template <int XDT, int LN, bool WS, int CB, int KS>
+__global__ void __launch_bounds__(256) lpf_kernel(const LpfP p) {
+  __shared__ __attribute__((aligned(16))) unsigned char fw[2 * FBYTES];  // Fwd hi, lo (columns permuted)
+  __shared__ __attribute__((aligned(16))) unsigned char iv[2 * IBYTES];
+  for (int e = threadIdx.x; e < NCOEF * 16; e += 256) {  // Fwd [80][64] in the GEMM's pixel order
+    const int r = e >> 4, c4 = (e & 15) * 4;             // staged columns c4 .. c4 + 3
+    const int kb = c4 >> 5, lgs = (c4 >> 3) & 3, i0 = c4 & 7;  // i0 = 0 or 4
+    const int px0 = 32 * kb + 16 * (i0 >> 2) + 4 * lgs;  // 4 consecutive pixels
+    const f32x4 f = *reinterpret_cast<const f32x4*>(p.fwd + r * 64 + px0);
+    put4_split(fw + r * FROWB + c4 * 2, fw + FBYTES + r * FROWB + c4 * 2, f);
+  }
+  stage_inv(iv, p.inv);
+  __syncthreads();
+
+  constexpr bool AS = LN != 0 || XDT == DT_F32 || WS;  // A not entered as it stands
+  constexpr int XES = XDT == DT_BF16 ? 2 : 4;
+  constexpr int WES = WS ? 4 : 2;
+  constexpr int MAXS = KS;                              // LN rows in registers: K <= 32 KS
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  const int H = (int)p.h, W = (int)p.w, K = (int)p.k;
+  const int ph = (int)cdiv(p.h, 8), pw = (int)cdiv(p.w, 8);
+  const int ctiles = (int)cdiv(p.n, 16 * CB);  // channel tiles of CB 16-channel blocks
+  const int S = (int)cdiv(p.k, 32);            // 32-k steps
+  const float invk = 1.0f / (float)K;
+
+  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < p.units; u += (int64_t)gridDim.x * 4) {
+    asm volatile("" ::: "memory");
+    const int ct = (int)(u % ctiles);
+    const int64_t patch = u / ctiles;
+    const int64_t n = patch / ((int64_t)ph * pw);
+    const int rem = (int)(patch - n * ph * pw);
+    const int py = rem / pw, px = rem - (rem / pw) * pw;
+    int64_t chl[CB];
+    bool cval[CB];
+    const unsigned char* wrow[CB];
+    float bias[CB];
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      const int64_t ch = ((int64_t)ct * CB + b) * 16 + lc;
+      cval[b] = ch < p.n;
+      chl[b] = cval[b] ? ch : 0;
+      wrow[b] = (const unsigned char*)p.wt + chl[b] * p.k * WES;
+      bias[b] = (cval[b] && p.bias) ? p.bias[chl[b]] : 0.f;
+    }
+
+    // ---- GEMM: dd[b][pb] = prologue(A) . W (channel block b), + bias; each A row is loaded and
+    // normalised once for the CB blocks
+    f32x4 dd[CB][4];
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      const int pp = pb * 16 + lc;  // this lane's A row: patch pixel pp
+      int yy = py * 8 + (pp >> 3), xx = px * 8 + (pp & 7);
+      if (yy >= H) yy = 2 * (H - 1) - yy;
+      if (xx >= W) xx = 2 * (W - 1) - xx;
+      const unsigned char* arow = (const unsigned char*)p.x + (((n * H + yy) * W + xx) * p.k) * XES;
+#pragma unroll
+      for (int b = 0; b < CB; ++b) dd[b][pb] = f32x4{bias[b], bias[b], bias[b], bias[b]};
+      float mean = 0.f, rstd = 1.f;
+      f32x8 a[LN != 0 ? MAXS : 1];
+      if constexpr (LN != 0) {
+        // the row in registers (K <= 256), exact two-pass statistics over the 4 lanes of the row
+        float s1 = 0.f;
+#pragma unroll
+        for (int st = 0; st < MAXS; ++st) {
+          const int k0 = st * 32 + lg * 8;
+          a[st] = (st < S && k0 < K) ? load8<XDT>(arow + (int64_t)k0 * XES) : zero8();
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s1 += a[st].v[i];
+        }
+        mean = LN == 1 ? sum_col4(s1) * invk : 0.f;
+        float s2 = 0.f;
+#pragma unroll
+        for (int st = 0; st < MAXS; ++st) {
+          const bool kv = st < S && st * 32 + lg * 8 < K;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float d = kv ? a[st].v[i] - mean : 0.f;
+            s2 += d * d;
+          }
+        }
+        rstd = rsqrtf(sum_col4(s2) * invk + p.eps);
+      }
+      // LN rows: a constant trip count, fully unrolled (the row stays in registers); otherwise
+      // a runtime loop over the steps (nothing indexed by the step)
+      constexpr int NST = LN != 0 ? MAXS : 1;
+#pragma unroll
+      for (int st0 = 0; st0 < (LN != 0 ? NST : S); ++st0) {
+        const int st = st0;
+        if (LN != 0 && st >= S) continue;
+        const int k0 = st * 32 + lg * 8;
+        const bool kv = k0 < K;
+        if constexpr (!AS) {  // bf16 rows and bf16 weights: one product
+          const bf16x8 av = kv ? *reinterpret_cast<const bf16x8*>(arow + (int64_t)k0 * 2) : bf16x8{};
+#pragma unroll
+          for (int b = 0; b < CB; ++b) {
+            const bf16x8 wv = (cval[b] && kv) ? *reinterpret_cast<const bf16x8*>(wrow[b] + (int64_t)k0 * 2) : bf16x8{};
+            dd[b][pb] = mfma_bf16(av, wv, dd[b][pb]);
+          }
+        } else {
+          f32x8 v;
+          if constexpr (LN != 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v.v[i] = kv ? (a[st0 < NST ? st0 : 0].v[i] - mean) * rstd : 0.f;
+          } else {
+            v = kv ? load8<XDT>(arow + (int64_t)k0 * XES) : zero8();
+          }
+          if constexpr (WS) {  // fp32 weights: fp32 MFMAs, slot i = instruction i's k
+#pragma unroll
+            for (int b = 0; b < CB; ++b) {
+              const f32x8 wv = (cval[b] && kv) ? load8<DT_F32>(wrow[b] + (int64_t)k0 * 4) : zero8();
+#pragma unroll
+              for (int i = 0; i < 8; ++i) dd[b][pb] = mfma_f32(v.v[i], wv.v[i], dd[b][pb]);
+            }
+          } else {  // bf16 weights: A as hi + lo pairs
+            bf16x8 ah, al;
+            split_bf16(v, ah, al);
+#pragma unroll
+            for (int b = 0; b < CB; ++b) {
+              const bf16x8 wv = (cval[b] && kv) ? *reinterpret_cast<const bf16x8*>(wrow[b] + (int64_t)k0 * 2) : bf16x8{};
+              dd[b][pb] = mfma_bf16(ah, wv, dd[b][pb]);
+              dd[b][pb] = mfma_bf16(al, wv, dd[b][pb]);
+            }
+          }
+        }
+      }
+    }
+
+    // ---- forward DFT: B operand k-block kb = pixel blocks 2 kb (slots 0-3), 2 kb + 1 (4-7); each
+    // operator fragment read from LDS once for the CB blocks
+    bf16x8 xh[CB][2], xl[CB][2];
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x8 xv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xv.v[j] = dd[b][2 * kb][j];
+          xv.v[4 + j] = dd[b][2 * kb + 1][j];
+        }
+        split_bf16(xv, xh[b][kb], xl[b][kb]);
+      }
+    f32x4 d1[CB][5];
+#pragma unroll
+    for (int rb = 0; rb < 5; ++rb) {
+#pragma unroll
+      for (int b = 0; b < CB; ++b) d1[b][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int off = (rb * 16 + lc) * FROWB + (kb * 32 + lg * 8) * 2;
+        const bf16x8 fh = lds8(fw + off), fl = lds8(fw + FBYTES + off);
+#pragma unroll
+        for (int b = 0; b < CB; ++b) {
+          d1[b][rb] = mfma_bf16(fh, xh[b][kb], d1[b][rb]);
+          d1[b][rb] = mfma_bf16(fh, xl[b][kb], d1[b][rb]);
+          d1[b][rb] = mfma_bf16(fl, xh[b][kb], d1[b][rb]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < CB; ++b) {
+        const f32x4 g = cval[b] ? *reinterpret_cast<const f32x4*>(p.gain + chl[b] * NCOEF + rb * 16 + lg * 4)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d1[b][rb][j] *= g[j];
+      }
+    }
+    bf16x8 dh[CB][3], dl[CB][3];
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 3; ++kb2) {
+        f32x8 dv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dv.v[j] = d1[b][2 * kb2][j];
+          dv.v[4 + j] = (2 * kb2 + 1 < 5) ? d1[b][2 * kb2 + 1 < 5 ? 2 * kb2 + 1 : 0][j] : 0.f;
+        }
+        split_bf16(dv, dh[b][kb2], dl[b][kb2]);
+      }
+    // ---- inverse, residual, store
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) {
+      f32x4 y[CB];
+#pragma unroll
+      for (int b = 0; b < CB; ++b) y[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb2 = 0; kb2 < 3; ++kb2) {
+        const int off = (ob * 16 + lc) * IROWB + (kb2 * 32 + lg * 8) * 2;
+        const bf16x8 ih = lds8(iv + off), il = lds8(iv + IBYTES + off);
+#pragma unroll
+        for (int b = 0; b < CB; ++b) {
+          y[b] = mfma_bf16(ih, dh[b][kb2], y[b]);
+          y[b] = mfma_bf16(ih, dl[b][kb2], y[b]);
+          y[b] = mfma_bf16(il, dh[b][kb2], y[b]);
+        }
+      }
+      const int pi0 = ob * 16 + lg * 4;  // pixels pi0 .. pi0 + 3: one patch row, 4 columns
+      const int yy = py * 8 + (pi0 >> 3);
+      if (yy >= H) continue;
+#pragma unroll
+      for (int b = 0; b < CB; ++b) {
+        if (!cval[b]) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int xx = px * 8 + (pi0 & 7) + j;
+          if (xx >= W) continue;
+          const int64_t o = ((n * H + yy) * W + xx) * p.n + chl[b];
+          float v = y[b][j];
+          if (p.res) v += load1(p.res, p.r_dt, o);
+          store1(p.out, p.o_dt, o, v);
+        }
+      }
+    }
+  }
+}
+
 static int launch_patch(FreqP& p, hipStream_t s, const char* what) {
   p.small_offsets = (7 * p.sh + 7 * p.sw + 2 * p.c) < ((int64_t)1 << 31) && p.sh < ((int64_t)1 << 31) &&
                     p.sw < ((int64_t)1 << 31);
@@ -230,12 +511,14 @@ static int launch_patch(FreqP& p, hipStream_t s, const char* what) {
   // persistent: ~3 resident workgroups per CU (the LDS operator copies), so each stages the
   // matrices once for many units
   int64_t blocks = cdiv(p.units, 4);
-  if (blocks > 768) blocks = 768;
+  if (blocks > 3LL * device_cus()) blocks = 3LL * device_cus();
   const dim3 g((unsigned)blocks);
   if (p.corr) {
+    note_kernel("patch_kernel corr=1");
     if (p.x_dt == DT_BF16) hipLaunchKernelGGL((patch_kernel<DT_BF16, true>), g, dim3(256), 0, s, p);
     else hipLaunchKernelGGL((patch_kernel<DT_F32, true>), g, dim3(256), 0, s, p);
   } else {
+    note_kernel("patch_kernel corr=0");
     if (p.x_dt == DT_BF16) hipLaunchKernelGGL((patch_kernel<DT_BF16, false>), g, dim3(256), 0, s, p);
     else hipLaunchKernelGGL((patch_kernel<DT_F32, false>), g, dim3(256), 0, s, p);
   }
@@ -282,4 +565,79 @@ extern "C" int clarus_hip_patch_corr(const void* x, int32_t x_dtype, int64_t sn,
   p.batch = batch; p.h = h; p.w = w; p.c = c;
   p.x_dt = x_dtype; p.r_dt = DT_F32; p.o_dt = DT_F32; p.corr = 1;
   return launch_patch(p, (hipStream_t)stream, "patch_corr");
+}
+
+extern "C" int clarus_hip_linear_patch_filter(const void* x, int32_t x_dtype, const void* wt, int32_t w_dtype,
+                                              const float* bias, int32_t ln, float ln_eps, const float* fwd,
+                                              const float* inv, const float* gain, const void* res, int32_t r_dtype,
+                                              void* out, int32_t o_dtype, int64_t batch, int64_t h, int64_t w,
+                                              int64_t k, int64_t n, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(x && wt && fwd && inv && gain && out, "linear_patch_filter: null operand");
+  CLARUS_REQUIRE(batch > 0 && h > 0 && w > 0 && k > 0 && n > 0, "linear_patch_filter: bad sizes");
+  CLARUS_REQUIRE((x_dtype == DT_F32 || x_dtype == DT_BF16) && (w_dtype == DT_F32 || w_dtype == DT_BF16) &&
+                     (o_dtype == DT_F32 || o_dtype == DT_BF16), "linear_patch_filter: bad dtype");
+  CLARUS_REQUIRE(ln >= 0 && ln <= 2, "linear_patch_filter: ln is 0 (none), 1 (LayerNorm) or 2 (RMS)");
+  CLARUS_REQUIRE(k % 8 == 0 && (ln == 0 || k <= 256), "linear_patch_filter: K=%lld must be a multiple of 8 (and <= 256 "
+                 "with a LayerNorm / RMS prologue)", (long long)k);
+  CLARUS_REQUIRE(h >= 9 && w >= 9, "linear_patch_filter: reflect padding to a multiple of 8 needs h, w >= 9");
+  CLARUS_REQUIRE(aligned(x, 16) && aligned(wt, 16) && aligned(gain, 16) && aligned(fwd, 16) && aligned(inv, 16),
+                 "linear_patch_filter: 16-byte alignment");
+  CLARUS_REQUIRE(batch * h * w * (k > n ? k : n) < ((int64_t)1 << 62), "linear_patch_filter: too large");
+  if (res) CLARUS_REQUIRE(r_dtype == DT_F32 || r_dtype == DT_BF16, "linear_patch_filter: bad residual dtype");
+  LpfP p{};
+  p.x = x; p.wt = wt; p.bias = bias; p.fwd = fwd; p.inv = inv; p.gain = gain; p.res = res; p.out = out;
+  p.batch = batch; p.h = h; p.w = w; p.k = k; p.n = n;
+  p.eps = ln_eps; p.r_dt = r_dtype; p.o_dt = o_dtype;
+  // channel tile: CB 16-channel blocks of one patch per wave (operator fragments and A rows
+  // reused CB times): 3 when they divide N (FFTformer's N = 6c), else 2. With a LayerNorm / RMS
+  // prologue the row is held in KS 32-k steps, the fewest that cover K.
+  const int cb = n % 48 == 0 ? 3 : 2;
+  const int steps = (int)cdiv(k, 32);
+  const int ks = steps <= 2 ? 2 : steps <= 3 ? 3 : steps <= 4 ? 4 : steps <= 6 ? 6 : 8;
+  p.units = batch * cdiv(h, 8) * cdiv(w, 8) * cdiv(n, 16 * cb);
+  int64_t blocks = cdiv(p.units, 4);
+  if (blocks > 3LL * device_cus()) blocks = 3LL * device_cus();
+  const dim3 g((unsigned)blocks);
+  hipStream_t s = (hipStream_t)stream;
+  // instantiated: LayerNorm / RMS prologues for bf16 activations with bf16 weights and fp32 with
+  // fp32 (the two backends); no prologue for every dtype pair (the rows pass feeds bf16 rows to
+  // fp32 weights)
+  const bool same = (x_dtype == DT_BF16) == (w_dtype == DT_BF16);
+  CLARUS_REQUIRE(ln == 0 || same, "linear_patch_filter: a LayerNorm / RMS prologue needs activations and weights "
+                 "of one dtype");
+  note_kernel("lpf_kernel ln=%d ws=%d cb=%d ks=%d", ln, w_dtype == DT_F32, cb, ln ? ks : 0);
+#define CLARUS_LPF_CB(XDT, LNV, WSV, KSV)                                                               \
+  do {                                                                                                  \
+    if (cb == 3) hipLaunchKernelGGL((lpf_kernel<XDT, LNV, WSV, 3, KSV>), g, dim3(256), 0, s, p);        \
+    else hipLaunchKernelGGL((lpf_kernel<XDT, LNV, WSV, 2, KSV>), g, dim3(256), 0, s, p);                \
+  } while (0)
+#define CLARUS_LPF_KS(XDT, LNV, WSV)                   \
+  do {                                                 \
+    switch (ks) {                                      \
+      case 2: CLARUS_LPF_CB(XDT, LNV, WSV, 2); break;  \
+      case 3: CLARUS_LPF_CB(XDT, LNV, WSV, 3); break;  \
+      case 4: CLARUS_LPF_CB(XDT, LNV, WSV, 4); break;  \
+      case 6: CLARUS_LPF_CB(XDT, LNV, WSV, 6); break;  \
+      default: CLARUS_LPF_CB(XDT, LNV, WSV, 8); break; \
+    }                                                  \
+  } while (0)
+  if (ln == 0) {
+    if (x_dtype == DT_BF16) {
+      if (w_dtype == DT_F32) CLARUS_LPF_CB(DT_BF16, 0, true, 1);
+      else CLARUS_LPF_CB(DT_BF16, 0, false, 1);
+    } else {
+      if (w_dtype == DT_F32) CLARUS_LPF_CB(DT_F32, 0, true, 1);
+      else CLARUS_LPF_CB(DT_F32, 0, false, 1);
+    }
+  } else if (x_dtype == DT_BF16) {
+    if (ln == 1) CLARUS_LPF_KS(DT_BF16, 1, false);
+    else CLARUS_LPF_KS(DT_BF16, 2, false);
+  } else {
+    if (ln == 1) CLARUS_LPF_KS(DT_F32, 1, true);
+    else CLARUS_LPF_KS(DT_F32, 2, true);
+  }
+#undef CLARUS_LPF_KS
+#undef CLARUS_LPF_CB
+  return check_launch("linear_patch_filter");
 }

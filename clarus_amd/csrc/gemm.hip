@@ -48,11 +48,11 @@ static int auto_tile(int64_t m, int64_t n, int64_t k, int64_t batch, bool gate, 
 }
 
 // persistent grid: when W^T fits in one LDS chunk a workgroup keeps it and walks several
-// pixel tiles; aim for ~1024 resident workgroups (256 CUs x 4)
+// pixel tiles; aim for ~4 resident workgroups per CU
 static dim3 grid_for(int64_t ptiles, int64_t ntiles, int64_t batch, int64_t k, int kc) {
   int64_t gx = ptiles;
   if (k <= kc) {
-    const int64_t target = 1024;
+    const int64_t target = 4LL * device_cus();
     int64_t per = ntiles * batch;
     int64_t want = (target + per - 1) / per;
     if (want < 1) want = 1;
@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(256) row_stats_kernel(const void* a, int64_t l
 
 static void launch_row_stats(const void* a, int a_dt, int64_t lda, int64_t m, int64_t k, bool rms, float eps,
                              float* stats, hipStream_t s) {
-  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(m, 4), 2048);
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(m, 4), 8LL * device_cus());
   if (a_dt == DT_BF16)
     hipLaunchKernelGGL(row_stats_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, a, lda, m, k, (int)rms, eps, stats);
   else
@@ -613,7 +613,7 @@ extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const floa
   const int64_t m = batch * h * w;
   if (cout % 64 == 0 && batch * h * w * 3 < ((int64_t)1 << 31)) {
     const int64_t units = cdiv(m, 16) * (cout / 64);
-    const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(units, 4), 2048);
+    const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(units, 4), 8LL * device_cus());
     if (out_dtype == DT_BF16)
       hipLaunchKernelGGL(intro_mfma_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, inp, wt, bias,
                          out, (int)m, (int)h, (int)w, (int)cout);
@@ -624,7 +624,7 @@ extern "C" int clarus_hip_intro3x3(const float* inp, const float* wt, const floa
   }
   const int64_t work = m * (cout / 8);
   const size_t lds = (size_t)28 * cout * sizeof(float);
-  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(work, 256), 2048);
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(work, 256), 8LL * device_cus());
   if (out_dtype == DT_BF16)
     hipLaunchKernelGGL(intro_kernel<DT_BF16>, dim3(blocks), dim3(256), lds, (hipStream_t)stream, inp, wt, bias, out,
                        (int)m, (int)h, (int)w, (int)cout);

@@ -28,7 +28,7 @@ void launch_one(GemmP& p, hipStream_t s) {
   p.ptiles = cdiv(p.m, LT_P);
   const int64_t tiles = p.ptiles * cdiv(p.n, LT_R / (GATE ? 2 : 1));
   // persistent: every workgroup resident, a multiple of 8 so each XCD gets the same number
-  int64_t gx = 256LL * per_cu;
+  int64_t gx = (int64_t)device_cus() * per_cu;
   const int64_t need = cdiv(tiles, 8) * 8;
   if (gx > need) gx = need;
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), lds, s, p);
@@ -49,7 +49,7 @@ void launch_dma(GemmP& p, hipStream_t s) {
   }();
   p.ptiles = cdiv(p.m, DMA_P);
   const int64_t tiles = p.ptiles * cdiv(p.n, DMA_R / (GATE ? 2 : 1));
-  int64_t gx = 256LL * per_cu;
+  int64_t gx = (int64_t)device_cus() * per_cu;
   const int64_t need = cdiv(tiles, 8) * 8;
   if (gx > need) gx = need;
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), lds, s, p);
@@ -70,7 +70,7 @@ void launch_m32(GemmP& p, hipStream_t s) {
   }();
   p.ptiles = cdiv(p.m, M32_P);
   const int64_t tiles = p.ptiles * cdiv(p.n, M32_R / (GATE ? 2 : 1));
-  int64_t gx = 256LL * per_cu;
+  int64_t gx = (int64_t)device_cus() * per_cu;
   const int64_t need = cdiv(tiles, 8) * 8;
   if (gx > need) gx = need;
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(256), M32_LDS, s, p);
@@ -92,7 +92,7 @@ void launch_big(GemmP& p, hipStream_t s) {
   }();
   p.ptiles = cdiv(p.m, C::P);
   const int64_t tiles = p.ptiles * cdiv(p.n, BIG_R / (GATE ? 2 : 1));
-  int64_t gx = 256LL * per_cu;
+  int64_t gx = (int64_t)device_cus() * per_cu;
   const int64_t need = cdiv(tiles, 8) * 8;
   if (gx > need) gx = need;
   hipLaunchKernelGGL(fn, dim3((unsigned)gx), dim3(C::NT), C::LDS, s, p);

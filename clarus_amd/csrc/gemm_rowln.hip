@@ -540,7 +540,7 @@ int rowln_launch(const GemmP& p, const RowLnP& q, const Ln2P& r2, void* stream, 
   // one tile per workgroup at most (the fused second GEMM reuses the ring, so a workgroup
   // cannot prefetch a next tile); without the fusion, persistent up to the resident count
   const int64_t need = cdiv(p.ptiles, 8) * 8;
-  int64_t gx = FUSE ? need : std::min<int64_t>(256LL * per_cu, need);
+  int64_t gx = FUSE ? need : std::min<int64_t>((int64_t)device_cus() * per_cu, need);
   note_kernel("gemm_rowln_kernel fuse=%d", (int)FUSE);
   hipLaunchKernelGGL(gemm_rowln_kernel<FUSE>, dim3((unsigned)gx), dim3(RL_THREADS), RL_LDS, (hipStream_t)stream, p,
                      q, r2);

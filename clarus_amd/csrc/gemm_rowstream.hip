@@ -26,7 +26,7 @@ void launch_one(const GemmP& p, unsigned ny, unsigned nz, hipStream_t s) {
   // every workgroup resident: 256 CUs x per_cu, split over the channel tiles and batch; a
   // multiple of 8 keeps the channel tiles of a pixel range on one XCD
   const int64_t blocks = cdiv(p.m, RS_BP);
-  int64_t gx = (256LL * per_cu) / ((int64_t)ny * nz);
+  int64_t gx = ((int64_t)device_cus() * per_cu) / ((int64_t)ny * nz);
   if (gx < 1) gx = 1;
   const int64_t need = cdiv(blocks, nw);
   if (gx > need) gx = need;

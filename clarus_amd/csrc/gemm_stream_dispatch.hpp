@@ -1,6 +1,7 @@
 // Instantiation table of gemm_stream_kernel (W-resident streaming GEMM).
 #pragma once
 
+#include "capi.hpp"
 #include "gemm_dispatch.hpp"
 #include "gemm_stream.hpp"
 
@@ -25,7 +26,7 @@ void launch_stream_one(const GemmP& p, dim3 grid_max, hipStream_t s, int) {
   }();
   // every workgroup resident: 256 CUs x per_cu, split over the channel tiles and batch
   const int64_t blocks16 = cdiv(p.m, 16);
-  int64_t gx = (256LL * per_cu) / ((int64_t)grid_max.y * grid_max.z);
+  int64_t gx = ((int64_t)device_cus() * per_cu) / ((int64_t)grid_max.y * grid_max.z);
   if (gx < 1) gx = 1;
   const int64_t need = cdiv(blocks16, 4);  // one 16-pixel block per wave at least
   if (gx > need) gx = need;

@@ -129,6 +129,7 @@ template <int TA, int G, int FR, bool SPLIT>
 static void launch_split(const SplitP& p, hipStream_t s) {
   constexpr int rows_per_block = 4 * (64 / G);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(p.m, rows_per_block), 4096);
+  note_kernel("rows_split_kernel g=%d split=%d", G, (int)SPLIT);
   hipLaunchKernelGGL((rows_split_kernel<TA, G, FR, SPLIT>), dim3(blocks), dim3(256), 0, s, p);
 }
 

@@ -474,7 +474,7 @@ extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float*
         k = 1;                                                                                                  \
       return k;                                                                                                 \
     }();                                                                                                        \
-    const int64_t cap = std::max<int64_t>(1, 256LL * per_cu / nslices);                                        \
+    const int64_t cap = std::max<int64_t>(1, (int64_t)device_cus() * per_cu / nslices);                                        \
     const unsigned blocks = (unsigned)(nslices * std::min<int64_t>(chunks, cap));                               \
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);                                                   \
   } while (0)
@@ -497,7 +497,7 @@ extern "C" int clarus_hip_dwconv3x3(const void* x, int32_t x_dtype, const float*
         k = 1;                                                                                                  \
       return k;                                                                                                 \
     }();                                                                                                        \
-    const int64_t cap = std::max<int64_t>(1, 256LL * per_cu / nslices);                                        \
+    const int64_t cap = std::max<int64_t>(1, (int64_t)device_cus() * per_cu / nslices);                                        \
     const unsigned blocks = (unsigned)(nslices * std::min<int64_t>(rchunks, cap));                              \
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);                                                   \
   } while (0)

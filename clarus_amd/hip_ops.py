@@ -77,6 +77,9 @@ class HipOps(Backend):
     # output written by its epilogue (clarus_hip_gemm_ln_rows) and then the second GEMM on those
     # rows when only the first fits; False runs the two linear ops.
     fuse_ln_rows = True
+    # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
+    # linear (fp32 output) and patch_filter as two ops.
+    fuse_patch_filter = True
     # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
     # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
     round_short_prologue = False
@@ -209,17 +212,18 @@ class HipOps(Backend):
         reference's ln_rows / mul_small, ops/triton_cuda.py:104-110), then a plain bf16 GEMM."""
         return pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.split_min_k <= k <= 2048 and k % 32 == 0
 
-    def _prologue_rows(self, x, pro, sm, geom, ln_eps, m, k):
+    def _prologue_rows(self, x, pro, sm, geom, ln_eps, m, k, split=None):
         """The prologue applied to every row, rounded once to bf16 ([m, K]), or as [hi | lo] bf16
-        ([m, 2K]) with prologue_split."""
-        kk = 2 * k if self.prologue_split else k
+        ([m, 2K]) with prologue_split (or split=True)."""
+        split = self.prologue_split if split is None else split
+        kk = 2 * k if split else k
         rows = torch.empty((m, kk), device=x.device, dtype=torch.bfloat16)
         hh, ww, oh, ow, pt, pl = geom
         args = _lib.GemmArgs(a=x.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(x.dtype),
                              pro=pro, ln_eps=float(ln_eps), small=_lib.ptr(sm),
                              s_dtype=_lib.dtype_code(sm.dtype) if sm is not None else 0,
                              h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
-        fn = self.lib.clarus_hip_rows_split if self.prologue_split else self.lib.clarus_hip_rows_prologue
+        fn = self.lib.clarus_hip_rows_split if split else self.lib.clarus_hip_rows_prologue
         _lib.check(fn(ctypes.byref(args), rows.data_ptr(), self._stream(x)), "linear")
         return rows
 
@@ -498,25 +502,26 @@ class HipOps(Backend):
                           bias=self._bias(bias), res=residual, ldr=nout, batch=n, a_bs=x.stride(0),
                           w_bs=nout * k, c_bs=h * wd * nout, r_bs=h * wd * nout)
 
-    def attention_apply(self, qkv, attn_t, residual=None, out_dtype=None):
-        """attn . V of Restormer's MDTA per head: out[p, hd*ch + j] = sum_i v[p, hd*ch + i]
-        * attn_t[n, hd, i, j], with v = qkv[..., 2C:] and attn_t = A^T per head [N, heads, ch, ch].
-        Equals linear_per_image(v, blockdiag(attn_t)) (the block-diagonal mix the Restormer block
-        builds, python/clarus/models/restormer/__init__.py:203-210) without the zero blocks:
-        one batched GEMM launch per image with the heads as the batch."""
+    def attention_apply(self, qkv, attn, residual=None, out_dtype=None):
+        """attn . V of Restormer's MDTA per head: out[p, hd*ch + j] = sum_i A[n, hd, j, i]
+        * v[p, hd*ch + i], with v = qkv[..., 2C:] and A the map channel_attention returns
+        [N, heads, ch, ch]. Equals linear_per_image(v, blockdiag(A^T)) (the block-diagonal mix the
+        Restormer block builds, python/clarus/models/restormer/__init__.py:203-210) without the
+        zero blocks: one batched GEMM launch per image with the heads as the batch, A read as
+        the GEMM's transposed weight as it is (no copy when it is contiguous)."""
         n, h, wd, c3 = qkv.shape
         c = c3 // 3
-        if attn_t.dim() == 3:
-            attn_t = attn_t.unsqueeze(0)
-        heads, ch = attn_t.shape[1], attn_t.shape[2]
-        if (not qkv.is_contiguous() or c3 % 3 or heads * ch != c or tuple(attn_t.shape) != (n, heads, ch, ch)
+        if attn.dim() == 3:
+            attn = attn.unsqueeze(0)
+        heads, ch = attn.shape[1], attn.shape[2]
+        if (not qkv.is_contiguous() or c3 % 3 or heads * ch != c or tuple(attn.shape) != (n, heads, ch, ch)
                 or not _same(residual, (n, h, wd, c))):
             raise Unsupported("attention_apply: contiguous qkv, attn [N, heads, ch, ch], residual of the output's shape")
         odt = out_dtype or self.dtype
-        if not (_kdt(qkv, attn_t, residual) and odt in _KDT and ch % 8 == 0 and _vec16(qkv, c3, ch)):
+        if not (_kdt(qkv, attn, residual) and odt in _KDT and ch % 8 == 0 and _vec16(qkv, c3, ch)):
             raise Unsupported("attention_apply: bf16 / fp32, head width % 8 == 0")
         out = torch.empty((n, h, wd, c), device=qkv.device, dtype=odt)
-        wt = attn_t.transpose(2, 3).contiguous()  # W^T per head: [n, heads, j, i]
+        wt = attn.contiguous()  # W^T per head [n, heads, j, i] is A itself
         for i in range(n):
             self._gemm("attention_apply", a=qkv[i, ..., 2 * c:], wt=wt[i], c=out[i], m=h * wd, n=ch, k=ch, lda=c3,
                        ldc=c, res=residual[i] if residual is not None else None, ldr=c, batch=heads, a_bs=ch,
@@ -544,13 +549,48 @@ class HipOps(Backend):
         return out
 
     def linear_patch_filter(self, x, w, bias, f, ln=False, ln_eps=1e-6, residual=None):
+        """patch_filter(linear(x, w, bias, ln) kept fp32, f, residual) in one kernel
+        (clarus_hip_linear_patch_filter): the GEMM output goes from the MFMA accumulators
+        straight into the patch DFT, never to memory. Prologue arithmetic as linear's: LayerNorm /
+        RMS inside the kernel in fp32 for K < split_min_k (or fp32 weights, K <= 256), else the
+        rows pass rounded once to bf16 first (the reference's ln_rows for K > 128,
+        ops/triton_cuda.py:267-270). fuse_patch_filter = False runs the two ops instead."""
         n, h, wd, k = x.shape
-        if (tuple(f.shape[1:]) != (8, 5) or f.shape[0] != w.shape[1] or min(h, wd) < 9 or bias is None
-                or x.dtype != self.dtype or not _dense(x, w, bias) or not _same(residual, (n, h, wd, w.shape[1]))):
+        nout = w.shape[1] if w.dim() == 2 else -1
+        if (tuple(f.shape[1:]) != (8, 5) or f.shape[0] != nout or min(h, wd) < 9 or bias is None
+                or x.dtype != self.dtype or not _dense(x, w, bias) or not _same(residual, (n, h, wd, nout))):
             raise Unsupported("linear_patch_filter: 8x8 patches, H, W >= 9, contiguous, bias, x in the compute "
                               "dtype, residual of the output's shape")
-        y = self.linear(x, w, bias, ln=ln, ln_eps=ln_eps, out_dtype=torch.float32)
-        return self.patch_filter(y, f, residual=residual)
+        if ln not in (False, True, "rms"):
+            raise Unsupported(f"linear_patch_filter: ln={ln!r}")
+        if not self.fuse_patch_filter:
+            y = self.linear(x, w, bias, ln=ln, ln_eps=ln_eps, out_dtype=torch.float32)
+            return self.patch_filter(y, f, residual=residual)
+        if not (_kdt(x, w, residual) and w.shape[0] == k and k % 8 == 0 and _vec16(x)):
+            raise Unsupported("linear_patch_filter: bf16 / fp32 operands, K % 8 == 0, 16-byte aligned rows")
+        code = {False: 0, True: 1, "rms": 2}[ln]
+        a, kk, wt = x, k, self._wt(w)
+        pro = _lib.PRO_RMS if ln == "rms" else _lib.PRO_LN
+        if code and (self._prologue_pass(w, pro, k) or k > 256):
+            # bf16 weights: rows rounded once (or [hi | lo] with prologue_split), as linear; fp32
+            # weights with K > 256 (past the kernel's in-register rows): [hi | lo] rows, fp32-accurate
+            split = self.prologue_split or w.dtype != torch.bfloat16
+            if not (k <= 2048 and k % 32 == 0):
+                raise Unsupported("linear_patch_filter: LayerNorm rows over K > 256 need K % 32 == 0, K <= 2048")
+            a = self._prologue_rows(x, pro, None, (0, 0, 0, 0, 0, 0), ln_eps, n * h * wd, k, split=split)
+            kk = a.shape[1]
+            wt = self._wt2(w) if split else wt
+            code = 0
+        fwd, inv = self._mats(x.device)
+        gain = self.cached(f, "gain", lambda t: t.float().reshape(t.shape[0], -1).repeat_interleave(2, dim=1)
+                           .contiguous())
+        out = torch.empty((n, h, wd, nout), device=x.device, dtype=self.dtype)
+        _lib.check(self.lib.clarus_hip_linear_patch_filter(
+            a.data_ptr(), _lib.dtype_code(a.dtype), wt.data_ptr(), _lib.dtype_code(wt.dtype), self._bias(bias).data_ptr(),
+            code, float(ln_eps), fwd.data_ptr(), inv.data_ptr(), gain.data_ptr(), _lib.ptr(residual),
+            _lib.dtype_code(residual.dtype) if residual is not None else 0, out.data_ptr(), _lib.dtype_code(self.dtype),
+            n, h, wd, kk, nout, self._stream(x)), "linear_patch_filter")
+        return out
 
     def patch_corr(self, x, c, p=8):
         n, h, w, cx = x.shape

@@ -166,10 +166,10 @@ def config4_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
                                 {"qkv": qkvh, "t": th},
                                 lambda r, q=qkvh, t=th, heads=heads: r.channel_attention(q, heads, t)))
             a = hip.channel_attention(qkv, heads, t)
-            wa = a[0].transpose(1, 2).contiguous().to(dt)  # per head A^T [heads, 48, 48]
+            wa = a.to(dt)  # the maps A [1, heads, 48, 48] in the activation dtype
             # the reference applies the maps as one per-image matrix blockdiag(A^T) through
             # linear_per_image (python/clarus/models/restormer/__init__.py:203-210)
-            bd = torch.block_diag(*wa.float().cpu()).unsqueeze(0)
+            bd = torch.block_diag(*wa[0].transpose(1, 2).float().cpu()).unsqueeze(0)
             cases.append(OpCase(f"mdta attn.V l{lvl} {tag}", 4, tag, heads * 2.0 * 48 * 48 * hw, 2.0 * c * hw * e,
                                 lambda hip=hip, qkv=qkv, wa=wa: hip.attention_apply(qkv, wa),
                                 {"qkv": qkvh, "blockdiag": bd},
@@ -252,9 +252,34 @@ def nafnet_pair_case(hip, device, seed: int = 0) -> OpCase:
                   lambda r_: pair(r_, host))
 
 
+def fftformer_dffn_case(hip, device, seed: int = 0) -> OpCase:
+    """FFTformer level-0 DFFN project_in + frequency filter at 720p as one op (linear_patch_filter:
+    LayerNorm eps 1e-5 -> 1x1 conv 48 -> 288 + bias -> per-patch rfft2 * filter -> irfft2, bf16),
+    python/clarus/models/fftformer/__init__.py:160-161. F = 2 M K N (GEMM) + (M / 64) N 20720
+    (the dense DFT-GEMM flops of config 3 per patch-channel); B = 2 M K (in) + 2 M N (out) +
+    2 K N (weights) + 4 N (bias) + 4 * 80 N (filter gains)."""
+    g = _gen(seed + 11)
+    h, w, k, n = 720, 1280, 48, 288
+    m = h * w
+    x = torch.randn(1, h, w, k, generator=g).bfloat16()
+    wk = _kaiming_uniform_kn(g, k, n).bfloat16()
+    b = torch.rand(n, generator=g) * 0.2 - 0.1
+    f = torch.randn(n, 8, 5, generator=g)
+    host = dict(x=x, w=wk, b=b, f=f)
+    d = {nm: t.to(device) for nm, t in host.items()}
+
+    def run(r=None, d=d):
+        return (r or hip).linear_patch_filter(d["x"], d["w"], d["b"], d["f"], ln=True, ln_eps=1e-5)
+    flops = 2.0 * m * k * n + (m / 64.0) * n * 20720.0
+    nbytes = 2.0 * m * k + 2.0 * m * n + 2.0 * k * n + 4.0 * n + 4.0 * 80 * n
+    return OpCase("fftformer L0 DFFN LN -> 48->288 -> patch filter (fused)", 3, "bf16", flops, nbytes, run, host,
+                  lambda r: run(r, host))
+
+
 def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
-    """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5
-    and the fused NAFNet pair."""
+    """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5,
+    the fused FFTformer DFFN op and the fused NAFNet pair."""
     return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
             + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
-            + config5_cases(hip_bf16, device, seed) + [nafnet_pair_case(hip_bf16, device, seed)])
+            + config5_cases(hip_bf16, device, seed) + [fftformer_dffn_case(hip_bf16, device, seed),
+                                                        nafnet_pair_case(hip_bf16, device, seed)])

@@ -254,6 +254,27 @@ int clarus_hip_patch_filter(const void* x, int32_t x_dtype, int64_t ldx, const f
                             int64_t h, int64_t w, int64_t c, void* stream);
 
 /*
+ * patch_filter(prologue(x) . W + bias) (+ residual) in one kernel: per 8x8 patch and output
+ * channel, y = Inv . (g_c * (Fwd . z)) with z the patch's 64 values of the GEMM output, which
+ * never leaves the registers. x [batch, h, w, k] contiguous (x_dtype); wt = W^T [n][k] (w_dtype,
+ * bf16 or fp32); bias fp32 [n] or NULL; ln 0 = none, 1 = LayerNorm, 2 = RMS norm over the k
+ * channels of each pixel (eps ln_eps, no affine; k <= 256; x and wt of one dtype), applied in
+ * fp32; fwd / inv / gain as
+ * clarus_hip_patch_filter with gain [n][80]. Sizes that are not multiples of 8 are reflect-padded
+ * (h, w >= 9), which for a per-pixel GEMM is the GEMM of the reflected pixels. out [batch, h, w, n]
+ * contiguous (o_dtype); residual contiguous like out or NULL. k % 8 == 0. With bf16 weights the
+ * GEMM's A values enter bf16 MFMAs as hi + lo pairs where they are not bf16 already (2^-16
+ * relative per operand); with fp32 weights it runs on fp32 MFMAs. The DFT products are those of
+ * clarus_hip_patch_filter.
+ * replaces kernels/freq.py:189-273 ln_gemm_patch_filter (ops/triton_cuda.py:260-272)
+ */
+int clarus_hip_linear_patch_filter(const void* x, int32_t x_dtype, const void* wt, int32_t w_dtype,
+                                   const float* bias, int32_t ln, float ln_eps, const float* fwd,
+                                   const float* inv, const float* gain, const void* res, int32_t r_dtype,
+                                   void* out, int32_t o_dtype, int64_t batch, int64_t h, int64_t w,
+                                   int64_t k, int64_t n, void* stream);
+
+/*
  * FFTformer FSAS correlation (ops/torch_ref.py:278-288): per 8x8 patch,
  * irfft2(rfft2(q) * rfft2(k)) with q = x[..., :c], k = x[..., c:2c]; x has unit channel
  * stride and arbitrary batch / row / pixel strides (elements); out fp32 [batch, h, w, c].

@@ -106,20 +106,20 @@ def _blockdiag_t(a):
 def test_config4_attention_apply(lvl, h, w, dt, hip_bf16, hip_f32):
     """HipOps.attention_apply (the config-4 attn . V the benchmark times: one batched GEMM launch
     per image, the heads as the batch, v read from qkv with pixel stride 3C) against the oracle's
-    linear_per_image(v, blockdiag(A^T)), at every config-4 level. As in the benchmark, the maps
-    are passed as A^T per head in the activation dtype; fp32 output, then the backend's own."""
+    linear_per_image(v, blockdiag(A^T)), at every config-4 level. As in the benchmark, the maps A
+    are passed in the activation dtype; fp32 output, then the backend's own."""
     hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
     g = gen(60 + lvl)
     c, heads = 48 * 2 ** lvl, 2 ** lvl
     qkv = rnd(g, 1, h, w, 3 * c, dtype=dt)
     logits = rnd(g, 1, heads, 48, 48, scale=2.0)
     a = torch.softmax(logits, -1)  # a row-stochastic map like channel_attention's
-    at = a.transpose(-1, -2).contiguous().to(dt)  # A^T per head
+    am = a.to(dt)  # the maps in the activation dtype
     print(f"[attn.V] l{lvl} {dt}", flush=True)
-    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag(at), out_dtype=torch.float32)
-    got = hip.attention_apply(qkv.cuda(), at.cuda(), out_dtype=torch.float32)
+    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag_t(am), out_dtype=torch.float32)
+    got = hip.attention_apply(qkv.cuda(), am.cuda(), out_dtype=torch.float32)
     assert_fp32(got.cpu(), ref, rel=1e-5, what=f"attention_apply l{lvl} {dt}")
-    got = hip.attention_apply(qkv.cuda(), at.cuda())
+    got = hip.attention_apply(qkv.cuda(), am.cuda())
     assert got.dtype == dt
     if dt == torch.bfloat16:
         assert_bf16(got.cpu(), ref, what=f"attention_apply l{lvl} bf16 out")
@@ -136,14 +136,18 @@ def test_attention_apply_batch_and_residual(dt, hip_bf16, hip_f32):
     n, h, w, heads, ch = 2, 13, 29, 4, 24
     c = heads * ch
     qkv = rnd(g, n, h, w, 3 * c, dtype=dt)
-    at = torch.softmax(rnd(g, n, heads, ch, ch, scale=2.0), -1).transpose(-1, -2).contiguous()
+    a = torch.softmax(rnd(g, n, heads, ch, ch, scale=2.0), -1)
     res = rnd(g, n, h, w, c, dtype=dt)
-    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag(at), residual=res, out_dtype=torch.float32)
-    got = hip.attention_apply(qkv.cuda(), at.cuda(), residual=res.cuda(), out_dtype=torch.float32)
+    ref = REF.linear_per_image(qkv[..., 2 * c:], _blockdiag_t(a), residual=res, out_dtype=torch.float32)
+    got = hip.attention_apply(qkv.cuda(), a.cuda(), residual=res.cuda(), out_dtype=torch.float32)
     assert_fp32(got.cpu(), ref, rel=1e-5, what=f"attention_apply batch 2 + residual {dt}")
+    # a map with a transposed (non-contiguous) view gives the same result
+    got2 = hip.attention_apply(qkv.cuda(), a.transpose(-1, -2).contiguous().cuda().transpose(-1, -2),
+                               residual=res.cuda(), out_dtype=torch.float32)
+    assert torch.equal(got, got2)
     from clarus_amd.dispatch import Unsupported
     with pytest.raises(Unsupported):
-        hip.attention_apply(qkv.cuda(), at[0].cuda())
+        hip.attention_apply(qkv.cuda(), a[0].cuda())
 
 
 @pytest.mark.parametrize("lvl", [0, 2])
@@ -224,6 +228,54 @@ def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
     assert_bf16(got.cpu(), REF.linear_patch_filter(xr, wl, b, f, ln=False, residual=rr), what + " (rounded rows)")
     err = (got.cpu().double() - ref.double()).abs().max().item() / ref.abs().max().item()
     assert err < 2e-2, f"{what}: {err:.3e} of the output scale against the fp32 oracle"
+
+
+# FFTformer DFFN project_in + filter (python/clarus/models/fftformer/__init__.py:160-161): K = c,
+# N = 2 * hidden = 6c, LayerNorm eps 1e-5, at levels 0 / 1 / 3 (c = 48 / 96 / 384; K = 384 takes
+# the rounded rows pass), on 180 x 320 or smaller images; EVSSM EDFFN project_out + filter
+# (python/clarus/models/evssm/__init__.py:158): K = 144, N = 48, no LayerNorm, residual.
+LPF_SHAPES = [(180, 320, 48, 288, True, False), (90, 161, 96, 576, True, False), (45, 83, 384, 2304, True, False),
+              (180, 320, 144, 48, False, True), (93, 150, 144, 48, "rms", True)]
+
+
+@pytest.mark.parametrize("h,w,k,nout,ln,res", LPF_SHAPES)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_linear_patch_filter_fused_model_shapes(h, w, k, nout, ln, res, dt, hip_bf16, hip_f32):
+    """The one-kernel linear_patch_filter (clarus_hip_linear_patch_filter) at the FFTformer / EVSSM
+    call shapes against the oracle (fp32: 1e-5 relative; bf16: the bf16 rule, against the rows
+    rounded once to bf16 where the rows pass runs), and against the two-op path on the GPU (the
+    same arithmetic up to fp32 summation order)."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(50 + k)
+    x, f = rnd(g, 1, h, w, k).to(dt), rnd(g, nout, 8, 5)
+    wl, b = rnd(g, k, nout, scale=k ** -0.5).to(dt), rnd(g, nout, scale=0.1)
+    rr = rnd(g, 1, h, w, nout).to(dt) if res else None
+    dv = [None if t is None else t.cuda() for t in (x, wl, b, f, rr)]
+    print(f"[lpf] {dt} {h}x{w} k{k} n{nout} ln={ln} res={res}", flush=True)
+    got = hip.linear_patch_filter(*dv[:4], ln=ln, ln_eps=1e-5, residual=dv[4])
+    assert "lpf_kernel" in _lib.last_kernel(), _lib.last_kernel()
+    saved = HipOps.fuse_patch_filter
+    try:
+        HipOps.fuse_patch_filter = False
+        two = hip.linear_patch_filter(*dv[:4], ln=ln, ln_eps=1e-5, residual=dv[4])
+    finally:
+        HipOps.fuse_patch_filter = saved
+    what = f"fused linear_patch_filter {dt} {h}x{w} k{k} ln={ln}"
+    rounded = (bool(ln) and dt == torch.bfloat16 and not HipOps.prologue_split and HipOps.split_min_k <= k <= 2048
+               and k % 32 == 0)
+    xr = REF.ln(x.float(), 1e-5, rms=(ln == "rms")).to(torch.bfloat16) if rounded else x
+    ref = REF.linear_patch_filter(xr, wl, b, f, ln=False if rounded else ln, ln_eps=1e-5, residual=rr)
+    if dt == torch.float32:
+        assert_fp32(got.cpu(), ref, rel=1e-5, what=what)
+        assert_fp32(got.cpu(), two.cpu(), rel=1e-5, what=what + " vs two ops")
+    else:
+        ref32 = REF.linear(xr, wl, b, ln=False if rounded else ln, ln_eps=1e-5, out_dtype=torch.float32)
+        ref32 = TorchRef(torch.float32, "cpu").patch_filter(ref32, f, residual=rr)
+        assert_bf16(got.cpu(), ref32, what)
+        d = (got.float() - two.float()).abs().max().item()
+        assert d <= 2e-2 * max(1.0, ref32.abs().max().item()), f"{what} vs two ops: {d:.3e}"
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
