@@ -233,6 +233,15 @@ def time_cpu(fn, reps: int = 3) -> float:
     return statistics.median(ts)
 
 
+class _CpuMetrics:
+    """The float64 metric definitions on the host (the CPU leg of the metrics row)."""
+
+    @staticmethod
+    def metrics(pred, gt):
+        from oracle import metrics_ref
+        return metrics_ref.psnr(pred, gt), metrics_ref.ssim(pred, gt)
+
+
 class _OracleBackend:
     """The oracle behind the op dispatch (CPU baseline legs only)."""
 
@@ -266,10 +275,12 @@ def cpu_legs(step, others, e2e_reps: int, log=print) -> dict:
         r = refs[torch.float32 if c.dtype == "fp32" else torch.bfloat16]
         if c.config == 4:
             r = refs[torch.float32 if c.name.endswith("fp32") else torch.bfloat16]
+        if c.dtype == "fp64":
+            r = _CpuMetrics()
         with torch.no_grad():
-            t = time_cpu(lambda c=c, r=r: c.cpu_run(r))
-        per_op[c.name] = t * 1e3
-        log(f"[cpu] {c.name:<48} {t * 1e3:10.2f} ms")
+            t = time_cpu(lambda c=c, r=r: c.cpu_run(r)) * c.cpu_scale
+        per_op[c.name] = (t * 1e3, c.cpu_sample)
+        log(f"[cpu] {c.name:<48} {t * 1e3:10.2f} ms{'  (' + c.cpu_sample + ')' if c.cpu_sample else ''}")
     flops = sum(c.flops for c in step)
     r16 = refs[torch.bfloat16]
     with torch.no_grad():
@@ -344,7 +355,8 @@ def main() -> None:
     log(f"[bench] config-2 step: {len(step)} GEMMs, {flops_step / 1e9:.2f} GFLOP")
     others = [] if args.no_ops else (wl.config1_cases(hip32, dev) + wl.config3_cases(hip32, dev)
                                      + wl.config4_cases(hip, hip32, dev) + wl.config5_cases(hip, dev)
-                                     + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev)])
+                                     + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev),
+                                        wl.evssm_scan_case(hip, dev), wl.metrics_case(dev)])
     if args.pmc_pass:  # the last dispatches: two markers, the copy, then a marker before each op and one after
         cases = wl.all_cases(hip, hip32, dev)
         os.makedirs(os.path.dirname(os.path.abspath(args.pmc_cases)), exist_ok=True)
@@ -478,10 +490,13 @@ def main() -> None:
         legs = cpu_legs(step, others, 0 if args.no_e2e else args.cpu_e2e_reps, log=log)
         cpu = legs["baseline"]
         for r in rows:
-            ms = legs["per_op_ms"].get(r["op"])
-            if ms is not None:
+            got = legs["per_op_ms"].get(r["op"])
+            if got is not None:
+                ms, sample = got
                 r["cpu_ms"] = round(ms, 2)
                 r["cpu_over_gpu"] = round(ms * 1e3 / r["us"], 1)
+                if sample:
+                    r["cpu_sample"] = sample
         if e2e is not None and legs["e2e"] is not None:
             e2e["cpu"] = legs["e2e"]
         log(f"[bench] cpu baseline {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['ms_per_step']} ms/step)")

@@ -81,6 +81,11 @@ SIGNATURES = {
     "clarus_hip_boxmean_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "clarus_hip_boxmean": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t,
                                   _vp]),
+    "clarus_hip_psnr_ssim_workspace": (ctypes.c_size_t, [_i64, _i64]),
+    "clarus_hip_psnr_ssim": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, ctypes.c_size_t, _vp]),
+    "clarus_hip_selective_scan_workspace": (ctypes.c_size_t, [_i64, _i64, _i64]),
+    "clarus_hip_selective_scan": (_i32, [_vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp,
+                                         ctypes.c_size_t, _vp]),
     "clarus_hip_abi_version": (_i32, []),
     "clarus_hip_sizeof_gemm_args": (ctypes.c_size_t, []),
     "clarus_hip_sizeof_conv_args": (ctypes.c_size_t, []),

@@ -9,7 +9,9 @@ adapter (python/clarus/ops/triton_cuda.py): arguments the kernels do not handle 
 
 Ops served: linear, down, up, intro, ending, conv3x3, channel_attention, linear_per_image,
 patch_filter, linear_patch_filter, patch_corr, ln_mul_linear (the GEMM family), plus dwconv
-(depthwise 3x3 + gates, the next op on the NAFNet forward) and attention_apply (MDTA attn . V).
+(depthwise 3x3 + gates) and boxmean (the other ops of the NAFNet forward), selective_scan
+(EVSSM's state-space scan), attention_apply (MDTA attn . V) and linear_ln_linear (a residual
+GEMM and the LayerNorm GEMM on its output).
 
 Capture safety: kernels launch on torch's current stream, scratch comes from torch's
 allocator, weight re-layouts are computed once through `Backend.cached` (in the eager warm-up
@@ -527,6 +529,30 @@ class HipOps(Backend):
                        ldc=c, res=residual[i] if residual is not None else None, ldr=c, batch=heads, a_bs=ch,
                        w_bs=ch * ch, c_bs=ch, r_bs=ch)
         return out
+
+    # ------------------------------------------------------------------ state-space scan (EVSSM)
+    def selective_scan(self, u, dbl, dt_w, dt_bias, A, D):
+        """Mamba selective scan along each crop's raster sequence, d_state 8 (the reference's
+        scan, ops/torch_ref.py:312-341; acceptance as ops/triton_cuda.py:228-235):
+        clarus_hip_selective_scan, segments scanned in parallel. Returns fp32 [T, h, w, d]."""
+        r, ns = dt_w.shape[1], A.shape[1]
+        if (not (u.is_contiguous() and dbl.is_contiguous() and dbl.dtype == torch.float32) or ns != 8
+                or tuple(dbl.shape[:3]) != tuple(u.shape[:3]) or dbl.shape[-1] < r + 2 * ns):
+            raise Unsupported("selective_scan: contiguous inputs, fp32 dbl, d_state 8")
+        t, hh, ww, d = u.shape
+        if not (_kdt(u) and 1 <= r <= 16 and tuple(dt_w.shape) == (d, r) and tuple(A.shape) == (d, ns)):
+            raise Unsupported("selective_scan: bf16 / fp32 u, 1 <= r <= 16")
+        a2 = self.cached(A, "a2", lambda v: (v.float() * 1.4426950408889634).contiguous())
+        y = torch.empty(u.shape, device=u.device, dtype=torch.float32)
+        if y.numel() == 0:
+            return y
+        need = self.lib.clarus_hip_selective_scan_workspace(t, hh * ww, d)
+        scratch = torch.empty((need + 3) // 4, device=u.device, dtype=torch.float32)
+        _lib.check(self.lib.clarus_hip_selective_scan(
+            u.data_ptr(), _lib.dtype_code(u.dtype), dbl.data_ptr(), dbl.shape[-1], self._bias(dt_w.reshape(-1)).data_ptr(),
+            r, self._bias(dt_bias).data_ptr(), a2.data_ptr(), self._bias(D).data_ptr(), y.data_ptr(), t, hh * ww, d,
+            scratch.data_ptr(), need, self._stream(u)), "selective_scan")
+        return y
 
     # ------------------------------------------------------------------ frequency ops
     def patch_filter(self, x, f, residual=None, out_dtype=None):

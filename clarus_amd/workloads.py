@@ -25,7 +25,7 @@ from typing import Callable
 
 import torch
 
-PEAK_FLOPS = {"bf16": 2.5e15, "fp32": 157.3e12}
+PEAK_FLOPS = {"bf16": 2.5e15, "fp32": 157.3e12, "fp64": 78.6e12}
 PEAK_HBM = 8.0e12
 
 
@@ -41,6 +41,10 @@ class OpCase:
     # the same op on a CPU backend with the reference's op signatures (the caller passes the
     # backend, so this package never imports one): cpu_run(backend) runs it once on `cpu`
     cpu_run: Callable[[object], object] | None = None
+    # cpu_run covers 1 / cpu_scale of the op's work (a bounded sample where the CPU backend would
+    # take minutes); the reported CPU time is the sample's times cpu_scale
+    cpu_scale: float = 1.0
+    cpu_sample: str = ""
 
     def t_bound(self) -> tuple[float, str]:
         tm = self.flops / PEAK_FLOPS[self.dtype]
@@ -276,10 +280,60 @@ def fftformer_dffn_case(hip, device, seed: int = 0) -> OpCase:
                   lambda r: run(r, host))
 
 
+def evssm_scan_case(hip, device, seed: int = 0) -> OpCase:
+    """EVSSM level-0 selective scan at 720p: 8 crops of 384 x 384 (L = 147456), 96 channels,
+    r = 3, d_state 8, bf16 u (python/clarus/models/evssm/__init__.py:152). Per (step, channel):
+    F = 2 r (dt projection) + 4 (softplus) + 8 * 6 (state update) + 2 * 8 + 2 (output) flops,
+    plus 8 exp2; B = 2 (u) + 4 (y) bytes per (step, channel) + 4 (r + 16) per step (dbl). The
+    CPU sample is one of the 8 crops."""
+    g = _gen(seed + 13)
+    t, h, w, d, r = 8, 384, 384, 96, 3
+    L = h * w
+    u = torch.randn(t, h, w, d, generator=g).bfloat16()
+    dbl = torch.randn(t, h, w, r + 16, generator=g)
+    dtw = torch.randn(d, r, generator=g) * 0.5
+    dtb = torch.randn(d, generator=g) - 2
+    dsk = torch.randn(d, generator=g)
+    A = -torch.rand(d, 8, generator=g) * 4 - 0.5
+    host = dict(u=u, dbl=dbl, dtw=dtw, dtb=dtb, A=A, dsk=dsk)
+    dv = {n: v.to(device) for n, v in host.items()}
+    sample = {n: (v[:1] if n in ("u", "dbl") else v) for n, v in host.items()}
+
+    def run(be=None, a=dv):
+        return (be or hip).selective_scan(a["u"], a["dbl"], a["dtw"], a["dtb"], a["A"], a["dsk"])
+    flops = t * L * d * (2.0 * r + 4 + 8 * 6 + 2 * 8 + 2)
+    nbytes = t * L * d * (2.0 + 4.0) + t * L * (r + 16) * 4.0
+    return OpCase("evssm L0 selective scan 8 x 384x384 d96", 0, "fp32", flops, nbytes, run, host,
+                  lambda be: run(be, sample), cpu_scale=float(t), cpu_sample="one of the 8 crops, times 8")
+
+
+def metrics_case(device, seed: int = 0) -> OpCase:
+    """PSNR + SSIM of a 720p uint8 pair (the evaluation loop's per-image metrics). F: per
+    pixel-channel ~11 * 30 (channel mix + horizontal taps of 5 moments) + 11 * 10 (vertical) + 20
+    (SSIM map) fp64 flops and 3 (squared difference); B = 2 * 3 bytes per pixel."""
+    from .metrics import make_metrics
+    g = _gen(seed + 17)
+    h, w = 720, 1280
+    gt = torch.randint(0, 256, (h, w, 3), generator=g, dtype=torch.uint8)
+    pred = (gt.float() * 0.9 + 12 + 6 * torch.randn(h, w, 3, generator=g)).round().clamp(0, 255).to(torch.uint8)
+    m = make_metrics(device, "hip")
+    a, b = pred.to(device), gt.to(device)
+    res = torch.zeros(2, dtype=torch.float64, device=device)
+    sc = m.scratch(h, w)
+
+    def run():
+        m.compute(a, b, res, sc)
+        return res
+    n = h * w * 3
+    return OpCase("psnr + ssim 720p (uint8, fp64 moments)", 0, "fp64", n * (11 * 30 + 11 * 10 + 20 + 3), 2.0 * n, run,
+                  {"pred": pred, "gt": gt}, lambda be: be.metrics(pred.numpy(), gt.numpy()))
+
+
 def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
     """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5,
-    the fused FFTformer DFFN op and the fused NAFNet pair."""
+    the fused FFTformer DFFN op, the fused NAFNet pair, EVSSM's scan and the metrics."""
     return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
             + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
             + config5_cases(hip_bf16, device, seed) + [fftformer_dffn_case(hip_bf16, device, seed),
-                                                        nafnet_pair_case(hip_bf16, device, seed)])
+                                                        nafnet_pair_case(hip_bf16, device, seed),
+                                                        evssm_scan_case(hip_bf16, device, seed), metrics_case(device, seed)])

@@ -310,6 +310,38 @@ int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int32_t o_dtyp
                        int64_t w, int64_t c, int64_t k1, int64_t k2, void* scratch, size_t scratch_bytes,
                        void* stream);
 
+/*
+ * PSNR and SSIM of two images on the device, basicsr's definitions (calculate_psnr /
+ * calculate_ssim, crop_border 0): pred and gt contiguous uint8 [h, w, 3]; res[0] = PSNR in dB
+ * (exact integer sum of squared differences; peak 1 when max(pred) <= 1, else 255; +inf for
+ * identical images), res[1] = SSIM (the 11 x 11 x 11 Gaussian, sigma 1.5, over (h, w, channel)
+ * with replicate padding, C1 = (0.01 peak)^2, C2 = (0.03 peak)^2, mean of the map; fp64
+ * moments). res: 2 float64 on the device, written by the last kernel; no host synchronisation.
+ * scratch holds clarus_hip_psnr_ssim_workspace(h, w) bytes, 16-byte aligned.
+ * replaces python/clarus/metrics.py:59-159 (ssd_max_kernel, ssim_h_kernel, ssim_v_kernel) and
+ * TritonMetrics.compute (:164-246)
+ */
+size_t clarus_hip_psnr_ssim_workspace(int64_t h, int64_t w);
+int clarus_hip_psnr_ssim(const void* pred, const void* gt, int64_t h, int64_t w, double* res,
+                         void* scratch, size_t scratch_bytes, void* stream);
+
+/*
+ * EVSSM's Mamba selective scan (one direction, no z gate, d_state 8) along each crop's raster
+ * sequence: delta_l = softplus(dbl_l[0 .. r) . dt_w[d] + dt_b[d]);
+ * h_l[n] = 2^(delta_l a2[d, n]) h_{l-1}[n] + delta_l dbl_l[r + n] u_l[d];
+ * y_l[d] = sum_n dbl_l[r + 8 + n] h_l[n] + dsk[d] u_l[d], h_{-1} = 0.
+ * u [t, l, d] contiguous (u_dtype bf16 or fp32); dbl [t, l, nc] fp32 (nc >= r + 16: dt_raw | B |
+ * C); dt_w [d, r] (1 <= r <= 16), dt_b [d], a2 [d, 8] = A log2(e), dsk [d] fp32; y [t, l, d] fp32.
+ * The sequence is cut into segments scanned in parallel and joined by their exact start states;
+ * scratch holds clarus_hip_selective_scan_workspace(t, l, d) bytes. Deterministic.
+ * replaces python/clarus/kernels/ssm.py:149-190 selective_scan (scan8_kernel, carry_kernel)
+ */
+size_t clarus_hip_selective_scan_workspace(int64_t t, int64_t l, int64_t d);
+int clarus_hip_selective_scan(const void* u, int32_t u_dtype, const float* dbl, int64_t nc, const float* dt_w,
+                              int64_t r, const float* dt_b, const float* a2, const float* dsk, float* y,
+                              int64_t t, int64_t l, int64_t d, void* scratch, size_t scratch_bytes,
+                              void* stream);
+
 /* ABI version (CLARUS_HIP_ABI_VERSION) and struct sizes, for binding checks. */
 int clarus_hip_abi_version(void);
 size_t clarus_hip_sizeof_gemm_args(void);

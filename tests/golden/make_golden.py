@@ -26,6 +26,11 @@ tests/test_oracle.py pin every single GEMM-family op, but not how the reference 
   odd 13x22 or 9x16 image (reflect padding) and a 16x16 one; the fp32 intermediate between the GEMM and
   the filter is what the bf16 cases pin (a rounded intermediate gives other bits).
 
+* metrics.safetensors: the reference's on-device metric semantics on the CPU: its host psnr()
+  (basicsr rule, python/clarus/metrics.py:46-56) and TorchMetrics.compute (the fp32 restatement of
+  its Triton SSIM, :202-269) on small uint8 image pairs: random, a blurred / noisy pair, one
+  with max(pred) <= 1 (peak 1), identical images, odd sizes.
+
 Inputs are drawn from one torch.Generator seeded per case; the generator is in this file, so the
 fixtures can be rewritten, but the tests read only the stored tensors.
 """
@@ -183,6 +188,32 @@ def freq_fixture(ref_root: str) -> dict:
     return {k: v.contiguous() for k, v in out.items()}
 
 
+METRIC_CASES = [("rand", 23, 37), ("blur", 40, 52), ("small", 17, 29), ("same", 21, 19), ("tall", 64, 11)]
+
+
+def metrics_fixture(ref_root: str) -> dict:
+    from clarus.metrics import TorchMetrics, psnr
+
+    g = torch.Generator().manual_seed(41)
+    m = TorchMetrics(torch.device("cpu"))
+    out = {}
+    for name, h, w in METRIC_CASES:
+        if name == "small":
+            a = torch.randint(0, 2, (h, w, 3), generator=g, dtype=torch.uint8)
+            b = torch.randint(0, 2, (h, w, 3), generator=g, dtype=torch.uint8)
+        elif name == "blur":
+            b = torch.randint(0, 256, (h, w, 3), generator=g, dtype=torch.uint8)
+            a = (b.float() * 0.8 + 20 + 8 * torch.randn(h, w, 3, generator=g)).round().clamp(0, 255).to(torch.uint8)
+        else:
+            a = torch.randint(0, 256, (h, w, 3), generator=g, dtype=torch.uint8)
+            b = a.clone() if name == "same" else torch.randint(0, 256, (h, w, 3), generator=g, dtype=torch.uint8)
+        res = torch.zeros(2, dtype=torch.float64)
+        m.compute(a, b, res)
+        out.update({f"{name}.pred": a, f"{name}.gt": b, f"{name}.torch_metrics": res,
+                    f"{name}.psnr": torch.tensor([psnr(a.numpy(), b.numpy())], dtype=torch.float64)})
+    return out
+
+
 def main(ref_root: str = "/root/reference", which: str = "all") -> None:
     sys.path.insert(0, os.path.join(ref_root, "python"))
     torch.manual_seed(0)
@@ -198,6 +229,10 @@ def main(ref_root: str = "/root/reference", which: str = "all") -> None:
         save_file(freq_fixture(ref_root), os.path.join(HERE, "ops_freq.safetensors"),
                   metadata={"cases": json.dumps(LPF_CASES)})
         written.append("ops_freq.safetensors")
+    if which in ("all", "metrics"):
+        save_file(metrics_fixture(ref_root), os.path.join(HERE, "metrics.safetensors"),
+                  metadata={"cases": json.dumps(METRIC_CASES)})
+        written.append("metrics.safetensors")
     for f in written:
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
