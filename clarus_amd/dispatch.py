@@ -57,7 +57,7 @@ def _register_backend(name: str, path: str | None = None):
 def backend_class(name: str):
     entry = _REGISTRY.get(name)
     if entry is None:
-        raise ValueError(f"unknown op backend {name!r}; known: {sorted(_REGISTRY)}")
+        raise ValueError(f"{name!r} is not a registered backend (registered: {', '.join(sorted(_REGISTRY))})")
     if isinstance(entry, str):
         module, cls = entry.split(":")
         entry = getattr(importlib.import_module(module), cls)
@@ -119,21 +119,21 @@ class _Ops:
                 self.backends.append(backend_class(name)(dtype, device))
             except _BackendUnavailable as exc:
                 self.skipped[name] = str(exc)
-                log(f"[clarus] op backend {name!r} unavailable: {exc}")
+                log(f"[dispatch] skipping backend {name!r}: {exc}")
         if not self.backends:
-            raise RuntimeError(f"no usable op backend among {backends}: {self.skipped}")
+            raise RuntimeError(f"none of the backends {backends} could be constructed ({self.skipped})")
         self.by_name = {b.name: b for b in self.backends}
         self.overrides = dict(overrides or {})
         for op, bname in self.overrides.items():
             if bname not in self.by_name:
-                raise ValueError(f"op_overrides: {op} -> {bname!r}, but backend {bname!r} is not active")
+                raise ValueError(f"override pins {op!r} to {bname!r}, which is not in this chain")
         self.served: collections.Counter = collections.Counter()
 
     def _chain(self, op: str):
         chain = [self.by_name[self.overrides[op]]] if op in self.overrides else self.backends
         impls = [(b.name, getattr(b, op)) for b in chain if callable(getattr(b, op, None))]
         if not impls:
-            raise AttributeError(f"no backend implements op {op!r}")
+            raise AttributeError(f"{op!r}: not an op of any backend in the chain")
         return impls
 
     def __getattr__(self, op: str):

@@ -49,7 +49,8 @@ class OpCase:
     def t_bound(self) -> tuple[float, str]:
         tm = self.flops / PEAK_FLOPS[self.dtype]
         tb = self.nbytes / PEAK_HBM
-        return (tm, "mfma") if tm >= tb else (tb, "hbm")
+        # fp64 ops (the metrics) run on the vector ALUs; MI355X's fp64 vector and matrix peaks agree
+        return (tm, "fp64" if self.dtype == "fp64" else "mfma") if tm >= tb else (tb, "hbm")
 
 
 def kernel_of(case: OpCase) -> str:
