@@ -82,9 +82,11 @@ def summarize_trace(directory: str) -> None:
 
 
 def summarize_e2e(directory: str, top: int = 40) -> None:
-    """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: launches from
-    the first intro kernel (intro_mfma_kernel / intro_kernel, the NAFNet stem) on, grouped by
-    (kernel, grid), divided by the number of forwards in the trace (one intro kernel each)."""
+    """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: the launches from
+    the first intro kernel (intro_mfma_kernel / intro_kernel, the NAFNet stem) on, cut into forwards
+    at each intro kernel, each forward classed by its call pattern (paired linear_ln_linear ops when
+    it launches gemm_rowln_kernel<true>, else the reference block), grouped by (kernel, grid) and
+    divided by the number of forwards of that pattern."""
     files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {directory}")
@@ -93,25 +95,41 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
         with open(f) as fh:
             rows += list(csv.DictReader(fh))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
     def is_intro(r):
         name = r.get("Kernel_Name", "")
         return "intro_kernel" in name or "intro_mfma_kernel" in name
-    first = next((i for i, r in enumerate(rows) if is_intro(r)), None)
-    if first is None:
+    starts = [i for i, r in enumerate(rows) if is_intro(r)]
+    if not starts:
         raise SystemExit("no NAFNet forward (intro kernel) in the trace")
-    e2e = rows[first:]
-    nfwd = sum(1 for r in e2e if is_intro(r))
-    groups: dict = {}
-    for r in e2e:
-        name = r.get("Kernel_Name", "?").replace("(anonymous namespace)::", "")
-        name = name.split("(")[0].replace("void ", "")
-        grid = r.get("Grid_Size_X") or r.get("Grid_Size", "?")
-        groups.setdefault((name, grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
-    total = sum(sum(v) for v in groups.values()) / nfwd
-    print(f"forwards {nfwd}, launches per forward {len(e2e) / nfwd:.0f}, kernel time per forward {total:.0f} us")
-    print(f"{'us/fwd':>8} {'calls':>6} {'mean_us':>8}  grid  kernel")
-    for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
-        print(f"{sum(d) / nfwd:8.1f} {len(d) / nfwd:6.1f} {statistics.mean(d):8.2f}  {grid}  {name[:100]}")
+    forwards = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
+    # the last forward runs to the end of the trace: cut it after its ending conv (conv_halo_kernel<16, ...)
+    last = forwards[-1]
+    ends = [i for i, r in enumerate(last) if "conv_halo_kernel<16" in r.get("Kernel_Name", "")]
+    if ends:
+        forwards[-1] = last[:ends[-1] + 1]
+    patterns = {"paired linear_ln_linear ops": [], "reference block (five linear calls)": []}
+    for fw in forwards:
+        fused = any("gemm_rowln_kernel<true>" in r.get("Kernel_Name", "") for r in fw)
+        patterns["paired linear_ln_linear ops" if fused else "reference block (five linear calls)"].append(fw)
+    for pat, fws in patterns.items():
+        if not fws:
+            continue
+        nfwd = len(fws)
+        groups: dict = {}
+        for fw in fws:
+            for r in fw:
+                name = r.get("Kernel_Name", "?").replace("(anonymous namespace)::", "")
+                name = name.split("(")[0].replace("void ", "")
+                grid = r.get("Grid_Size_X") or r.get("Grid_Size", "?")
+                groups.setdefault((name, grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+        total = sum(sum(v) for v in groups.values()) / nfwd
+        nl = sum(len(fw) for fw in fws) / nfwd
+        print(f"== {pat}: forwards {nfwd}, launches per forward {nl:.0f}, kernel time per forward {total:.0f} us")
+        print(f"{'us/fwd':>8} {'calls':>6} {'mean_us':>8}  grid  kernel")
+        for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+            print(f"{sum(d) / nfwd:8.1f} {len(d) / nfwd:6.1f} {statistics.mean(d):8.2f}  {grid}  {name[:100]}")
+        print()
 
 
 COPY_BYTES = 256 * 1024 * 1024  # the pmc pass's calibration copy: this many bytes read and written

@@ -22,6 +22,7 @@
 // waves (LDS) give the mean, a second exchange the variance (two-pass, as the reference), then
 // (y - mean) * rsqrt(var + eps) is rounded to bf16 and stored as the next GEMM's A rows.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi.hpp"
 #include "gemm_mfma32.hpp"
@@ -62,7 +63,9 @@ constexpr int L2_ROWS = 512;                     // W^T rows per pass
 constexpr int L2_STEPS = RL_N / 16;              // 16-k steps per pass (32)
 constexpr int L2_GROUPS = L2_STEPS / 4;          // 64-k groups per pass (8)
 constexpr int L2_A = 0;                          // LN rows: 64 rows x 1 KiB, units XOR (row % 16)
-static_assert(RL_P * RL_N * 2 <= RL_RING, "the LN rows reuse the first GEMM's ring");
+constexpr int L2_OUT = RL_P * RL_N * 2;          // a pass's output per wave: 64 pixels x 64 channels bf16
+constexpr int L2_OUT_WAVE = RL_P * 64 * 2;       // 8 KiB per wave
+static_assert(L2_OUT + RL_WAVES * L2_OUT_WAVE <= RL_RING, "the LN rows and the output staging reuse the ring");
 
 struct Ln2P {
   const void* w2p;     // packed W^T rows (above), bf16
@@ -419,22 +422,27 @@ gemm_rowln_kernel(const GemmP p, const RowLnP q, const Ln2P r2) {
             for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf2[buf][ks][rb], af2[pb], acc[pb][rb]);
         }
       };
-      // pass epilogue: + bias2 (SimpleGate), rounded once to bf16, stored from the MFMA layout
-      // (16 consecutive channels of one pixel per lane and block)
+      // pass epilogue: + bias2 (SimpleGate), rounded once to bf16, through the wave's LDS staging
+      // (64 pixel rows of its 64 channels, 32 with the gate; 16-byte units XOR-swizzled by row) so
+      // each store instruction writes 8 whole 128-byte row pieces (16 of 64 bytes with the gate)
+      // instead of 64 16-byte pieces from the MFMA layout
+      unsigned char* so = lds + L2_OUT + wave_f * L2_OUT_WAVE;
       auto pass_epilogue = [&](const int pass) __attribute__((always_inline)) {
+        const bool GATE = r2.gate;
+        const int upr = GATE ? 4 : 8;  // 16-byte units per staged row
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
-          const int64_t qq = q0 + pb * 32 + l32f;
+          const int px = pb * 32 + l32f;
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) {
-            if (r2.gate && rb == 1) continue;
-            const int c0 = r2.gate ? pass * (L2_ROWS / 2) + wave_f * 32 + 16 * hlf
-                                   : pass * L2_ROWS + wave_f * 64 + rb * 32 + 16 * hlf;
+            if (GATE && rb == 1) continue;
+            const int lc = GATE ? 16 * hlf : rb * 32 + 16 * hlf;  // first channel within the wave's run
+            const int c0 = GATE ? pass * (L2_ROWS / 2) + wave_f * 32 + lc : pass * L2_ROWS + wave_f * 64 + lc;
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const f32x4 b1 = r2.bias2 ? *reinterpret_cast<const f32x4*>(r2.bias2 + c0 + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
-              if (r2.gate) {
+              if (GATE) {
                 const f32x4 b2 = r2.bias2 ? *reinterpret_cast<const f32x4*>(r2.bias2 + r2.n2w / 2 + c0 + 4 * i)
                                           : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -444,17 +452,26 @@ gemm_rowln_kernel(const GemmP p, const RowLnP q, const Ln2P r2) {
                 for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
               }
             }
-            if (qq < p.m) {
-              unsigned char* op = (unsigned char*)r2.out2 + (qq * r2.ld2 + c0) * 2;
 #pragma unroll
-              for (int h = 0; h < 2; ++h) {
-                f32x8 o;
+            for (int h = 0; h < 2; ++h) {
+              f32x8 o;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) o.v[i] = v[8 * h + i];
-                *reinterpret_cast<bf16x8*>(op + 16 * h) = pack_bf16(o);
-              }
+              for (int i = 0; i < 8; ++i) o.v[i] = v[8 * h + i];
+              const int u = lc / 8 + h;
+              *reinterpret_cast<bf16x8*>(so + px * upr * 16 + (u ^ (px & (upr - 1))) * 16) = pack_bf16(o);
             }
           }
+        }
+        // read back in row order (the wave's own staging: its LDS accesses stay in order)
+        const int ppi = 64 / upr;  // pixels per store instruction
+        const int c_base = GATE ? pass * (L2_ROWS / 2) + wave_f * 32 : pass * L2_ROWS + wave_f * 64;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          if (j * ppi >= RL_P) break;
+          const int px = j * ppi + lane_f / upr, u = lane_f % upr;
+          const bf16x8 ov = *reinterpret_cast<const bf16x8*>(so + px * upr * 16 + (u ^ (px & (upr - 1))) * 16);
+          const int64_t qq = q0 + px;
+          if (qq < p.m) *reinterpret_cast<bf16x8*>((unsigned char*)r2.out2 + (qq * r2.ld2 + c_base + u * 8) * 2) = ov;
         }
 #pragma unroll
         for (int a = 0; a < 2; ++a)
