@@ -125,6 +125,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// A raw buffer descriptor for base address p (wave-uniform): 32-bit byte offsets from p, a
+// range of 2^31 - 1 bytes, word 3 = 0x00020000 (32-bit data format, as CDNA's untyped buffer
+// instructions need). Loads and stores through it take a scalar base and a VGPR offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+
 // exact-erf GELU (torch.nn.functional.gelu default)
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
