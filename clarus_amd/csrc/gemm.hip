@@ -359,7 +359,9 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
   // (interleaved A/B on the NAFNet shapes, us):
   //   * gated, with at least 200 tiles of 256 pixels x 256 W^T rows: gemm_big_kernel (level-3
   //     conv4 28.8 vs 31.7 on 32x32 / 29.8 on 16x16; level-2 conv4 33.6 vs 37.4 / 35.9);
-  //   * with a residual and K > 256: 32x32 MFMAs (K = 512 with an fp32 residual: 25.2 vs 28.6);
+  //   * with a residual, K > 256 and at least 320 tiles of 128 x 128: 32x32 MFMAs (K = 512 with an
+  //     fp32 residual, 452 tiles: 25.2 vs 28.6); with fewer tiles 16x16 (config-2 c1024
+  //     c->c+scale+res, 3600 x 1024 x 1024, 232 tiles: 29.3 vs 32.1);
   //   * otherwise 16x16 MFMAs (level-3 conv1 34.0 vs 36.7; level-2 conv1 41.6 vs 43.8;
   //     c1024 rows 29.1 vs 32.1; c256 c->c+scale+res 31.2 vs 35.6)
   const bool long_auto = a->tile == 0 && (auto_dma || use_lds);
@@ -369,7 +371,7 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
     launch_gemm_big(p, a->gate != 0, a->tile == 15 ? 1 : 2, (hipStream_t)stream);
     return check_launch("gemm");
   }
-  const bool m32_auto = m32_ok && long_auto && a->res && a->k > 256;
+  const bool m32_auto = m32_ok && long_auto && a->res && a->k > 256 && cdiv(a->m, 128) * cdiv(a->n, 128) >= 320;
   if (a->tile == 13 || m32_auto) {
     note_kernel("gemm_mfma32_kernel gate=%d", a->gate != 0);
     launch_gemm_m32(p, a->gate != 0, (hipStream_t)stream);

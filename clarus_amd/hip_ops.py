@@ -79,6 +79,10 @@ class HipOps(Backend):
     # output written by its epilogue (clarus_hip_gemm_ln_rows) and then the second GEMM on those
     # rows when only the first fits; False runs the two linear ops.
     fuse_ln_rows = True
+    # The fused pair with K = 512 and an fp32 residual on clarus_hip_gemm_ln_gemm_w1p (both weights
+    # streamed into registers, the residual staged in LDS during the first GEMM); False keeps it on
+    # clarus_hip_gemm_ln_gemm (the first GEMM's weights staged through LDS).
+    pair_w1p = True
     # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
@@ -325,9 +329,16 @@ class HipOps(Backend):
         if fused:
             n2w = w2.shape[1]
             u = torch.empty((n, h, wd, n2w // 2 if gate2 else n2w), device=x.device, dtype=torch.bfloat16)
-            _lib.check(self.lib.clarus_hip_gemm_ln_gemm(
-                ctypes.byref(args), float(ln_eps), rms, self._w2p(w2, bool(gate2)).data_ptr(), _lib.ptr(b2),
-                u.data_ptr(), n2w, int(bool(gate2)), self._stream(a)), "linear_ln_linear")
+            if args.k == 512 and residual.dtype == torch.float32 and self.pair_w1p:
+                # both weights streamed into registers, the residual staged in LDS during the K loop
+                _lib.check(self.lib.clarus_hip_gemm_ln_gemm_w1p(
+                    ctypes.byref(args), self._w2p(w, False).data_ptr(), float(ln_eps), rms,
+                    self._w2p(w2, bool(gate2)).data_ptr(), _lib.ptr(b2), u.data_ptr(), n2w, int(bool(gate2)),
+                    self._stream(a)), "linear_ln_linear")
+            else:
+                _lib.check(self.lib.clarus_hip_gemm_ln_gemm(
+                    ctypes.byref(args), float(ln_eps), rms, self._w2p(w2, bool(gate2)).data_ptr(), _lib.ptr(b2),
+                    u.data_ptr(), n2w, int(bool(gate2)), self._stream(a)), "linear_ln_linear")
             self.pair_launches["gemm_ln_gemm"] += 1
             return y, u
         rows = torch.empty((n, h, wd, 512), device=x.device, dtype=torch.bfloat16)

@@ -173,6 +173,19 @@ int clarus_hip_gemm_ln_gemm(const ClarusGemmArgs* args, float eps, int32_t rms, 
                             void* out2, int64_t n2w, int32_t gate2, void* stream);
 
 /*
+ * clarus_hip_gemm_ln_gemm for K = N = 512 and an fp32 residual, with the first GEMM's weight also
+ * passed packed: w1p holds W1^T [512][512] in w2p's fragment order for one 512-row pass without
+ * the gate (n2w = 512, gate2 = 0), and args->wt is not read. Both weights stream from L2 into
+ * registers and the residual tile is staged in LDS during the first GEMM; args->c is written,
+ * bit-identical to clarus_hip_gemm_ln_rows's output, and out2 as clarus_hip_gemm_ln_gemm's up
+ * to the row statistics' summation order.
+ * No counterpart in the reference: the same fusion as clarus_hip_gemm_ln_gemm, for NAFNet's
+ * level-3 pairs (conv3 -> conv4, conv5 -> conv1).
+ */
+int clarus_hip_gemm_ln_gemm_w1p(const ClarusGemmArgs* args, const void* w1p, float eps, int32_t rms, const void* w2p,
+                                const float* bias2, void* out2, int64_t n2w, int32_t gate2, void* stream);
+
+/*
  * Dense 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM:
  *   y = act(conv3x3(up2 ? nearest_x2(x) : x) + bias) * out_scale (+ residual)
  * x [batch, h, w, cin] with pixel stride ldx (h, w = INPUT size); wt [cout][9 * cin] with

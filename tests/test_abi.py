@@ -66,6 +66,12 @@ def test_validation_rejects_before_launch(lib):
     a.n, a.ldc = 512, 512
     assert lib.clarus_hip_gemm_ln_gemm(ctypes.byref(a), 1e-6, 0, 16, None, 16, 768, 1, None) == _lib.EINVAL  # n2w
     assert b"n2w" in lib.clarus_hip_last_error()
+    a.k, a.lda, a.res, a.ldr, a.r_dtype = 512, 512, 16, 512, _lib.BF16
+    assert lib.clarus_hip_gemm_ln_gemm_w1p(ctypes.byref(a), 16, 1e-6, 0, 16, None, 16, 1024, 1, None) == _lib.EINVAL
+    assert b"fp32 residual" in lib.clarus_hip_last_error()
+    a.r_dtype = _lib.F32
+    assert lib.clarus_hip_gemm_ln_gemm_w1p(ctypes.byref(a), 16, 1e-6, 0, 16, None, 16, 768, 1, None) == _lib.EINVAL
+    assert b"n2w" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
 

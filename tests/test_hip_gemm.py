@@ -589,11 +589,13 @@ def test_linear_ln_linear_rows_path(hip_bf16):
 @pytest.mark.parametrize("gate2,n2w,ln,res_dt", [(True, 1024, True, torch.float32), (False, 1024, True, torch.float32),
                                                  (True, 512, "rms", torch.bfloat16), (False, 512, True, None)])
 def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
-    """clarus_hip_gemm_ln_gemm (HipOps.linear_ln_linear) against the same two GEMMs run apart
-    (clarus_hip_gemm_ln_rows, then a GEMM on the rows it wrote). The first output is the same
-    kernel code (bit-identical); so are the normalised rows, which the fused kernel keeps in
-    LDS, so the second output differs only by the second GEMM's summation order (another
-    kernel): within one bf16 rounding step. Both outputs are also held to the oracle: y to the
+    """clarus_hip_gemm_ln_gemm / clarus_hip_gemm_ln_gemm_w1p (HipOps.linear_ln_linear) against the
+    same two GEMMs run apart (clarus_hip_gemm_ln_rows, then a GEMM on the rows it wrote). The first
+    output is bit-identical (the same fp32 products and summation order). The normalised rows the
+    fused kernel keeps in LDS are the same fp32 LayerNorm, but the w1p kernel sums its statistics in
+    another order, so about 1e-4 of the row elements round to the neighbouring bf16 value; the
+    second output then agrees within one bf16 rounding step except, where u is small, at a few
+    elements such a row element feeds. Both outputs are also held to the oracle: y to the
     bf16 / fp32 rule, u to the fp32 LayerNorm GEMM within rounding_bound (the rows rounded once to
     bf16, as the reference's ln_rows pass does) plus the output's bf16 rounding. M = 1230 leaves
     a ragged last 64-pixel tile."""
@@ -633,7 +635,8 @@ def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
     u0, u1 = u0.float().cpu(), u1.float().cpu()
     assert torch.isfinite(u1).all()
     d = (u0 - u1).abs()
-    assert (d <= 2 ** -7 * u0.abs() + 1e-6).all(), d.max().item()
+    beyond = (d > 2 ** -7 * u0.abs() + 1e-6).float().mean().item()
+    assert beyond <= 1e-3, (beyond, d.max().item())
     assert (d > 0).float().mean().item() <= 0.02
     # against the oracle: y as the reference's fused_gemm; u as its LayerNorm GEMM on y in fp32,
     # within the bound that rounding every normalised row element once to bf16 allows (the
@@ -647,6 +650,43 @@ def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
              + 2 ** -8 * u_ref.abs() + 1e-5 * u_ref.abs().max().item())
     du = (u1.double() - u_ref).abs()
     assert bool((du <= bound).all()), f"u vs oracle: {int((du > bound).sum())} beyond the bound, max {du.max():.3e}"
+
+
+@pytest.mark.parametrize("gate2,odt,m", [(True, torch.float32, 1230), (False, torch.bfloat16, 64 * 40 + 7)])
+def test_linear_ln_linear_w1p_vs_pair(gate2, odt, m, hip_bf16):
+    """The two fused pair kernels on the same fp32-residual operands: clarus_hip_gemm_ln_gemm_w1p
+    (HipOps.pair_w1p, W1 packed and streamed through registers) and clarus_hip_gemm_ln_gemm (W1
+    from LDS). y: the same fp32 products in the same order, bit-identical. u: the LayerNorm
+    statistics are summed in another order, so it agrees within one bf16 rounding step except at
+    a few elements (at most 1e-3) where a row element rounded to the neighbouring bf16 value and u
+    is small. bf16 y and an M that ends in a 7-pixel tile are the second case."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(48)
+    x = rnd(g, 1, 1, m, 512, dtype=torch.bfloat16).cuda()
+    w3, b3 = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 512).cuda()
+    w4, b4 = rnd(g, 512, 1024, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 1024).cuda()
+    beta = rnd(g, 512).cuda()
+    inp = (2 + rnd(g, 1, 1, m, 512)).cuda()
+    saved = HipOps.pair_w1p
+    outs, kernels = [], []
+    try:
+        for w1p in (True, False):
+            HipOps.pair_w1p = w1p
+            outs.append(hip_bf16.linear_ln_linear(x, w3, b3, scale=beta, residual=inp, out_dtype=odt, w2=w4,
+                                                  bias2=b4, gate2=gate2, ln=True))
+            kernels.append(_lib.last_kernel())
+    finally:
+        HipOps.pair_w1p = saved
+    assert kernels[0].startswith("pair_kernel") and kernels[1].startswith("gemm_rowln_kernel"), kernels
+    (y1, u1), (y0, u0) = outs
+    assert torch.equal(y0, y1)
+    u0, u1 = u0.float().cpu(), u1.float().cpu()
+    assert torch.isfinite(u1).all()
+    d = (u0 - u1).abs()
+    beyond = (d > 2 ** -7 * u0.abs() + 1e-6).float().mean().item()
+    assert beyond <= 1e-3 and (d > 0).float().mean().item() <= 0.02, (beyond, d.max().item())
+    assert d.max().item() <= 0.25, d.max().item()
 
 
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
