@@ -1,0 +1,403 @@
+// Long-K bf16 GEMM with the weight streamed from L2 into registers: clarus_hip_gemm_wp (gfx950).
+//
+// y = act(A W^T + bias (SimpleGate: the product of both halves)) * scale * out_scale (+ residual)
+// for plain bf16 rows A [m][K] (no prologue), K % 128 == 0, and W^T rows (N, or 2 N with the gate)
+// a multiple of 512, with W^T also passed packed in the MFMA fragment order of
+// clarus_hip_gemm_ln_gemm's second weight.
+//
+// Why: on the NAFNet level-2..4 shapes (M = 3600 .. 57600, K = 256 .. 1024) the LDS-staged tile
+// kernels spend their K loop on LDS traffic (a 128 x 128 tile moves 32 KiB of copies and 64 KiB of
+// fragment reads per 64-k chunk, about the MFMA time again) with one chunk in flight, and their
+// epilogue reads the residual after the K loop, when every workgroup does so at once.
+//
+// One workgroup of 8 waves per (64-pixel tile, 512-row pass of W^T); wave w computes the 64 pixels
+// x 64 W^T rows 64 w .. 64 w + 63 of the pass (2 x 2 blocks of 32x32x16 MFMAs, 64 accumulators):
+//   * A chunks (64 rows x 64 k, 8 KiB) go global -> LDS by direct copies into a 3-stage ring
+//     shared by the 8 waves, two chunks ahead; a chunk costs 8 KiB of copies and 64 KiB of
+//     fragment reads;
+//   * each wave's W^T fragments come from L2 straight into registers, packed so that one load
+//     instruction moves 1 KiB of consecutive bytes, two 64-k groups (8 loads each) ahead: with one
+//     group ahead the L2 round trip under this load (~1 us) exceeded a chunk's MFMA time and the
+//     K loop took 1.2 - 1.8 us per chunk;
+//   * the tile's residual (64 pixels x the pass's output channels) is copied into LDS during the
+//     K loop, a few 1 KiB copies per chunk, so the epilogue reads it from LDS;
+//   * epilogue in the MFMA layout: a lane holds 16 consecutive output channels of one pixel.
+// Tiles are dealt XCD-aware: a contiguous range of (tile, pass) pairs per XCD, the passes of a
+// pixel tile adjacent, so an A tile is fetched into one XCD's L2 once for all its passes.
+// Memory waits are explicit vmcnt counts: loads and copies complete in issue order.
+// replaces kernels/gemm.py:353-400 (fused_gemm) for these shapes
+#include "capi.hpp"
+#include "gemm_mfma32.hpp"
+
+namespace clarus {
+
+namespace {
+
+constexpr int WS_P = 64, WS_WAVES = 8, WS_THREADS = 64 * WS_WAVES;
+constexpr int WS_STAGE = WS_P * 128;                 // 8 KiB
+constexpr int WS_STAGES = 3;
+constexpr int WS_RES_MAX = WS_P * 512 * 4;           // 128 KiB: 64 rows x 512 fp32 channels
+constexpr int WS_TB_FLOATS = 1024;                   // bias (512 W^T rows) + scale (<= 512 outputs)
+
+__host__ __device__ constexpr int ws_res_row_bytes(bool gate, int rdt) {
+  return rdt < 0 ? 0 : (gate ? 256 : 512) * (rdt == DT_F32 ? 4 : 2);
+}
+// A area: without a residual the whole A tile stays in LDS (NCH chunks), else the 3-stage ring
+__host__ __device__ constexpr int ws_a_bytes(int rdt, int nch) { return (rdt < 0 ? nch : WS_STAGES) * WS_STAGE; }
+__host__ __device__ constexpr int ws_lds_bytes(bool gate, int rdt, int nch) {
+  return ws_a_bytes(rdt, nch) + WS_P * ws_res_row_bytes(gate, rdt) + WS_TB_FLOATS * 4;
+}
+static_assert(ws_lds_bytes(false, DT_F32, 16) <= 160 * 1024 && ws_lds_bytes(false, -1, 16) <= 160 * 1024, "LDS");
+
+struct WsP {
+  const bf16_t* a;    // [m][lda]
+  const void* wp;     // W^T packed: [pass][wave][16-k step][block][lane][8]
+  const float* bias;  // [W^T rows] or null
+  const float* scale; // [n] or null
+  const void* res;    // [m][ldr] (RDT) or null
+  void* c;            // [m][ldc] bf16 / fp32
+  int64_t m, n, lda, ldr, ldc;
+  int nch, npass, tiles, per_xcd;
+  int c_dt, act;
+  float out_scale, slope;
+};
+
+// RDT: residual dtype (-1: none); NCH: 64-k chunks (K / 64). The K loop is unrolled: with a
+// run-time trip count the compiler's own wait insertion could not count the loads issued between
+// a register's load and its use across the loop edge and drained every load before each chunk's
+// first MFMA (vmcnt(0)), which undid the prefetch.
+template <bool GATE, int RDT, int NCH>
+__global__ void __launch_bounds__(WS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+wstream_kernel(const WsP p) {
+  constexpr int NO = GATE ? 256 : 512;                    // output channels per pass
+  constexpr int RB = ws_res_row_bytes(GATE, RDT);         // residual bytes per row
+  constexpr int CPW = RB / 128;                           // residual copies per wave (64 RB / 1 KiB / 8)
+  constexpr int RSZ = RDT == DT_F32 ? 4 : 2;
+  constexpr int RPC = CPW <= NCH ? 1 : (CPW <= 2 * NCH ? 2 : (CPW <= 4 * NCH ? 4 : 8));  // copies per chunk
+  static_assert(CPW == 0 || (CPW % RPC == 0 && RPC * NCH >= CPW), "residual copies spread over the chunks");
+  constexpr int nch = NCH;
+  // Without a residual the A tile stays resident: chunks 0 .. 3 are copied in the prologue and
+  // chunks c + 4, c + 5 in every even iteration c, so a barrier (to see the other waves' copies)
+  // is needed only at even chunks. A barrier per chunk made every chunk wait for the slowest
+  // wave's weight loads; larger batches held up the weight loads behind them (the wait counts
+  // are in issue order).
+  constexpr bool RESIDENT = RDT < 0;
+  constexpr int ABYTES = ws_a_bytes(RDT, NCH);
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  float* tb = reinterpret_cast<float*>(lds + ABYTES + WS_P * RB);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int b = blockIdx.x;
+  const int lin = (b & 7) * p.per_xcd + (b >> 3);
+  if (lin >= p.tiles) return;  // before any LDS or memory traffic
+  const int pt = lin / p.npass, ps = lin - pt * p.npass;
+  const int64_t q0 = (int64_t)pt * WS_P;
+  const int64_t och = (int64_t)ps * NO;  // first output channel of the pass
+
+  // ---- A chunk c (8 KiB): wave w copies rows 8 w .. 8 w + 7, lane l row 8 w + l / 8, slot l % 8
+  const int arow = wave * 8 + (lane >> 3);
+  int64_t aq = q0 + arow;
+  if (aq > p.m - 1) aq = p.m - 1;  // rows past M: any valid row, never stored
+  const unsigned char* asrc = (const unsigned char*)(p.a + aq * p.lda) + m32_swz(arow, lane & 7) * 16;
+  auto issue_a = [&](int c) __attribute__((always_inline)) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(asrc + c * 128),
+                                     (__attribute__((address_space(3))) void*)(lds + (RESIDENT ? c : c % WS_STAGES) * WS_STAGE + wave * 1024),
+                                     16, 0, 0);
+  };
+  // ---- residual copy i of this wave: LDS bytes [1 KiB g, +1 KiB) of the rows, g = CPW w + i;
+  // lane l lands at byte 1 KiB g + 16 l = row r, slot s, holding the row's 16-byte unit s ^ (r % 8)
+  auto issue_res = [&](int c) __attribute__((always_inline)) {
+    if constexpr (RDT >= 0) {
+#pragma unroll
+      for (int j = 0; j < RPC; ++j) {
+        const int i = c * RPC + j;
+        if (i < CPW) {
+          const int off = (wave * CPW + i) * 1024 + lane * 16;
+          const int r = off / RB, s = (off % RB) / 16;
+          int64_t rq = q0 + r;
+          if (rq > p.m - 1) rq = p.m - 1;
+          const unsigned char* src =
+              (const unsigned char*)p.res + (rq * p.ldr + och) * RSZ + (s ^ (r & 7)) * 16;
+          __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                           (__attribute__((address_space(3))) void*)(lds + ABYTES + (wave * CPW + i) * 1024),
+                                           16, 0, 0);
+        }
+      }
+    }
+  };
+  // ---- W^T group c (k 64 c .. 64 c + 63): 4 16-k steps x 2 blocks of this wave's 64 rows
+  const unsigned char* wsrc =
+      (const unsigned char*)p.wp + (((int64_t)ps * WS_WAVES + wave) * (nch * 4) * 2 * 64 + lane) * 16;
+  bf16x8 wf[3][4][2];
+  auto load_w = [&](int buf, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+        wf[buf][ks][rb] = *reinterpret_cast<const bf16x8*>(wsrc + ((int64_t)(4 * c + ks) * 2 + rb) * 1024);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
+
+  // prologue: the tables (direct copies into LDS: bias of the pass's 512 W^T rows, then scale of
+  // its output channels; 1 for a missing scale, 0 for a missing bias), A chunks 0 and 1, W^T
+  // groups 0 and 1
+  {
+    const int64_t brow = GATE ? (wave < 4 ? och + 64 * wave : p.n + och + 64 * (wave - 4)) : och + 64 * wave;
+    if (p.bias)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.bias + brow + lane),
+                                       (__attribute__((address_space(3))) void*)(tb + 64 * wave), 4, 0, 0);
+    else
+      tb[tid] = 0.f;
+    if (64 * wave < NO) {
+      if (p.scale)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.scale + och + 64 * wave + lane),
+                                         (__attribute__((address_space(3))) void*)(tb + 512 + 64 * wave), 4, 0, 0);
+      else
+        tb[512 + tid] = 1.f;
+    }
+  }
+  asm volatile("" ::: "memory");
+  issue_a(0);
+  issue_a(1);
+  if constexpr (RESIDENT) {
+    issue_a(2);
+    issue_a(3);
+  }
+  asm volatile("" ::: "memory");
+  load_w(0, 0);
+  asm volatile("" ::: "memory");
+  load_w(1, 1);
+
+  // chunk c from ring stage c % 3 and register buffer buf; with `next`, W^T group c + 2 is loaded
+  // into buffer (buf + 2) % 3 two fragments per 16-k step, between the MFMAs, so that the vector
+  // memory unit drains the workgroup's loads while the matrix cores run (issued all at once after
+  // the barrier, the last wave's MFMAs started only once the others' loads had been accepted)
+  auto chunk = [&](const int buf, const int c, const bool next) __attribute__((always_inline)) {
+    const unsigned char* st = lds + (RESIDENT ? c : c % WS_STAGES) * WS_STAGE;
+    const int nb = (buf + 2) % 3;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 af[2];
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb) {
+        const int r = pb * 32 + l32;
+        af[pb] = *reinterpret_cast<const bf16x8*>(st + r * 128 + m32_swz(r, 2 * ks + hl) * 16);
+      }
+      if (next) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          wf[nb][ks][rb] = *reinterpret_cast<const bf16x8*>(wsrc + ((int64_t)(4 * (c + 2) + ks) * 2 + rb) * 1024);
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf[buf][ks][rb], af[pb], acc[pb][rb]);
+    }
+  };
+  // Ring: iteration c issues A chunk c + 2, the residual copies of chunk c and W^T group c + 2, in
+  // this order. Resident A: iteration c issues its A batch (if any), then W^T group c + 2. At the
+  // top of iteration c A chunk c and W^T group c (W^T issued in iteration c - 2 after that A) must
+  // have landed: still allowed outstanding is everything iteration c - 1 issued.
+  auto res_copies = [&](int j) __attribute__((always_inline)) {
+    return (RDT >= 0 && j >= 0 && j * RPC < CPW) ? RPC : 0;
+  };
+  auto batch_lo = [&](int c) __attribute__((always_inline)) { return c + 4 < NCH ? c + 4 : NCH; };
+  auto batch_hi = [&](int c) __attribute__((always_inline)) {
+    return c % 2 != 0 ? batch_lo(c) : (c + 6 < NCH ? c + 6 : NCH);
+  };
+  auto batch_n = [&](int c) __attribute__((always_inline)) {
+    return c >= 0 && c % 2 == 0 && batch_hi(c) > batch_lo(c) ? batch_hi(c) - batch_lo(c) : 0;
+  };
+  auto step = [&](const int buf, const int c) __attribute__((always_inline)) {
+    if (c == 0) {
+      wait_vmcnt<8>();  // W^T group 1 outstanding (the tables and A chunks 0, 1 came before group 0)
+    } else if constexpr (RESIDENT) {
+      // the copies issued after W^T group c (exact after unrolling: 0, 1, 2 + 0 or 8)
+      const int n = batch_n(c - 1) + (c + 1 < nch ? 8 : 0);
+      if (n >= 10) wait_vmcnt<10>();
+      else if (n >= 9) wait_vmcnt<9>();
+      else if (n >= 8) wait_vmcnt<8>();
+      else if (n >= 2) wait_vmcnt<2>();
+      else if (n >= 1) wait_vmcnt<1>();
+      else wait_vmcnt<0>();
+    } else {
+      // the largest allowed count that does not exceed the copies issued after W^T group c
+      const int n = res_copies(c - 1) + (c + 1 < nch ? 9 : 0);
+      if (n >= 9 + RPC) wait_vmcnt<9 + RPC>();
+      else if (n >= 9) wait_vmcnt<9>();
+      else if (n >= RPC) wait_vmcnt<RPC>();
+      else wait_vmcnt<0>();
+    }
+    // ring: every wave's share of A chunk c, and chunk c - 1 read by all (its stage is refilled);
+    // resident: every wave's share of the chunks up to the next batch
+    if (!RESIDENT || c % 2 == 0) barrier_keep_vm();
+    asm volatile("" ::: "memory");
+    const bool next = c + 2 < nch;
+    if constexpr (RESIDENT) {
+#pragma unroll
+      for (int j = batch_lo(c); j < batch_hi(c); ++j) issue_a(j);
+    } else {
+      if (next) issue_a(c + 2);
+    }
+    issue_res(c);
+    asm volatile("" ::: "memory");
+    chunk(buf, c, next);
+  };
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) step(c % 3, c);
+
+  // ---- epilogue in the MFMA layout: block (pb, rb), lane (l32, hl): pixel pb * 32 + l32; pass
+  // channel c0 = 64 wave + 32 rb + 16 hl (gate: 32 wave + 16 hl, both blocks) .. c0 + 15
+  wait_vmcnt<0>();
+  barrier_keep_vm();  // every residual row and the tables in LDS
+#pragma unroll
+  for (int pb = 0; pb < 2; ++pb) {
+    const int px = pb * 32 + l32;
+    const int64_t q = q0 + px;
+#pragma unroll
+    for (int rb = 0; rb < (GATE ? 1 : 2); ++rb) {
+      const int c0 = GATE ? wave * 32 + hl * 16 : wave * 64 + rb * 32 + hl * 16;
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(tb + (GATE ? c0 : c0) + 4 * i);
+        if constexpr (GATE) {
+          const f32x4 b2 = *reinterpret_cast<const f32x4*>(tb + 256 + c0 + 4 * i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+        }
+      }
+      if (p.act == ACT_GELU) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = gelu_erf(v[j]);
+      } else if (p.act == ACT_LRELU) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = v[j] >= 0.f ? v[j] : v[j] * p.slope;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 s = *reinterpret_cast<const f32x4*>(tb + 512 + c0 + 4 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * i + e] *= s[e] * p.out_scale;
+      }
+      if constexpr (RDT == DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int u = (c0 >> 2) + i;
+          const f32x4 r = *reinterpret_cast<const f32x4*>(lds + ABYTES + px * RB + (u ^ (px & 7)) * 16);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * i + e] += r[e];
+        }
+      } else if constexpr (RDT == DT_BF16) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int u = (c0 >> 3) + i;
+          const u32x4 r = *reinterpret_cast<const u32x4*>(lds + ABYTES + px * RB + (u ^ (px & 7)) * 16);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[8 * i + 2 * e] += __uint_as_float(r[e] << 16);
+            v[8 * i + 2 * e + 1] += __uint_as_float(r[e] & 0xffff0000u);
+          }
+        }
+      }
+      if (q < p.m) {
+        const int64_t o = q * p.ldc + och + c0;
+        if (p.c_dt == DT_BF16) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            f32x8 ov;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ov.v[i] = v[8 * h + i];
+            *reinterpret_cast<bf16x8*>((unsigned char*)p.c + (o + 8 * h) * 2) = pack_bf16(ov);
+          }
+        } else {
+          float* op = reinterpret_cast<float*>(p.c) + o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            reinterpret_cast<f32x4*>(op)[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+        }
+      }
+    }
+  }
+}
+
+template <bool GATE, int RDT, int NCH>
+void launch(const WsP& p, hipStream_t s) {
+  constexpr int lds = ws_lds_bytes(GATE, RDT, NCH);
+  auto fn = &wstream_kernel<GATE, RDT, NCH>;
+  static const bool attr = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL(fn, dim3((unsigned)(8 * p.per_xcd)), dim3(WS_THREADS), lds, s, p);
+}
+
+template <bool GATE, int RDT>
+void launch_k(const WsP& p, hipStream_t s) {
+  if (p.nch == 4) launch<GATE, RDT, 4>(p, s);
+  else if (p.nch == 8) launch<GATE, RDT, 8>(p, s);
+  else launch<GATE, RDT, 16>(p, s);
+}
+
+}  // namespace
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(a != nullptr && a->a && wp && a->c, "gemm_wp: null operand");
+  const bool gate = a->gate != 0;
+  const int64_t nw = gate ? 2 * a->n : a->n;
+  CLARUS_REQUIRE(a->m > 0 && a->n > 0 && nw % 512 == 0 && (a->k == 256 || a->k == 512 || a->k == 1024),
+                 "gemm_wp: W^T rows a multiple of 512, K = 256, 512 or 1024 (N=%lld K=%lld gate=%d)",
+                 (long long)a->n, (long long)a->k, (int)gate);
+  CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16 && (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
+                 "gemm_wp: bf16 A and W, bf16 / fp32 output");
+  CLARUS_REQUIRE(a->res == nullptr || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_wp: bf16 / fp32 residual");
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
+                     (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
+                 "gemm_wp: plain rows (no prologue, batch or pixel shuffle)");
+  const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
+  CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
+                 "gemm_wp: 16-byte A rows and packed weight");
+  CLARUS_REQUIRE(a->ldc >= a->n && (a->ldc * ec) % 16 == 0 && aligned(a->c, 16), "gemm_wp: 16-byte output rows");
+  if (a->res) {
+    const int rs = a->r_dtype == DT_BF16 ? 2 : 4;
+    CLARUS_REQUIRE(a->ldr >= a->n && (a->ldr * rs) % 16 == 0 && aligned(a->res, 16), "gemm_wp: 16-byte residual rows");
+  }
+  const int64_t ptiles = cdiv(a->m, WS_P), npass = nw / 512;
+  CLARUS_REQUIRE(ptiles * npass < ((int64_t)1 << 30), "gemm_wp: too many tiles");
+  WsP p{};
+  p.a = (const bf16_t*)a->a; p.wp = wp; p.bias = a->bias; p.scale = a->scale; p.res = a->res; p.c = a->c;
+  p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
+  p.nch = (int)(a->k / 64); p.npass = (int)npass; p.tiles = (int)(ptiles * npass);
+  p.per_xcd = (int)cdiv(p.tiles, 8);
+  p.c_dt = a->c_dtype; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
+  const int rdt = a->res ? a->r_dtype : -1;
+  note_kernel("wstream_kernel gate=%d res=%d k=%lld", (int)gate, rdt, (long long)a->k);
+  hipStream_t s = (hipStream_t)stream;
+  if (gate) {
+    if (rdt == DT_F32) launch_k<true, DT_F32>(p, s);
+    else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, s);
+    else launch_k<true, -1>(p, s);
+  } else {
+    if (rdt == DT_F32) launch_k<false, DT_F32>(p, s);
+    else if (rdt == DT_BF16) launch_k<false, DT_BF16>(p, s);
+    else launch_k<false, -1>(p, s);
+  }
+  return check_launch("gemm_wp");
+}

@@ -83,6 +83,13 @@ class HipOps(Backend):
     # streamed into registers, the residual staged in LDS during the first GEMM); False keeps it on
     # clarus_hip_gemm_ln_gemm (the first GEMM's weights staged through LDS).
     pair_w1p = True
+    # Plain bf16 GEMMs with K = 256, 512 or 1024 (>= wstream_min_k) and W^T rows a multiple of 512 on
+    # clarus_hip_gemm_wp (W^T packed once per weight and streamed from L2 into registers, the
+    # residual staged in LDS during the K loop); False keeps them on clarus_hip_gemm.
+    wstream = True
+    wstream_min_k = 256
+    wstream_min_tiles = 200  # (64-pixel tile, 512-row pass) workgroups: fewer leave CUs idle
+    wstream_gate_only = False
     # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
@@ -163,7 +170,7 @@ class HipOps(Backend):
     def _gemm(self, what, *, a, wt, c, m, n, k, lda, ldc, bias=None, scale=None, res=None, ldr=0,
               gate=False, act=0, pro=0, a_mode=0, c_mode=0, batch=1, a_bs=0, w_bs=0, c_bs=0, r_bs=0,
               small=None, geom=(0, 0, 0, 0, 0, 0), m2=None, ldm2=0, lnw=None, lnb=None, m2_act=0,
-              ln_eps=1e-6, out_scale=1.0, tile=0):
+              ln_eps=1e-6, out_scale=1.0, tile=0, wp=None):
         h, w, oh, ow, pt, pl = geom
         stats = None
         if (pro & 0xff) in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1:
@@ -180,8 +187,21 @@ class HipOps(Backend):
             m2_dtype=_lib.dtype_code(m2.dtype) if m2 is not None else 0,
             h=h, w=w, oh=oh, ow=ow, pt=pt, pl=pl, pro=pro, a_mode=a_mode, c_mode=c_mode, gate=int(gate),
             act=act, m2_act=m2_act, ln_eps=ln_eps, out_scale=out_scale, slope=0.0, tile=tile)
-        _lib.check(self.lib.clarus_hip_gemm(ctypes.byref(args), self._stream(a)), what)
+        if wp is not None:  # the same GEMM with W^T also packed (clarus_hip_gemm_wp)
+            _lib.check(self.lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(), self._stream(a)), what)
+        else:
+            _lib.check(self.lib.clarus_hip_gemm(ctypes.byref(args), self._stream(a)), what)
         return c
+
+    def _wp_for(self, a, w, k, nout, gate, act, m):
+        """W^T packed for clarus_hip_gemm_wp when this plain bf16 GEMM goes to it, else None."""
+        nw = (2 if gate else 1) * nout
+        if not (self.wstream and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+                and k >= self.wstream_min_k and k in (256, 512, 1024) and nw % 512 == 0
+                and act in (0, _lib.ACT_GELU) and (gate or not self.wstream_gate_only)
+                and -(-m // 64) * (nw // 512) >= self.wstream_min_tiles):
+            return None
+        return self._w2p(w, bool(gate))
 
     # ------------------------------------------------------------------ GEMMs
     def _linear_plan(self, x, w, bias, ln, act, gate, scale, residual, mul, out_dtype):
@@ -251,20 +271,22 @@ class HipOps(Backend):
             rows = self._prologue_rows(x, pro, sm, geom, ln_eps, m, k)
             kk = rows.shape[1]
             wt = self._wt2(w) if self.prologue_split else self._wt(w)
-            return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, **epi)
+            wp = None if self.prologue_split else self._wp_for(rows, w, kk, nout, gate, epi["act"], m)
+            return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, wp=wp, **epi)
         if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.round_short_prologue and not self.prologue_split:
             pro |= _lib.PRO_ROUND
+        wp = self._wp_for(x, w, k, nout, gate, epi["act"], m) if pro == _lib.PRO_NONE else None
         return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
-                          small=sm, geom=geom, ln_eps=float(ln_eps), **epi)
+                          small=sm, geom=geom, ln_eps=float(ln_eps), wp=wp, **epi)
 
     # ---- a residual GEMM and the LayerNorm GEMM on its output (linear_ln_linear)
     def _w2p(self, w2: torch.Tensor, gate: bool) -> torch.Tensor:
-        """[512, n2w] weight -> W^T in the MFMA fragment order of clarus_hip_gemm_ln_gemm
-        ([pass][wave][16-k step][block][lane][8], the rows of a block permuted so a lane
-        accumulates 16 consecutive channels)."""
+        """[K, n2w] weight -> W^T in the MFMA fragment order of clarus_hip_gemm_ln_gemm and
+        clarus_hip_gemm_wp ([pass][wave][16-k step][block][lane][8], the rows of a block permuted so
+        a lane accumulates 16 consecutive channels)."""
         def pack(t):
-            wt = t.t().contiguous()  # [n2w, 512]
-            n2w = wt.shape[0]
+            wt = t.t().contiguous()  # [n2w, K]
+            n2w, kk = wt.shape
             dv = wt.device
             wv = torch.arange(8, device=dv).view(1, 8, 1, 1)
             b = torch.arange(2, device=dv).view(1, 1, 2, 1)
@@ -272,8 +294,8 @@ class HipOps(Backend):
             j = 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3)
             pas = torch.arange(n2w // 512, device=dv).view(-1, 1, 1, 1)
             rows = (b * (n2w // 2) + 256 * pas + 32 * wv + j) if gate else (512 * pas + 64 * wv + 32 * b + j)
-            f = wt[rows]                                          # [pass, w, b, l32, 512]
-            f = f.view(n2w // 512, 8, 2, 32, 32, 2, 8)            # k = 16 s + 8 hl + e
+            f = wt[rows]                                          # [pass, w, b, l32, K]
+            f = f.view(n2w // 512, 8, 2, 32, kk // 16, 2, 8)      # k = 16 s + 8 hl + e
             return f.permute(0, 1, 4, 2, 5, 3, 6).contiguous()    # [pass, w, s, b, hl, l32, e]
         return self.cached(w2, "w2p_gate" if gate else "w2p", pack)
 

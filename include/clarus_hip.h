@@ -116,6 +116,19 @@ typedef struct ClarusGemmArgs {
 int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
 
 /*
+ * clarus_hip_gemm for plain bf16 rows (a_mode rows, pro none, batch 1, c_mode rows) with bf16 W,
+ * K = 256, 512 or 1024 and W^T rows (n, or 2 n with gate) a multiple of 512, with W^T
+ * also passed packed: wp holds it in the fragment order of clarus_hip_gemm_ln_gemm's w2p (K
+ * columns instead of 512: for pass P, wave w, 16-k step s (0 .. K / 16 - 1), block b, lane l, the
+ * 8 values W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e], with gate2 = gate).
+ * args->wt is not read. Epilogue as clarus_hip_gemm: bias (SimpleGate), act (none / GELU /
+ * leaky ReLU), scale * out_scale, bf16 / fp32 residual, bf16 / fp32 output.
+ * replaces kernels/gemm.py:353-400 fused_gemm for those shapes (the weight packed once per
+ * weight by the host, as the reference's ops cache their transposed weights)
+ */
+int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream);
+
+/*
  * Prologue pass of the split-operand GEMM path. Applies the prologue of args (pro = LN, RMS
  * or the TLC map multiply, with its eps / map geometry; a, lda, m, k, a_dtype) to every row in
  * fp32 and writes out[r] = [hi(0..k) | lo(0..k)], bf16, 2k elements per row, hi = bf16(v),

@@ -72,6 +72,19 @@ def test_validation_rejects_before_launch(lib):
     a.r_dtype = _lib.F32
     assert lib.clarus_hip_gemm_ln_gemm_w1p(ctypes.byref(a), 16, 1e-6, 0, 16, None, 16, 768, 1, None) == _lib.EINVAL
     assert b"n2w" in lib.clarus_hip_last_error()
+    a = _lib.GemmArgs(a=16, c=16, m=10, n=512, k=384, batch=1, lda=384, ldc=512, a_dtype=_lib.BF16,
+                      w_dtype=_lib.BF16, c_dtype=_lib.BF16)
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # K not 256 / 512 / 1024
+    assert b"K = 256, 512 or 1024" in lib.clarus_hip_last_error()
+    a.k, a.lda, a.n, a.ldc = 512, 512, 256, 256
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # 256 W^T rows
+    a.gate = 1
+    a.pro = _lib.PRO_LN
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # a prologue
+    assert b"plain rows" in lib.clarus_hip_last_error()
+    a.pro, a.a_dtype = 0, _lib.F32
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 A
+    assert b"bf16 A" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
 

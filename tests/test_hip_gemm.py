@@ -236,6 +236,87 @@ def test_m32_kernel_epilogues(gate, k, tile, hip_bf16):
     check(out.cpu(), ref, f"32x32 DMA GEMM tile {tile} gate={gate} K{k}")
 
 
+@pytest.mark.parametrize("gate,k,nout,rdt,odt,act,m", [
+    (False, 512, 512, torch.float32, torch.float32, None, 1000),
+    (True, 256, 256, None, torch.bfloat16, None, 64 * 9 + 1),
+    (True, 1024, 512, torch.bfloat16, torch.bfloat16, None, 700),
+    (False, 256, 1024, None, torch.bfloat16, "gelu", 130),
+    (False, 1024, 512, torch.float32, torch.bfloat16, None, 64),
+    (True, 512, 256, torch.float32, torch.float32, None, 333),
+])
+def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wp (W^T streamed from L2 into registers, packed by
+    HipOps._w2p): K = 256 / 512 / 1024, one or two 512-row passes, SimpleGate, GELU, no / bf16 /
+    fp32 residual (staged in LDS during the K loop), bf16 / fp32 output, out_scale, a ragged last
+    64-pixel tile, and bias / scale left out in one case. Held to the fp32 oracle: bf16 products
+    are exact in fp32, so an fp32 output matches to summation order and a bf16 one to its
+    rounding."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(36 + k + m)
+    nw = 2 * nout if gate else nout
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    w = rnd(g, k, nw, scale=k ** -0.5, dtype=torch.bfloat16)
+    plain = act == "gelu"  # the GELU case also runs without bias and scale
+    b = None if plain else rnd(g, nw)
+    sc = None if plain else rnd(g, nout)
+    res = None if rdt is None else rnd(g, m, nout).to(rdt)
+    out_scale = 0.5 if k == 1024 else 1.0
+    ref = REF.linear(x, w, b, gate=gate, act=act, scale=None if sc is None else sc * out_scale, residual=res)
+    if plain and out_scale != 1.0:
+        ref = ref * out_scale
+    xd, wd, bd, sd, rd = dev(x, w, b, sc, res)
+    wp = hip_bf16._w2p(wd, gate)
+    assert wp.numel() == k * nw
+    out = torch.empty(m, nout, device="cuda", dtype=odt)
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=0, c=out.data_ptr(), bias=_lib.ptr(bd), scale=_lib.ptr(sd),
+                         res=_lib.ptr(rd), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout, ldr=nout,
+                         a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+                         r_dtype=_lib.dtype_code(rdt) if rdt is not None else 0, gate=int(gate),
+                         act=_lib.ACT_GELU if act == "gelu" else 0, out_scale=out_scale)
+    _lib.check(lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "gemm_wp")
+    assert _lib.last_kernel().startswith("wstream_kernel"), _lib.last_kernel()
+    what = f"gemm_wp gate={gate} K{k} N{nout} res={rdt} out={odt} act={act} M{m}"
+    if odt == torch.float32:
+        assert_fp32(out.cpu(), ref, rel=1e-5, what=what)
+    else:
+        check(out.cpu(), ref, what)
+
+
+@pytest.mark.parametrize("case", ["c512 expand+gate", "c512 c->c+scale+res", "c1024 expand+gate", "c1024 c->c+scale+res"])
+def test_linear_wstream_routing(case, hip_bf16):
+    """HipOps.linear on the config-2 long-K shapes: the expands and the 225-tile c512 c->c run on
+    clarus_hip_gemm_wp, the 114-tile c1024 c->c stays on clarus_hip_gemm (wstream_min_tiles), and
+    the result matches clarus_hip_gemm's (HipOps.wstream = False): bit-identical for bf16 outputs
+    (the same bf16 products summed in fp32, then one rounding) up to summation order, fp32 ones
+    to summation order."""
+    from clarus_amd import _lib, workloads as wl
+    from clarus_amd.hip_ops import HipOps
+    c = next(c for c in wl.config2_cases(hip_bf16, "cuda", levels=(512, 1024)) if c.name == case)
+    saved = HipOps.wstream
+    try:
+        HipOps.wstream = True
+        y1 = c.run()
+        k1 = _lib.last_kernel()
+        HipOps.wstream = False
+        y0 = c.run()
+        k0 = _lib.last_kernel()
+    finally:
+        HipOps.wstream = saved
+    assert k1.startswith("wstream_kernel") == (case != "c1024 c->c+scale+res"), k1
+    assert not k0.startswith("wstream_kernel"), k0
+    fp32 = y0.dtype == torch.float32
+    y0, y1 = y0.float().cpu(), y1.float().cpu()
+    d = (y0 - y1).abs()
+    if fp32:
+        assert (d <= 1e-5 * (y0.abs() + 1.0)).all(), d.max().item()
+    else:
+        assert (d <= bf16_ulp(y0)).all() and (d > 0).float().mean().item() <= 0.01, d.max().item()
+
+
 @pytest.mark.parametrize("adt,wdt,gate,rdt,k,nout,batch", [
     (torch.bfloat16, torch.bfloat16, True, None, 64, 64, 1),
     (torch.bfloat16, torch.bfloat16, True, None, 128, 72, 1),
@@ -944,7 +1025,8 @@ def test_config2_nafnet_gemms(c, h, w, hip_bf16):
     the same seeded inputs and calls bench.py times): expand c->2c + bias + SimpleGate and c->c +
     bias + beta * . + residual (fp32 residual / output from level 3, c >= 512). Records the kernel
     each op ran, which must not depend on what ran before (an LN linear in between changes
-    nothing); at c = 512 the c->c op runs the 32x32 DMA kernel, as in the benchmark's profile."""
+    nothing); at c = 512 the c->c op runs the weight-streaming kernel (clarus_hip_gemm_wp), as in
+    the benchmark's profile."""
     from clarus_amd import workloads as wl
     expand, cc = wl.config2_cases(hip_bf16, "cuda", levels=(c,))
     d = expand.cpu
@@ -961,4 +1043,4 @@ def test_config2_nafnet_gemms(c, h, w, hip_bf16):
     assert [wl.kernel_of(expand), wl.kernel_of(cc)] == kernels
     print(f"[config2] c{c}: expand -> {kernels[0]}; c->c -> {kernels[1]}")
     if c == 512:
-        assert kernels[1].startswith("gemm_mfma32_kernel gate=0"), kernels[1]
+        assert kernels[1].startswith("wstream_kernel gate=0 res=0"), kernels[1]
