@@ -132,6 +132,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
 }
 
+// The same with a range of nbytes: loads at or past it read 0 and stores there are dropped, while
+// every lane still issues the instruction (so vmcnt counts it whatever the row)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const void* p, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)nbytes, 0x00020000);
+}
+
 // exact-erf GELU (torch.nn.functional.gelu default)
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));

@@ -58,6 +58,7 @@ struct PairP {
   float eps, out_scale;
 };
 
+template <bool CF32, bool GATE>
 __global__ void __launch_bounds__(PR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 pair_kernel(const PairP p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -68,6 +69,29 @@ pair_kernel(const PairP p) {
   const int64_t t = blockIdx.x;
   const int64_t q0 = t * PR_P;
   if (q0 >= p.m) return;  // before any LDS or memory traffic
+
+  // ---- the packed weights into this XCD's L2 first. Every workgroup reads all of W1 and W2 and
+  // they run in step, so from a cold cache each 64-k group would miss at once in all of them, one
+  // group ahead of its use. Workgroups go to the XCDs in turn (XCD = block % 8), so the ~28 on an
+  // XCD each touch one 128-byte line in 28 of W1 | W2 (at most two per thread; at 720p one). These are
+  // the kernel's first memory operations: the first chunk's wait covers them, and the value is
+  // only consumed at the end (a dependency the compiler keeps without waiting earlier).
+  unsigned int touch[2];
+  {
+    typedef const __attribute__((address_space(1))) unsigned int* gptr;
+    const int xcd = blockIdx.x % 8;
+    const int slot = blockIdx.x / 8, nslot = (int)((gridDim.x - xcd + 7) / 8);
+    const int lines1 = PR_K * PR_N * 2 / 128, lines = lines1 + PR_K * p.n2w * 2 / 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // two lines per thread at most (the index clamped: no branch)
+      int l = (slot + i * nslot) * PR_THREADS + tid;
+      l = l < lines ? l : lines - 1;
+      const unsigned char* src = l < lines1 ? (const unsigned char*)p.w1p + (int64_t)l * 128
+                                            : (const unsigned char*)p.w2p + (int64_t)(l - lines1) * 128;
+      touch[i] = *(gptr)(src);
+    }
+  }
+  asm volatile("" ::: "memory");
 
   // ---- copies. A chunk c (8 KiB): wave w moves rows 8 w .. 8 w + 7, lane l row 8 w + l / 8,
   // slot l % 8 with source unit m32_swz(row, slot). Residual row r (2 KiB, two 1 KiB copies): wave
@@ -159,18 +183,18 @@ pair_kernel(const PairP p) {
   }
 
   // ---- epilogue in the MFMA layout: block (pb, rb), lane (l32, hl): pixel pb * 32 + l32,
-  // channels 64 wave + 32 rb + 16 hl .. + 15 (element j = channel + j)
+  // channels 64 wave + 32 rb + 16 hl .. + 15 (element j = channel + j). y stays in registers
+  // (yv) and is stored during the second GEMM: stored here, every workgroup's 128 KiB would
+  // leave at once and the waves would wait on the write burst before the row statistics.
   wait_vmcnt<0>();
   barrier_keep_vm();  // every residual row in LDS; the tables too
-  const int ec = p.c_dt == DT_BF16 ? 2 : 4;
+  float yv[2][2][16];
 #pragma unroll
   for (int pb = 0; pb < 2; ++pb) {
     const int px = pb * 32 + l32;
-    const int64_t q = q0 + px;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       const int c0 = wave * 64 + rb * 32 + hl * 16;
-      float v[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 b = *reinterpret_cast<const f32x4*>(tb + c0 + 4 * i);
@@ -182,30 +206,15 @@ pair_kernel(const PairP p) {
         for (int e = 0; e < 4; ++e) {
           float t = (acc[pb][rb][4 * i + e] + b[e]) * s[e];
           asm volatile("" : "+v"(t));
-          v[4 * i + e] = t + r[e];
+          yv[pb][rb][4 * i + e] = t + r[e];
         }
       }
-      if (p.c_dt == DT_BF16) {  // the rows are normalised from the stored (rounded) values
+      if constexpr (!CF32) {  // the rows are normalised from the stored (rounded) values
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          f32x8 o;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o.v[i] = v[8 * h + i];
-          const bf16x8 ob = pack_bf16(o);
-          if (q < p.m) *reinterpret_cast<bf16x8*>((unsigned char*)p.c + (q * p.ldc + c0 + 8 * h) * 2) = ob;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[8 * h + i] = (float)ob[i];
-        }
-      } else if (q < p.m) {
-        float* op = reinterpret_cast<float*>((unsigned char*)p.c + (q * p.ldc + c0) * 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) reinterpret_cast<f32x4*>(op)[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+        for (int j = 0; j < 16; ++j) yv[pb][rb][j] = (float)(bf16_t)yv[pb][rb][j];
       }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[pb][rb][j] = v[j];
     }
   }
-  (void)ec;
 
   // ---- row statistics over the 512 channels, two passes as the reference: a lane's 32 values
   // in order, its pair lane (hl), the 8 waves in order through LDS
@@ -221,7 +230,7 @@ pair_kernel(const PairP p) {
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const float d = pass == 0 ? acc[pb][rb][j] : acc[pb][rb][j] - mean[pb];
+          const float d = pass == 0 ? yv[pb][rb][j] : yv[pb][rb][j] - mean[pb];
           s += pass == 0 ? d : d * d;
         }
       s += __shfl_xor(s, 32, 64);
@@ -250,7 +259,7 @@ pair_kernel(const PairP p) {
       for (int h = 0; h < 2; ++h) {
         f32x8 o;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o.v[i] = (acc[pb][rb][8 * h + i] - mean[pb]) * rstd[pb];
+        for (int i = 0; i < 8; ++i) o.v[i] = (yv[pb][rb][8 * h + i] - mean[pb]) * rstd[pb];
         const int u = (c0 >> 3) + h;
         *reinterpret_cast<bf16x8*>(lds + PR_ROWS + px * (PR_N * 2) + (u ^ (px & 15)) * 16) = pack_bf16(o);
       }
@@ -264,12 +273,46 @@ pair_kernel(const PairP p) {
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
   // ---- second GEMM: 8 waves x 64 W2^T rows per 512-row pass, A fragments from the LN rows, W2
-  // fragments from L2 into registers one 64-k group ahead
+  // fragments from L2 into registers one 64-k group ahead. The stores of this tile (y during
+  // pass 0, each pass's out2 during the next pass) are spread over the groups, after the next
+  // group's loads: the compiler's vmcnt waits before a group's MFMAs then leave them in flight
+  // for two groups. Nothing in the loop branches around a memory instruction (the counts the
+  // compiler derives at a join are those of the path with the fewest, which would wait for
+  // every store): the stores are buffer stores bounded to the tile's valid rows (rows past M are
+  // dropped by the range check), the look-ahead group index is clamped, and bias2 is read
+  // through a range of 0 bytes when absent (zeros).
   int lane_f = lane, wave_f = wave;
   asm volatile("" : "+v"(lane_f), "+v"(wave_f));
   const int l32f = lane_f & 31, hlf = lane_f >> 5;
   const int npass = p.n2w / 512;
   const int total = npass * 8;  // 64-k groups
+  constexpr int EC = CF32 ? 4 : 2;
+  const int rows_ok = (int)(p.m - q0 < PR_P ? p.m - q0 : PR_P);
+  const __amdgpu_buffer_rsrc_t yr = buf_rsrc_n((unsigned char*)p.c + q0 * p.ldc * EC, (uint32_t)(rows_ok * p.ldc * EC));
+  const __amdgpu_buffer_rsrc_t ur =
+      buf_rsrc_n((unsigned char*)p.out2 + q0 * p.ld2 * 2, (uint32_t)(rows_ok * p.ld2 * 2));
+  const __amdgpu_buffer_rsrc_t br = buf_rsrc_n(p.bias2, p.bias2 ? (uint32_t)(p.n2w * 4) : 0u);
+  // y store s of this lane: fp32, 16 of 16 bytes (block s / 4, elements 4 (s % 4) ..); bf16, 8 of
+  // 16 bytes (block s / 2, elements 8 (s % 2) ..)
+  constexpr int NY = CF32 ? 16 : 8;
+  auto store_y = [&](const int s) __attribute__((always_inline)) {
+    if constexpr (!CF32) {
+      const int blk = s / 2, h = s % 2, pb = blk / 2, rb = blk % 2;
+      const int c0 = wave_f * 64 + rb * 32 + hlf * 16 + 8 * h;
+      f32x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o.v[i] = yv[pb][rb][8 * h + i];
+      const bf16x8 ob = pack_bf16(o);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ob), yr,
+                                             (int)(((pb * 32 + l32f) * p.ldc + c0) * 2), 0, 0);
+    } else {
+      const int blk = s / 4, i = s % 4, pb = blk / 2, rb = blk % 2;
+      const int c0 = wave_f * 64 + rb * 32 + hlf * 16 + 4 * i;
+      const f32x4 v{yv[pb][rb][4 * i], yv[pb][rb][4 * i + 1], yv[pb][rb][4 * i + 2], yv[pb][rb][4 * i + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yr,
+                                             (int)(((pb * 32 + l32f) * p.ldc + c0) * 4), 0, 0);
+    }
+  };
   const unsigned char* W2 = (const unsigned char*)p.w2p + ((int64_t)wave_f * 32 * 2 * 64 + lane_f) * 16;
   bf16x8 wf2[2][4][2];
   auto load_group = [&](int buf, int g) __attribute__((always_inline)) {
@@ -297,32 +340,43 @@ pair_kernel(const PairP p) {
         for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf2[buf][ks][rb], af2[pb], acc[pb][rb]);
     }
   };
-  // pass epilogue: + bias2 (SimpleGate), rounded once to bf16, through the wave's staging in row
-  // order (8 whole 128-byte row pieces per store; 16 of 64 bytes with the gate)
+  // a pass's out2 through the wave's staging in row order (whole 128-byte row pieces; 64 bytes
+  // with the gate): stage() writes the accumulators + bias2 (SimpleGate) rounded once to bf16,
+  // store_u(pass, j) moves row group j (NST of them) to memory
   unsigned char* so = lds + PR_OUT + wave_f * 8192;
-  auto pass_epilogue = [&](const int pass) __attribute__((always_inline)) {
-    const bool gate = p.gate != 0;
-    const int upr = gate ? 4 : 8;
+  constexpr int UPR = GATE ? 4 : 8;  // 16-byte units per staged row
+  constexpr int PPI = 64 / UPR;      // rows per store
+  constexpr int NST = PR_P / PPI;    // stores per pass
+  // this lane's bias2 values of a pass: blocks (rb, i) at channel c0(rb) + 4 i; with the gate
+  // rb = 0 / 1 are the two halves' columns of the same output channels
+  f32x4 bv[2][4];
+  auto chan = [&](const int pass, const int rb) __attribute__((always_inline)) {
+    return GATE ? pass * 256 + wave_f * 32 + 16 * hlf + rb * (p.n2w / 2) : pass * 512 + wave_f * 64 + rb * 32 + 16 * hlf;
+  };
+  auto load_bias = [&](const int pass) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        bv[rb][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(br, (chan(pass, rb) + 4 * i) * 4, 0, 0));
+  };
+  auto stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
       const int px = pb * 32 + l32f;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        if (gate && rb == 1) continue;
-        const int lc = gate ? 16 * hlf : rb * 32 + 16 * hlf;
-        const int c0 = gate ? pass * 256 + wave_f * 32 + lc : pass * 512 + wave_f * 64 + lc;
+      for (int rb = 0; rb < (GATE ? 1 : 2); ++rb) {
+        const int lc = GATE ? 16 * hlf : rb * 32 + 16 * hlf;
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const f32x4 b1 = p.bias2 ? *reinterpret_cast<const f32x4*>(p.bias2 + c0 + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
-          if (gate) {
-            const f32x4 b2 = p.bias2 ? *reinterpret_cast<const f32x4*>(p.bias2 + p.n2w / 2 + c0 + 4 * i)
-                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (GATE) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+            for (int e = 0; e < 4; ++e)
+              v[4 * i + e] = (acc[pb][0][4 * i + e] + bv[0][i][e]) * (acc[pb][1][4 * i + e] + bv[1][i][e]);
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + bv[rb][i][e];
           }
         }
 #pragma unroll
@@ -331,19 +385,9 @@ pair_kernel(const PairP p) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) o.v[i] = v[8 * h + i];
           const int u = lc / 8 + h;
-          *reinterpret_cast<bf16x8*>(so + px * upr * 16 + (u ^ (px & (upr - 1))) * 16) = pack_bf16(o);
+          *reinterpret_cast<bf16x8*>(so + px * UPR * 16 + (u ^ (px & (UPR - 1))) * 16) = pack_bf16(o);
         }
       }
-    }
-    const int ppi = 64 / upr;
-    const int c_base = gate ? pass * 256 + wave_f * 32 : pass * 512 + wave_f * 64;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (j * ppi >= PR_P) break;
-      const int px = j * ppi + lane_f / upr, u = lane_f % upr;
-      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(so + px * upr * 16 + (u ^ (px & (upr - 1))) * 16);
-      const int64_t qq = q0 + px;
-      if (qq < p.m) *reinterpret_cast<bf16x8*>((unsigned char*)p.out2 + (qq * p.ld2 + c_base + u * 8) * 2) = ov;
     }
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -352,21 +396,42 @@ pair_kernel(const PairP p) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
   };
-  // groups in pairs (register buffers by constant index); vmcnt(8): the next group's 8 loads
-  // outstanding means this group has landed (loads and stores complete in issue order)
-  for (int g = 0; g < total; g += 2) {
-    load_group(1, g + 1);
-    wait_vmcnt<8>();
-    group(0, g);
-    if (g + 2 < total) {
-      load_group(0, g + 2);
-      wait_vmcnt<8>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    group(1, g + 1);
-    if ((g + 2) % 8 == 0) pass_epilogue((g + 1) / 8);
+  auto store_u = [&](const int pass, const int j) __attribute__((always_inline)) {
+    const int c_base = GATE ? pass * 256 + wave_f * 32 : pass * 512 + wave_f * 64;
+    const int px = j * PPI + lane_f / UPR, u = lane_f % UPR;
+    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(so + px * UPR * 16 + (u ^ (px & (UPR - 1))) * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ov), ur, (int)((px * p.ld2 + c_base + u * 8) * 2),
+                                           0, 0);
+  };
+  // pass 0: per group, the next group's loads (the index clamped to the last group; before them,
+  // two groups ahead of its use, the pass's bias2), the group's share of the y stores, then its
+  // MFMAs
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j == 6) load_bias(0);
+    load_group((j + 1) & 1, j + 1 < total ? j + 1 : total - 1);
+#pragma unroll
+    for (int s = j * NY / 8; s < (j + 1) * NY / 8; ++s) store_y(s);
+    __builtin_amdgcn_sched_barrier(0);  // the loads and stores go out before the MFMAs
+    group(j & 1, j);
   }
+  stage();
+  // passes 1 .. npass - 1: the previous pass's out2 stores over the first NST groups
+  for (int pass = 1; pass < npass; ++pass) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int g = pass * 8 + j;
+      if (j == 6) load_bias(pass);
+      load_group((j + 1) & 1, g + 1 < total ? g + 1 : total - 1);
+      if (j < NST) store_u(pass - 1, j);
+      __builtin_amdgcn_sched_barrier(0);
+      group(j & 1, g);
+    }
+    stage();
+  }
+#pragma unroll
+  for (int j = 0; j < NST; ++j) store_u(npass - 1, j);
+  asm volatile("" ::"v"(touch[0]), "v"(touch[1]));
 }
 
 }  // namespace
@@ -405,13 +470,15 @@ extern "C" int clarus_hip_gemm_ln_gemm_w1p(const ClarusGemmArgs* a, const void* 
   p.m = a->m; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc; p.ld2 = gate2 ? n2w / 2 : n2w;
   p.c_dt = a->c_dtype; p.rms = rms; p.gate = gate2; p.n2w = (int)n2w;
   p.eps = eps; p.out_scale = a->out_scale;
+  note_kernel("pair_kernel gate=%d c=%s", (int)gate2, a->c_dtype == DT_F32 ? "fp32" : "bf16");
+  auto kern = a->c_dtype == DT_F32 ? (gate2 ? pair_kernel<true, true> : pair_kernel<true, false>)
+                                   : (gate2 ? pair_kernel<false, true> : pair_kernel<false, false>);
   static const bool attr = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pair_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              PR_LDS);
+    for (auto k : {pair_kernel<true, true>, pair_kernel<true, false>, pair_kernel<false, true>, pair_kernel<false, false>})
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, PR_LDS);
     return true;
   }();
   (void)attr;
-  note_kernel("pair_kernel gate=%d", (int)gate2);
-  hipLaunchKernelGGL(pair_kernel, dim3((unsigned)cdiv(a->m, PR_P)), dim3(PR_THREADS), PR_LDS, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a->m, PR_P)), dim3(PR_THREADS), PR_LDS, (hipStream_t)stream, p);
   return check_launch("gemm_ln_gemm_w1p");
 }

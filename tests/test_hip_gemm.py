@@ -668,7 +668,8 @@ def test_linear_ln_linear_rows_path(hip_bf16):
 
 
 @pytest.mark.parametrize("gate2,n2w,ln,res_dt", [(True, 1024, True, torch.float32), (False, 1024, True, torch.float32),
-                                                 (True, 512, "rms", torch.bfloat16), (False, 512, True, None)])
+                                                 (True, 512, "rms", torch.bfloat16), (False, 512, True, None),
+                                                 (True, 512, "rms", torch.float32), (False, 512, True, torch.float32)])
 def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
     """clarus_hip_gemm_ln_gemm / clarus_hip_gemm_ln_gemm_w1p (HipOps.linear_ln_linear) against the
     same two GEMMs run apart (clarus_hip_gemm_ln_rows, then a GEMM on the rows it wrote). The first
@@ -733,20 +734,26 @@ def test_linear_ln_linear_fused(gate2, n2w, ln, res_dt, hip_bf16):
     assert bool((du <= bound).all()), f"u vs oracle: {int((du > bound).sum())} beyond the bound, max {du.max():.3e}"
 
 
-@pytest.mark.parametrize("gate2,odt,m", [(True, torch.float32, 1230), (False, torch.bfloat16, 64 * 40 + 7)])
-def test_linear_ln_linear_w1p_vs_pair(gate2, odt, m, hip_bf16):
+@pytest.mark.parametrize("gate2,odt,m,n2w,with_b2", [(True, torch.float32, 1230, 1024, True),
+                                                    (False, torch.bfloat16, 64 * 40 + 7, 1024, True),
+                                                    (True, torch.float32, 640, 512, False),
+                                                    (False, torch.float32, 64 * 3 + 33, 1536, False)])
+def test_linear_ln_linear_w1p_vs_pair(gate2, odt, m, n2w, with_b2, hip_bf16):
     """The two fused pair kernels on the same fp32-residual operands: clarus_hip_gemm_ln_gemm_w1p
     (HipOps.pair_w1p, W1 packed and streamed through registers) and clarus_hip_gemm_ln_gemm (W1
     from LDS). y: the same fp32 products in the same order, bit-identical. u: the LayerNorm
     statistics are summed in another order, so it agrees within one bf16 rounding step except at
     a few elements (at most 1e-3) where a row element rounded to the neighbouring bf16 value and u
-    is small. bf16 y and an M that ends in a 7-pixel tile are the second case."""
+    is small. bf16 y and an M that ends in a 7-pixel tile are the second case; one 512-column pass
+    (the look-ahead group index clamped) and three passes, both without bias2, the others."""
     from clarus_amd import _lib
     from clarus_amd.hip_ops import HipOps
     g = gen(48)
     x = rnd(g, 1, 1, m, 512, dtype=torch.bfloat16).cuda()
     w3, b3 = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 512).cuda()
-    w4, b4 = rnd(g, 512, 1024, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 1024).cuda()
+    w4, b4 = rnd(g, 512, n2w, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, n2w).cuda()
+    if not with_b2:
+        b4 = None
     beta = rnd(g, 512).cuda()
     inp = (2 + rnd(g, 1, 1, m, 512)).cuda()
     saved = HipOps.pair_w1p
