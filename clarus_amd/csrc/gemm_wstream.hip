@@ -90,6 +90,27 @@ wstream_kernel(const WsP p) {
   const int b = blockIdx.x;
   const int lin = (b & 7) * p.per_xcd + (b >> 3);
   if (lin >= p.tiles) return;  // before any LDS or memory traffic
+
+  // ---- the packed weight into this XCD's L2 first, when it fits comfortably (<= 2 MiB): the
+  // XCD's workgroups read it all, in step, so from a cold cache each 64-k group would miss in all
+  // of them at once. The per_xcd workgroups of an XCD each touch one 128-byte line in per_xcd (at
+  // most two per thread; the index clamped, and line 0 only for a larger weight: no branch).
+  // These are the kernel's first memory operations (the first chunk's wait covers them); the
+  // values are consumed only at the end.
+  unsigned int touch[2];
+  {
+    typedef const __attribute__((address_space(1))) unsigned int* gptr;
+    const int64_t wbytes = (int64_t)p.npass * 512 * p.nch * 64 * 2;
+    const bool on = wbytes <= ((int64_t)2 << 20);
+    const int lines = (int)(wbytes / 128), slot = b >> 3;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int l = (slot + i * p.per_xcd) * WS_THREADS + tid;
+      l = !on ? 0 : (l < lines ? l : lines - 1);
+      touch[i] = *(gptr)((const unsigned char*)p.wp + (int64_t)l * 128);
+    }
+  }
+  asm volatile("" ::: "memory");
   const int pt = lin / p.npass, ps = lin - pt * p.npass;
   const int64_t q0 = (int64_t)pt * WS_P;
   const int64_t och = (int64_t)ps * NO;  // first output channel of the pass
@@ -330,6 +351,7 @@ wstream_kernel(const WsP p) {
       }
     }
   }
+  asm volatile("" ::"v"(touch[0]), "v"(touch[1]));
 }
 
 template <bool GATE, int RDT, int NCH>
