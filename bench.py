@@ -85,7 +85,8 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
     """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: the launches from
     the first intro kernel (intro_mfma_kernel / intro_kernel, the NAFNet stem) on, cut into forwards
     at each intro kernel, each forward classed by its call pattern (paired linear_ln_linear ops when
-    it launches gemm_rowln_kernel<true>, else the reference block), grouped by (kernel, grid) and
+    it launches a fused pair kernel, pair_kernel or gemm_rowln_kernel<true>, else the reference
+    block), grouped by (kernel, grid) and
     divided by the number of forwards of that pattern."""
     files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
@@ -110,7 +111,8 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
         forwards[-1] = last[:ends[-1] + 1]
     patterns = {"paired linear_ln_linear ops": [], "reference block (five linear calls)": []}
     for fw in forwards:
-        fused = any("gemm_rowln_kernel<true>" in r.get("Kernel_Name", "") for r in fw)
+        fused = any("gemm_rowln_kernel<true>" in r.get("Kernel_Name", "") or "pair_kernel" in r.get("Kernel_Name", "")
+                    for r in fw)
         patterns["paired linear_ln_linear ops" if fused else "reference block (five linear calls)"].append(fw)
     for pat, fws in patterns.items():
         if not fws:

@@ -1,0 +1,401 @@
+// Short-K bf16 GEMM with the weight resident in registers, persistent over pixel tiles:
+// clarus_hip_gemm_wr (gfx950).
+//
+// y = act(A W^T + bias (SimpleGate: the product of both halves)) * scale * out_scale (+ residual)
+// for plain bf16 rows A [m][K], K = 128 or 256, with W^T passed packed in the fragment order of
+// clarus_hip_gemm_wp (passes of 512 W^T rows; with the gate each half padded to 256 rows, without
+// it the rows padded to a multiple of 512, the padding zero).
+//
+// Why: at K <= 256 a 64-pixel tile is only 1 - 2 us of MFMA work, and the tile kernels spend
+// as long again waiting for their first chunk and writing their output (NAFNet level 2 / config-2
+// c256: 900 single-tile workgroups ran in four rounds of ~6 us, of which the K loop was 2 us).
+//
+// One workgroup of 8 waves per CU (persistent), one 512-row W^T pass per workgroup: wave w keeps
+// the pass's W^T rows 64 w .. 64 w + 63 for all of K in registers (K / 16 steps x 2 blocks of
+// 32 rows, 64 or 128 VGPRs), loaded once, and computes 64 pixels x those 64 rows per tile (2 x 2
+// blocks of 32x32x16 MFMAs). Waves whose rows are all padding skip the products and stores.
+//   * A tiles (64 rows x K, 16 / 32 KiB) travel global -> LDS by direct copies into two buffers:
+//     the next tile's copies are issued at the top of a tile, so they land during its K loop and
+//     epilogue. A rows are 2K bytes with their 16-byte units XOR-swizzled by row % 16 (the 16
+//     lanes reading one unit of 16 consecutive rows hit distinct bank groups);
+//   * the tile's residual (64 pixels x the pass's output channels, <= 64 KiB) is copied into LDS
+//     at the top of the tile and read by the epilogue;
+//   * epilogue in the MFMA layout (a lane holds 16 consecutive output channels of one pixel) with
+//     buffer stores bounded to the tile's valid rows, so every wave issues the same number of
+//     stores and the wait at the next tile's top can leave them in flight.
+// Workgroups go to the XCDs in turn (XCD = block % 8); each XCD owns a contiguous range of pixel
+// tiles and its workgroups split into the passes, so an A tile is fetched into one L2 for all of
+// its passes. Memory waits are explicit vmcnt counts (copies, loads and stores complete in issue
+// order for the counter).
+// replaces kernels/gemm.py:353-400 (fused_gemm) for these shapes
+#include "capi.hpp"
+#include "gemm_mfma32.hpp"
+
+namespace clarus {
+
+namespace {
+
+constexpr int WR_P = 64, WR_WAVES = 8, WR_THREADS = 64 * WR_WAVES;
+constexpr int WR_TB_FLOATS = 1024;  // bias of the pass's 512 W^T rows, scale of its outputs
+
+__host__ __device__ constexpr int wr_res_row_bytes(int rc, int rdt) {
+  return rdt < 0 ? 0 : rc * (rdt == DT_F32 ? 4 : 2);
+}
+// A buffers: two (the next tile's copies land during the current tile)
+__host__ __device__ constexpr int wr_nbuf(int) { return 2; }
+__host__ __device__ constexpr int wr_lds_bytes(int k, int rc, int rdt) {
+  return wr_nbuf(rdt) * WR_P * k * 2 + WR_P * wr_res_row_bytes(rc, rdt) + WR_TB_FLOATS * 4;
+}
+static_assert(wr_lds_bytes(256, 256, DT_F32) <= 160 * 1024 && wr_lds_bytes(256, 512, DT_BF16) <= 160 * 1024 &&
+                  wr_lds_bytes(256, 0, -1) <= 160 * 1024, "LDS");
+
+struct WrP {
+  const bf16_t* a;    // [m][lda]
+  const void* wp;     // W^T packed: [pass][wave][16-k step][block][lane][8]
+  const float* bias;  // [n] or [2 n] with the gate, or null
+  const float* scale; // [n] or null
+  const void* res;    // [m][ldr] or null
+  void* c;            // [m][ldc]
+  int64_t m, n, lda, ldr, ldc;
+  int npass, ptiles, act;
+  float out_scale, slope;
+};
+
+// GATE: SimpleGate pairs (256 output channels per pass); RDT: residual dtype (-1 none); CDT:
+// output dtype; K: 128 or 256; RC: residual channels staged per row (256, or 512 without the gate)
+template <bool GATE, int RDT, int CDT, int K, int RC>
+__global__ void __launch_bounds__(WR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+wres_kernel(const WrP p) {
+  constexpr int KS = K / 16;                 // 16-k steps
+  constexpr int ROWB = K * 2;                // bytes per A row in LDS
+  constexpr int ABYTES = WR_P * ROWB;        // one A buffer
+  constexpr int NA = ABYTES / 1024 / WR_WAVES;  // A copies per wave (2 or 4)
+  constexpr int NO = GATE ? 256 : 512;       // output channels per pass
+  constexpr int RSZ = RDT == DT_F32 ? 4 : 2;
+  constexpr int RB = wr_res_row_bytes(RC, RDT);
+  constexpr int NR = RDT < 0 ? 0 : WR_P * RB / 1024 / WR_WAVES;  // residual copies per wave
+  constexpr int OES = CDT == DT_F32 ? 4 : 2;
+  constexpr int NS = 2 * (GATE ? 1 : 2) * (16 * OES / 16);  // 16-byte stores per lane per tile
+  static_assert(RDT < 0 || (WR_P * RB) % (1024 * WR_WAVES) == 0, "residual copies per wave");
+  static_assert(RDT < 0 || RC >= NO || !GATE, "the gate stages all 256 channels");
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  constexpr int NBUF = wr_nbuf(RDT);
+  unsigned char* rbuf = lds + NBUF * ABYTES;
+  float* tb = reinterpret_cast<float*>(rbuf + WR_P * RB);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- which pass and tiles: XCD x = block % 8 owns pixel tiles [x T / 8, (x + 1) T / 8); its
+  // workgroups j = block / 8 split into the passes (j % npass) and walk the range with stride R
+  const int nblk = (int)gridDim.x;
+  const int x = blockIdx.x & 7, j = blockIdx.x >> 3, J = nblk >> 3;
+  const int pass = j % p.npass, R = J / p.npass, r0 = j / p.npass;
+  if (r0 >= R) return;  // a leftover workgroup (J not a multiple of npass), before any memory traffic
+  const int t_lo = (int)((int64_t)x * p.ptiles / 8), t_hi = (int)((int64_t)(x + 1) * p.ptiles / 8);
+  const int t_first = t_lo + r0;
+  if (t_first >= t_hi) return;
+  const int64_t och = (int64_t)pass * NO;  // first output channel of the pass
+  // waves whose 64 W^T rows (32 output channels with the gate) are all padding
+  const bool active = (GATE ? och + 32 * wave : och + 64 * wave) < p.n;
+  const bool scaled = p.scale != nullptr || p.out_scale != 1.f;  // else the scale table is all 1
+
+  // ---- this wave's W^T fragments of the pass, all of K, into registers
+  bf16x8 wf[KS][2];
+  {
+    const unsigned char* wsrc = (const unsigned char*)p.wp + (((int64_t)pass * WR_WAVES + wave) * KS * 2 * 64 + lane) * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) wf[s][b] = *reinterpret_cast<const bf16x8*>(wsrc + ((int64_t)s * 2 + b) * 1024);
+  }
+  asm volatile("" ::: "memory");
+
+  // ---- copies. A tile t into buffer bf: copy g = NA w + i moves LDS bytes [1 KiB g, +1 KiB):
+  // lane l lands at row (1024 g + 16 l) / ROWB, slot s, and holds the row's unit s ^ (row % 16)
+  auto issue_a = [&](int t, int bf, int lane, int wave) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int off = (wave * NA + i) * 1024 + lane * 16;
+      const int row = off / ROWB, s = (off % ROWB) / 16;
+      int64_t q = (int64_t)t * WR_P + row;
+      if (q > p.m - 1) q = p.m - 1;  // rows past M: any valid row, never stored
+      const unsigned char* src = (const unsigned char*)(p.a + q * p.lda) + (s ^ (row & 15)) * 16;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(lds + bf * ABYTES + (wave * NA + i) * 1024),
+                                       16, 0, 0);
+    }
+  };
+  // residual of tile t: row r, slot s holds the row's unit s ^ (r % 8)
+  auto issue_r = [&](int t, int lane, int wave) __attribute__((always_inline)) {
+    if constexpr (RDT >= 0) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int off = (wave * NR + i) * 1024 + lane * 16;
+        const int row = off / RB, s = (off % RB) / 16;
+        int64_t q = (int64_t)t * WR_P + row;
+        if (q > p.m - 1) q = p.m - 1;
+        const unsigned char* src = (const unsigned char*)p.res + (q * p.ldr + och) * RSZ + (s ^ (row & 7)) * 16;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(rbuf + (wave * NR + i) * 1024),
+                                         16, 0, 0);
+      }
+    }
+  };
+
+  f32x16 acc[2][2];
+  issue_a(t_first, 0, lane, wave);
+  // ---- tables (after the W^T loads and the first copies, so the three latencies overlap): bias of the pass's W^T rows (gate: the first halves' 256, then the second
+  // halves'), scale of its output channels (1 for none, 0 bias for none; 0 past n)
+  {
+    const int c = tid;  // 512 threads, one table entry each
+    const int64_t ch = GATE ? och + (c & 255) : och + c;
+    const int64_t brow = GATE ? (c < 256 ? ch : p.n + ch) : ch;
+    tb[c] = (p.bias && ch < p.n) ? p.bias[brow] : 0.f;
+    if (c < NO) tb[512 + c] = ((p.scale && och + c < p.n) ? p.scale[och + c] : 1.f) * p.out_scale;
+  }
+  // ---- one tile: the products of A(t) from buffer bf into acc, then its epilogue
+  auto kloop = [&](const int bf, const int l32, const int hl) __attribute__((always_inline)) {
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+  if (active) {
+    // A fragments one 16-k step ahead of the MFMAs (the scheduling barriers keep the reads of
+    // later steps from being hoisted, which would take a register per read)
+    const unsigned char* ab = lds + bf * ABYTES;
+    bf16x8 af[2][2];
+    auto read_a = [&](int s, int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb) {
+        const int row = pb * 32 + l32;
+        af[buf][pb] = *reinterpret_cast<const bf16x8*>(ab + row * ROWB + ((2 * s + hl) ^ (row & 15)) * 16);
+      }
+    };
+    read_a(0, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (s + 1 < KS) read_a(s + 1, (s + 1) & 1);
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf[s][rb], af[s & 1][pb], acc[pb][rb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  };
+  auto epilogue = [&](const int t, const int l32, const int hl, const int wave) __attribute__((always_inline)) {
+  // ---- epilogue: block (pb, rb), lane (l32, hl): pixel pb * 32 + l32; pass channel c0 =
+  // 64 wave + 32 rb + 16 hl (gate: 32 wave + 16 hl, both blocks) .. c0 + 15
+  const int64_t q0 = (int64_t)t * WR_P;
+  const int rows_ok = (int)(p.m - q0 < WR_P ? p.m - q0 : WR_P);
+  const int nval = (int)(p.n - och < NO ? p.n - och : NO);  // output channels of the pass
+  const __amdgpu_buffer_rsrc_t cr =
+      buf_rsrc_n((unsigned char*)p.c + (q0 * p.ldc + och) * OES, (uint32_t)((rows_ok - 1) * p.ldc * OES + nval * OES));
+  if (active) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      const int px = pb * 32 + l32;
+#pragma unroll
+      for (int rb = 0; rb < (GATE ? 1 : 2); ++rb) {
+        const int c0 = GATE ? wave * 32 + hl * 16 : wave * 64 + rb * 32 + hl * 16;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 b1 = *reinterpret_cast<const f32x4*>(tb + c0 + 4 * i);
+          if constexpr (GATE) {
+            const f32x4 b2 = *reinterpret_cast<const f32x4*>(tb + 256 + c0 + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+          }
+        }
+        if (p.act == ACT_GELU) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[e] = gelu_erf(v[e]);
+        } else if (p.act == ACT_LRELU) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[e] = v[e] >= 0.f ? v[e] : v[e] * p.slope;
+        }
+        if (scaled) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 s = *reinterpret_cast<const f32x4*>(tb + 512 + c0 + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] *= s[e];
+          }
+        }
+        if constexpr (RDT == DT_F32) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int u = (c0 >> 2) + i;
+            const f32x4 rv = *reinterpret_cast<const f32x4*>(rbuf + px * RB + (u ^ (px & 7)) * 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] += rv[e];
+          }
+        } else if constexpr (RDT == DT_BF16) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int u = (c0 >> 3) + i;
+            const u32x4 rv = *reinterpret_cast<const u32x4*>(rbuf + px * RB + (u ^ (px & 7)) * 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[8 * i + 2 * e] += __uint_as_float(rv[e] << 16);
+              v[8 * i + 2 * e + 1] += __uint_as_float(rv[e] & 0xffff0000u);
+            }
+          }
+        }
+        // rows past M start past the range (ldc >= n); a run past n (the padding of the last
+        // pass) is sent past it too, so every lane still issues every store
+        const bool keep = och + c0 < p.n;
+        const int o = (int)((px * p.ldc + c0) * OES);
+        if constexpr (CDT == DT_BF16) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            f32x8 ov;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ov.v[i] = v[8 * h + i];
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, pack_bf16(ov)), cr,
+                                                   keep ? o + 16 * h : 0x7ffffff0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]}), cr,
+                keep ? o + 16 * i : 0x7ffffff0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one block's temporaries live at a time
+      }
+    }
+  }
+  };
+  // the lane and wave indices laundered per tile: the addresses derived from them are then
+  // recomputed per tile instead of being hoisted out of the loop and held in registers
+  auto fresh = [&](int& ln, int& wv) __attribute__((always_inline)) {
+    ln = threadIdx.x & 63;
+    wv = threadIdx.x >> 6;
+    asm volatile("" : "+v"(ln), "+v"(wv));
+  };
+
+  // One barrier at the top of a tile: every wave's copies of A(t) have landed and every wave is
+  // done with the previous tile (its A buffer, and the residual buffer its epilogue read, are
+  // free). A third A buffer, or the barrier between a tile's products and its epilogue, measured
+  // no faster: the two waves of a SIMD then wait on each other's products instead.
+  int bf = 0;
+  for (int t = t_first; t < t_hi; t += R, bf ^= 1) {
+    int ln, wv;
+    fresh(ln, wv);
+    const int l32 = ln & 31, hl = ln >> 5;
+    const bool has_next = t + R < t_hi;
+    // this wave's copies of A(t) have landed (what was issued after them: the previous tile's
+    // stores; a wave without outputs issues none), then every wave's
+    if (t == t_first || !active) wait_vmcnt<0>();
+    else wait_vmcnt<NS>();
+    barrier_keep_vm();
+    asm volatile("" ::: "memory");
+    issue_r(t, ln, wv);
+    if (has_next) issue_a(t + R, bf ^ 1, ln, wv);
+    asm volatile("" ::: "memory");
+    kloop(bf, l32, hl);
+    // the residual copies (issued before the next tile's A copies) have landed, in every wave
+    if constexpr (RDT >= 0) {
+      if (has_next) wait_vmcnt<NA>();
+      else wait_vmcnt<0>();
+      barrier_keep_vm();
+      asm volatile("" ::: "memory");
+    }
+    epilogue(t, l32, hl, wv);
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <bool GATE, int RDT, int CDT, int K, int RC>
+void launch(const WrP& p, int nblk, hipStream_t s) {
+  constexpr int lds = wr_lds_bytes(K, RC, RDT);
+  auto fn = &wres_kernel<GATE, RDT, CDT, K, RC>;
+  static const bool attr = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblk), dim3(WR_THREADS), lds, s, p);
+}
+
+template <bool GATE, int RDT, int CDT, int RC>
+void launch_k(const WrP& p, int k, int nblk, hipStream_t s) {
+  if (k == 128) launch<GATE, RDT, CDT, 128, RC>(p, nblk, s);
+  else launch<GATE, RDT, CDT, 256, RC>(p, nblk, s);
+}
+
+template <bool GATE, int RDT, int RC>
+void launch_c(const WrP& p, int cdt, int k, int nblk, hipStream_t s) {
+  if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC>(p, k, nblk, s);
+  else launch_k<GATE, RDT, DT_BF16, RC>(p, k, nblk, s);
+}
+
+}  // namespace
+
+}  // namespace clarus
+
+using namespace clarus;
+
+extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void* stream) {
+  clear_error();
+  CLARUS_REQUIRE(a != nullptr && a->a && wp && a->c, "gemm_wr: null operand");
+  const bool gate = a->gate != 0;
+  CLARUS_REQUIRE(a->m > 0 && a->n > 0 && (a->k == 128 || a->k == 256) && a->n % 16 == 0,
+                 "gemm_wr: K = 128 or 256, N a multiple of 16 (N=%lld K=%lld)", (long long)a->n, (long long)a->k);
+  CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16 && (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
+                 "gemm_wr: bf16 A and W, bf16 / fp32 output");
+  CLARUS_REQUIRE(a->res == nullptr || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_wr: bf16 / fp32 residual");
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
+                     (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
+                 "gemm_wr: plain rows (no prologue, batch or pixel shuffle)");
+  const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
+  CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
+                 "gemm_wr: 16-byte A rows and packed weight");
+  CLARUS_REQUIRE(a->ldc >= a->n && (a->ldc * ec) % 16 == 0 && aligned(a->c, 16), "gemm_wr: 16-byte output rows");
+  const int64_t no = gate ? 256 : 512;
+  const int64_t npass = cdiv(a->n, no);
+  int rc = 0;
+  if (a->res) {
+    const int rs = a->r_dtype == DT_BF16 ? 2 : 4;
+    CLARUS_REQUIRE(a->ldr >= a->n && (a->ldr * rs) % 16 == 0 && aligned(a->res, 16), "gemm_wr: 16-byte residual rows");
+    // staged residual rows: 256 channels, or 512 (bf16, no gate, N a multiple of 512)
+    // staged residual rows [och, och + rc) of every pass lie inside [0, n): rc = 256 with the gate
+    // (N a multiple of 256) or for N = 256, else 512 (bf16, N a multiple of 512)
+    rc = (gate || a->n <= 256) ? 256 : 512;
+    CLARUS_REQUIRE(a->n % rc == 0 && (rc == 256 || a->r_dtype == DT_BF16),
+                   "gemm_wr: a residual needs N a multiple of 256 with the gate, N = 256, or a bf16 residual "
+                   "with N a multiple of 512");
+  }
+  const int64_t ptiles = cdiv(a->m, WR_P);
+  CLARUS_REQUIRE(ptiles < ((int64_t)1 << 30) && a->m * a->ldc * ec < ((int64_t)1 << 40), "gemm_wr: too many tiles");
+  CLARUS_REQUIRE((WR_P - 1) * a->ldc * ec + no * ec < ((int64_t)1 << 31), "gemm_wr: output rows too long");
+  const int cus = device_cus();
+  int nblk = 8 * (cus / 8);
+  if (nblk < 8 * (int)npass) nblk = 8 * (int)npass;
+  WrP p{};
+  p.a = (const bf16_t*)a->a; p.wp = wp; p.bias = a->bias; p.scale = a->scale; p.res = a->res; p.c = a->c;
+  p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
+  p.npass = (int)npass; p.ptiles = (int)ptiles; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
+  const int rdt = a->res ? a->r_dtype : -1;
+  note_kernel("wres_kernel gate=%d res=%d k=%lld", (int)gate, rdt, (long long)a->k);
+  hipStream_t s = (hipStream_t)stream;
+  const int k = (int)a->k, cdt = a->c_dtype;
+  if (gate) {
+    if (rdt == DT_F32) launch_c<true, DT_F32, 256>(p, cdt, k, nblk, s);
+    else if (rdt == DT_BF16) launch_c<true, DT_BF16, 256>(p, cdt, k, nblk, s);
+    else launch_c<true, -1, 256>(p, cdt, k, nblk, s);
+  } else {
+    if (rdt == DT_F32) launch_c<false, DT_F32, 256>(p, cdt, k, nblk, s);
+    else if (rdt == DT_BF16 && rc == 512) launch_c<false, DT_BF16, 512>(p, cdt, k, nblk, s);
+    else if (rdt == DT_BF16) launch_c<false, DT_BF16, 256>(p, cdt, k, nblk, s);
+    else launch_c<false, -1, 256>(p, cdt, k, nblk, s);
+  }
+  return check_launch("gemm_wr");
+}

@@ -90,6 +90,11 @@ class HipOps(Backend):
     wstream_min_k = 256
     wstream_min_tiles = 200  # (64-pixel tile, 512-row pass) workgroups: fewer leave CUs idle
     wstream_gate_only = False
+    # Plain bf16 GEMMs with K in wres_ks on clarus_hip_gemm_wr (persistent workgroups, each keeping
+    # its 512-row W^T pass in registers for all of its pixel tiles, the next A tile copied during the
+    # current one); False or other K keep them on the kernels above.
+    wres = True
+    wres_ks = (128, 256)
     # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
@@ -187,21 +192,28 @@ class HipOps(Backend):
             m2_dtype=_lib.dtype_code(m2.dtype) if m2 is not None else 0,
             h=h, w=w, oh=oh, ow=ow, pt=pt, pl=pl, pro=pro, a_mode=a_mode, c_mode=c_mode, gate=int(gate),
             act=act, m2_act=m2_act, ln_eps=ln_eps, out_scale=out_scale, slope=0.0, tile=tile)
-        if wp is not None:  # the same GEMM with W^T also packed (clarus_hip_gemm_wp)
-            _lib.check(self.lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(), self._stream(a)), what)
+        if wp is not None:  # the same GEMM with W^T also packed: ("wp" | "wr", packed weight)
+            fn = self.lib.clarus_hip_gemm_wr if wp[0] == "wr" else self.lib.clarus_hip_gemm_wp
+            _lib.check(fn(ctypes.byref(args), wp[1].data_ptr(), self._stream(a)), what)
         else:
             _lib.check(self.lib.clarus_hip_gemm(ctypes.byref(args), self._stream(a)), what)
         return c
 
-    def _wp_for(self, a, w, k, nout, gate, act, m):
-        """W^T packed for clarus_hip_gemm_wp when this plain bf16 GEMM goes to it, else None."""
+    def _wp_for(self, a, w, k, nout, gate, act, m, res=None):
+        """("wr" | "wp", W^T packed) when this plain bf16 GEMM goes to clarus_hip_gemm_wr /
+        clarus_hip_gemm_wp, else None."""
         nw = (2 if gate else 1) * nout
+        if (self.wres and k in self.wres_ks and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+                and act in (0, _lib.ACT_GELU) and nout % 16 == 0
+                and (res is None or (nout % 256 == 0 if gate else (nout == 256 or (res.dtype == torch.bfloat16
+                                                                                     and nout % 512 == 0))))):
+            return "wr", self._wr_pack(w, bool(gate))
         if not (self.wstream and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
                 and k >= self.wstream_min_k and k in (256, 512, 1024) and nw % 512 == 0
                 and act in (0, _lib.ACT_GELU) and (gate or not self.wstream_gate_only)
                 and -(-m // 64) * (nw // 512) >= self.wstream_min_tiles):
             return None
-        return self._w2p(w, bool(gate))
+        return "wp", self._w2p(w, bool(gate))
 
     # ------------------------------------------------------------------ GEMMs
     def _linear_plan(self, x, w, bias, ln, act, gate, scale, residual, mul, out_dtype):
@@ -271,33 +283,51 @@ class HipOps(Backend):
             rows = self._prologue_rows(x, pro, sm, geom, ln_eps, m, k)
             kk = rows.shape[1]
             wt = self._wt2(w) if self.prologue_split else self._wt(w)
-            wp = None if self.prologue_split else self._wp_for(rows, w, kk, nout, gate, epi["act"], m)
+            wp = None if self.prologue_split else self._wp_for(rows, w, kk, nout, gate, epi["act"], m, residual)
             return self._gemm("linear", a=rows, wt=wt, c=out, m=m, n=nout, k=kk, lda=kk, ldc=nout, wp=wp, **epi)
         if pro != _lib.PRO_NONE and w.dtype == torch.bfloat16 and self.round_short_prologue and not self.prologue_split:
             pro |= _lib.PRO_ROUND
-        wp = self._wp_for(x, w, k, nout, gate, epi["act"], m) if pro == _lib.PRO_NONE else None
+        wp = self._wp_for(x, w, k, nout, gate, epi["act"], m, residual) if pro == _lib.PRO_NONE else None
         return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                           small=sm, geom=geom, ln_eps=float(ln_eps), wp=wp, **epi)
 
     # ---- a residual GEMM and the LayerNorm GEMM on its output (linear_ln_linear)
+    @staticmethod
+    def _frag_pack(t: torch.Tensor, gate: bool) -> torch.Tensor:
+        """[K, n2w] weight (n2w % 512 == 0) -> W^T in the MFMA fragment order of
+        clarus_hip_gemm_ln_gemm, clarus_hip_gemm_wp and clarus_hip_gemm_wr ([pass][wave][16-k step]
+        [block][lane][8], the rows of a block permuted so a lane accumulates 16 consecutive
+        channels; with gate block 0 / 1 of a wave are the two halves' rows of the same channels)."""
+        wt = t.t().contiguous()  # [n2w, K]
+        n2w, kk = wt.shape
+        dv = wt.device
+        wv = torch.arange(8, device=dv).view(1, 8, 1, 1)
+        b = torch.arange(2, device=dv).view(1, 1, 2, 1)
+        i = torch.arange(32, device=dv).view(1, 1, 1, 32)
+        j = 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3)
+        pas = torch.arange(n2w // 512, device=dv).view(-1, 1, 1, 1)
+        rows = (b * (n2w // 2) + 256 * pas + 32 * wv + j) if gate else (512 * pas + 64 * wv + 32 * b + j)
+        f = wt[rows]                                          # [pass, w, b, l32, K]
+        f = f.view(n2w // 512, 8, 2, 32, kk // 16, 2, 8)      # k = 16 s + 8 hl + e
+        return f.permute(0, 1, 4, 2, 5, 3, 6).contiguous()    # [pass, w, s, b, hl, l32, e]
+
     def _w2p(self, w2: torch.Tensor, gate: bool) -> torch.Tensor:
-        """[K, n2w] weight -> W^T in the MFMA fragment order of clarus_hip_gemm_ln_gemm and
-        clarus_hip_gemm_wp ([pass][wave][16-k step][block][lane][8], the rows of a block permuted so
-        a lane accumulates 16 consecutive channels)."""
+        """[K, n2w] weight -> W^T packed (_frag_pack), computed once per weight."""
+        return self.cached(w2, "w2p_gate" if gate else "w2p", lambda t: self._frag_pack(t, gate))
+
+    def _wr_pack(self, w: torch.Tensor, gate: bool) -> torch.Tensor:
+        """[K, N] (gate: [K, 2 N]) weight -> W^T padded for clarus_hip_gemm_wr (gate: each half to a
+        multiple of 256 columns, else to a multiple of 512; zeros), then packed (_frag_pack)."""
         def pack(t):
-            wt = t.t().contiguous()  # [n2w, K]
-            n2w, kk = wt.shape
-            dv = wt.device
-            wv = torch.arange(8, device=dv).view(1, 8, 1, 1)
-            b = torch.arange(2, device=dv).view(1, 1, 2, 1)
-            i = torch.arange(32, device=dv).view(1, 1, 1, 32)
-            j = 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3)
-            pas = torch.arange(n2w // 512, device=dv).view(-1, 1, 1, 1)
-            rows = (b * (n2w // 2) + 256 * pas + 32 * wv + j) if gate else (512 * pas + 64 * wv + 32 * b + j)
-            f = wt[rows]                                          # [pass, w, b, l32, K]
-            f = f.view(n2w // 512, 8, 2, 32, kk // 16, 2, 8)      # k = 16 s + 8 hl + e
-            return f.permute(0, 1, 4, 2, 5, 3, 6).contiguous()    # [pass, w, s, b, hl, l32, e]
-        return self.cached(w2, "w2p_gate" if gate else "w2p", pack)
+            kk, nw = t.shape
+            if gate:
+                n = nw // 2
+                z = t.new_zeros(kk, -(-n // 256) * 256 - n)
+                tp = torch.cat([t[:, :n], z, t[:, n:], z], dim=1)
+            else:
+                tp = torch.cat([t, t.new_zeros(kk, -(-nw // 512) * 512 - nw)], dim=1)
+            return self._frag_pack(tp.contiguous(), gate)
+        return self.cached(w, "wr_gate" if gate else "wr", pack)
 
     def _pair_first(self, x, w, bias, scale, residual, mul, out_dtype, ln):
         """The first GEMM of linear_ln_linear on the LN-rows kernel: (A rows, W^T, output,

@@ -129,6 +129,19 @@ int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
 int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream);
 
 /*
+ * clarus_hip_gemm for plain bf16 rows (a_mode rows, pro none, batch 1, c_mode rows) with bf16 W,
+ * K = 128 or 256 and N a multiple of 16, on a persistent kernel that keeps each workgroup's
+ * 512-row W^T pass in registers for all of its pixel tiles. wp is W^T packed as for
+ * clarus_hip_gemm_wp after padding: with gate each half of W^T padded to a multiple of 256 rows
+ * (n2w = 2 * 256 * ceil(n / 256)), without it W^T padded to a multiple of 512 rows, the padding
+ * zero. A residual (bf16 / fp32) needs n a multiple of 256 with gate, n = 256 without it, or a
+ * bf16 residual with n a multiple of 512. args->wt is not read. Epilogue as clarus_hip_gemm.
+ * replaces kernels/gemm.py:353-400 fused_gemm for those shapes (the weight packed once per
+ * weight by the host, as the reference's ops cache their transposed weights)
+ */
+int clarus_hip_gemm_wr(const ClarusGemmArgs* args, const void* wp, void* stream);
+
+/*
  * Prologue pass of the split-operand GEMM path. Applies the prologue of args (pro = LN, RMS
  * or the TLC map multiply, with its eps / map geometry; a, lda, m, k, a_dtype) to every row in
  * fp32 and writes out[r] = [hi(0..k) | lo(0..k)], bf16, 2k elements per row, hi = bf16(v),

@@ -85,6 +85,15 @@ def test_validation_rejects_before_launch(lib):
     a.pro, a.a_dtype = 0, _lib.F32
     assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 A
     assert b"bf16 A" in lib.clarus_hip_last_error()
+    a = _lib.GemmArgs(a=16, c=16, m=64, n=256, k=512, batch=1, lda=512, ldc=256, a_dtype=_lib.BF16,
+                      w_dtype=_lib.BF16, c_dtype=_lib.BF16)
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # K = 512
+    assert b"K = 128 or 256" in lib.clarus_hip_last_error()
+    a.k, a.lda, a.res, a.ldr, a.r_dtype, a.gate, a.n = 256, 256, 16, 128, _lib.F32, 1, 128
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # gated 128 with a residual
+    assert b"residual" in lib.clarus_hip_last_error()
+    a.gate, a.n, a.ldc, a.ldr = 0, 512, 512, 512
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 residual, 512 outputs
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
 

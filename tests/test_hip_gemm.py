@@ -286,6 +286,59 @@ def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
         check(out.cpu(), ref, what)
 
 
+@pytest.mark.parametrize("gate,k,nout,rdt,odt,act,m", [
+    (True, 256, 256, None, torch.bfloat16, None, 64 * 9 + 1),
+    (True, 128, 128, None, torch.bfloat16, None, 1000),
+    (False, 256, 256, torch.bfloat16, torch.bfloat16, None, 700),
+    (False, 256, 512, None, torch.bfloat16, "gelu", 130),
+    (False, 128, 512, torch.bfloat16, torch.float32, None, 333),
+    (True, 256, 512, torch.float32, torch.float32, None, 64),
+    (False, 256, 1024, None, torch.bfloat16, None, 3000),
+    (False, 128, 96, None, torch.float32, None, 200),
+    (True, 128, 256, torch.bfloat16, torch.float32, None, 64 * 40 + 7),
+])
+def test_gemm_wr_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wr (persistent workgroups with their W^T pass resident in
+    registers, packed and padded by HipOps._wr_pack): K = 128 / 256, SimpleGate, GELU, no / bf16 /
+    fp32 residual, bf16 / fp32 output, out_scale, one to two passes, output widths that leave
+    waves idle (gated 128, plain 96 and 256), a ragged last tile, more tiles than workgroups (3000
+    and 2567 rows), bias / scale left out in one case. Held to the fp32 oracle as
+    clarus_hip_gemm_wp."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(52 + k + m)
+    nw = 2 * nout if gate else nout
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    w = rnd(g, k, nw, scale=k ** -0.5, dtype=torch.bfloat16)
+    plain = act == "gelu"
+    b = None if plain else rnd(g, nw)
+    sc = None if plain else rnd(g, nout)
+    res = None if rdt is None else rnd(g, m, nout).to(rdt)
+    out_scale = 0.5 if k == 128 else 1.0
+    ref = REF.linear(x, w, b, gate=gate, act=act, scale=None if sc is None else sc * out_scale, residual=res)
+    if plain and out_scale != 1.0:
+        ref = ref * out_scale
+    xd, wd, bd, sd, rd = dev(x, w, b, sc, res)
+    wp = hip_bf16._wr_pack(wd, gate)
+    out = torch.full((m, nout), float("nan"), device="cuda", dtype=odt)
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=0, c=out.data_ptr(), bias=_lib.ptr(bd), scale=_lib.ptr(sd),
+                         res=_lib.ptr(rd), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout, ldr=nout,
+                         a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+                         r_dtype=_lib.dtype_code(rdt) if rdt is not None else 0, gate=int(gate),
+                         act=_lib.ACT_GELU if act == "gelu" else 0, out_scale=out_scale)
+    _lib.check(lib.clarus_hip_gemm_wr(ctypes.byref(args), wp.data_ptr(),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "gemm_wr")
+    assert _lib.last_kernel().startswith("wres_kernel"), _lib.last_kernel()
+    what = f"gemm_wr gate={gate} K{k} N{nout} res={rdt} out={odt} act={act} M{m}"
+    assert torch.isfinite(out).all(), what + ": an output element was not written"
+    if odt == torch.float32:
+        assert_fp32(out.cpu(), ref, rel=1e-5, what=what)
+    else:
+        check(out.cpu(), ref, what)
+
+
 @pytest.mark.parametrize("case", ["c512 expand+gate", "c512 c->c+scale+res", "c1024 expand+gate", "c1024 c->c+scale+res"])
 def test_linear_wstream_routing(case, hip_bf16):
     """HipOps.linear on the config-2 long-K shapes: the expands and the 225-tile c512 c->c run on

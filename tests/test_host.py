@@ -239,18 +239,15 @@ def test_nafnet_tlc_windows_known_answer():
 
 @pytest.mark.parametrize("gate", [False, True])
 def test_ln_gemm_weight_packing_matches_header(gate):
-    """HipOps._w2p (torch gather / permute) against the fragment order clarus_hip_gemm_ln_gemm
-    documents in include/clarus_hip.h, evaluated element by element at sampled positions:
+    """HipOps._frag_pack (torch gather / permute; the packing of _w2p and _wr_pack) against the
+    fragment order clarus_hip_gemm_ln_gemm documents in include/clarus_hip.h, evaluated element by
+    element at sampled positions:
     packed[P][w][s][b][l][e] = W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e]."""
     from clarus_amd.hip_ops import HipOps
 
-    class Stub:
-        def cached(self, t, tag, fn):
-            return fn(t)
-
     n2w = 1024
     w = torch.randn(512, n2w, generator=torch.Generator().manual_seed(5))
-    packed = HipOps._w2p(Stub(), w, gate).reshape(-1)
+    packed = HipOps._frag_pack(w, gate).reshape(-1)
     assert packed.numel() == n2w * 512
     wt = w.t()
     rng = np.random.default_rng(0)
@@ -263,6 +260,34 @@ def test_ln_gemm_weight_packing_matches_header(gate):
         assert packed[flat].item() == wt[row, 16 * s + 8 * (l // 32) + e].item()
     # every W^T element lands exactly once
     assert torch.equal(packed.sort().values, w.reshape(-1).sort().values)
+
+
+@pytest.mark.parametrize("gate,n", [(True, 128), (True, 256), (False, 96), (False, 256), (False, 1024)])
+def test_wr_weight_padding(gate, n):
+    """HipOps._wr_pack: the weight padded with zero columns (gate: each half to a multiple of 256,
+    else to a multiple of 512) before the fragment packing, so the packed halves of a gated weight
+    start at row 256 * ceil(n / 256) and the padding rows are zero."""
+    from clarus_amd.hip_ops import HipOps
+
+    class Stub:
+        _frag_pack = staticmethod(HipOps._frag_pack)
+
+        def cached(self, t, tag, fn):
+            return fn(t)
+
+    k = 128
+    w = torch.randn(k, 2 * n if gate else n, generator=torch.Generator().manual_seed(6)) + 3  # no zeros
+    packed = HipOps._wr_pack(Stub(), w, gate)
+    half = -(-n // 256) * 256
+    nw = 2 * half if gate else -(-n // 512) * 512
+    assert packed.numel() == k * nw
+    wt = torch.zeros(nw, k)
+    if gate:
+        wt[:n], wt[half:half + n] = w[:, :n].t(), w[:, n:].t()
+    else:
+        wt[:n] = w.t()
+    assert torch.equal(packed, HipOps._frag_pack(wt.t().contiguous(), gate))
+    assert int((packed == 0).sum()) == k * (nw - (2 * n if gate else n))
 
 
 def test_linear_ln_linear_unfused_is_two_linears():
