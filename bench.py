@@ -22,9 +22,10 @@ Extra fields of the JSON line:
                 timed eagerly behind a GPU spin (back to back, as in the step); the others cold:
                 before each rep a read-only pass over 512 MB (more than the 256 MB MALL) evicts
                 the caches without leaving dirty lines whose write-back would overlap the op.
-  nafnet_e2e    NAFNet-w64 720p bf16 forward in ms (median of graph replays), with the paired
-                residual GEMM -> LayerNorm GEMM op and with the reference's unchanged five-linear
-                block, and the same forward on the oracle on the CPU
+  nafnet_e2e    NAFNet-w64 720p bf16 forward in ms (median of graph replays), with the fused ops
+                (residual GEMM -> LayerNorm GEMM pairs at width 512, the feed-forward half as one op
+                at the other widths) and with the reference's unchanged five-linear block, and the
+                same forward on the oracle on the CPU
 
   python bench.py --summarize-trace DIR   per-(kernel, grid) durations from a rocprofv3 kernel trace
   python bench.py --summarize-e2e DIR     the same for the NAFNet forwards only, per forward
@@ -84,9 +85,9 @@ def summarize_trace(directory: str) -> None:
 def summarize_e2e(directory: str, top: int = 40) -> None:
     """Per-forward kernel time of the NAFNet e2e phase of a bench.py kernel trace: the launches from
     the first intro kernel (intro_mfma_kernel / intro_kernel, the NAFNet stem) on, cut into forwards
-    at each intro kernel, each forward classed by its call pattern (paired linear_ln_linear ops when
-    it launches a fused pair kernel, pair_kernel or gemm_rowln_kernel<true>, else the reference
-    block), grouped by (kernel, grid) and
+    at each intro kernel, each forward classed by its call pattern (the fused ops when it launches
+    a fused pair kernel, pair_kernel or gemm_rowln_kernel<true>, else the reference block),
+    grouped by (kernel, grid) and
     divided by the number of forwards of that pattern."""
     files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
@@ -109,11 +110,11 @@ def summarize_e2e(directory: str, top: int = 40) -> None:
     ends = [i for i, r in enumerate(last) if "conv_halo_kernel<16" in r.get("Kernel_Name", "")]
     if ends:
         forwards[-1] = last[:ends[-1] + 1]
-    patterns = {"paired linear_ln_linear ops": [], "reference block (five linear calls)": []}
+    patterns = {"fused ops (linear_ln_linear, linear_gate_linear)": [], "reference block (five linear calls)": []}
     for fw in forwards:
         fused = any("gemm_rowln_kernel<true>" in r.get("Kernel_Name", "") or "pair_kernel" in r.get("Kernel_Name", "")
                     for r in fw)
-        patterns["paired linear_ln_linear ops" if fused else "reference block (five linear calls)"].append(fw)
+        patterns["fused ops (linear_ln_linear, linear_gate_linear)" if fused else "reference block (five linear calls)"].append(fw)
     for pat, fws in patterns.items():
         if not fws:
             continue
@@ -376,6 +377,7 @@ def main() -> None:
     others = [] if args.no_ops else (wl.config1_cases(hip32, dev) + wl.config3_cases(hip32, dev)
                                      + wl.config4_cases(hip, hip32, dev) + wl.config5_cases(hip, dev)
                                      + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev),
+                                        wl.nafnet_ffn_case(hip, dev),
                                         wl.evssm_scan_case(hip, dev), wl.metrics_case(dev)])
     if args.pmc_pass:  # the last dispatches: two markers, the copy, then a marker before each op and one after
         cases = wl.all_cases(hip, hip32, dev)

@@ -95,11 +95,27 @@ def linear_ln_linear_unfused(self, x, w, bias=None, scale=None, residual=None, m
     return y, self.linear(y, w2, bias2, ln=ln, gate=gate2, ln_eps=ln_eps)
 
 
+def linear_gate_linear_unfused(self, x, w1, b1=None, w2=None, b2=None, scale=None, ln=False, ln_eps=1e-6,
+                               out_dtype=None):
+    """u = linear(x, w1, b1, ln=ln, gate=True) followed by linear(u, w2, b2, scale=scale,
+    residual=x): the feed-forward half of a NAFNet block (conv4 -> SimpleGate -> conv5 scaled by
+    gamma on the block's running sum, python/clarus/models/nafnet/__init__.py:159-161) and the
+    pointwise chain of BASELINE config 1. Returns the second op's output. Backends without a fused
+    kernel run the two ops."""
+    u = self.linear(x, w1, b1, ln=ln, gate=True, ln_eps=ln_eps)
+    return self.linear(u, w2, b2, scale=scale, residual=x, out_dtype=out_dtype)
+
+
+_FUSED_DEFAULTS = {"linear_ln_linear": linear_ln_linear_unfused, "linear_gate_linear": linear_gate_linear_unfused}
+
+
 def give_pair_default(backend_cls) -> None:
-    """Attach linear_ln_linear_unfused to a backend base class that has no linear_ln_linear, so
-    every backend derived from it answers the op with the two linear calls."""
-    if not callable(getattr(backend_cls, "linear_ln_linear", None)):
-        backend_cls.linear_ln_linear = linear_ln_linear_unfused
+    """Attach the unfused defaults (linear_ln_linear_unfused, linear_gate_linear_unfused) to a
+    backend base class that lacks those ops, so every backend derived from it answers them with
+    their linear calls."""
+    for name, fn in _FUSED_DEFAULTS.items():
+        if not callable(getattr(backend_cls, name, None)):
+            setattr(backend_cls, name, fn)
 
 
 give_pair_default(_Backend)
@@ -178,7 +194,7 @@ if _host is not None:
     Ops = _host.Ops
     register_backend = _host.register_backend
     register_backend("hip", "clarus_amd.hip_ops:HipOps")
-    give_pair_default(Backend)  # clarus's Backend has no linear_ln_linear of its own
+    give_pair_default(Backend)  # clarus's Backend has neither fused op of its own
 else:
     Unsupported = _Unsupported
     BackendUnavailable = _BackendUnavailable

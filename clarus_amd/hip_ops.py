@@ -25,7 +25,8 @@ import torch
 
 from . import _lib
 from .dft import dft_matrices
-from .dispatch import Backend, BackendUnavailable, Unsupported, linear_ln_linear_unfused, register_backend
+from .dispatch import (Backend, BackendUnavailable, Unsupported, linear_gate_linear_unfused, linear_ln_linear_unfused,
+                       register_backend)
 from .geometry import box_geometry, is_small, make_small
 
 _KDT = (torch.bfloat16, torch.float32)
@@ -98,6 +99,10 @@ class HipOps(Backend):
     # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
+    # linear_gate_linear (NAFNet's feed-forward half-block and the config-1 chain, an explicit op
+    # the caller asks for) as one kernel (clarus_hip_ffn) for c = 32 / 64 channels with weights of
+    # the activation dtype; False (or other shapes) runs its two linear ops.
+    fuse_ffn = True
     # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
     # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
     round_short_prologue = False
@@ -126,6 +131,7 @@ class HipOps(Backend):
         # launches of the fused pair kernel (clarus_hip_gemm_ln_gemm) and of the LN-rows GEMM
         # (clarus_hip_gemm_ln_rows) made by linear_ln_linear; counters only, never read by the dispatch
         self.pair_launches = {"gemm_ln_gemm": 0, "gemm_ln_rows": 0}
+        self.ffn_launches = 0  # linear_gate_linear calls served by clarus_hip_ffn
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -399,6 +405,66 @@ class HipOps(Backend):
         self.pair_launches["gemm_ln_rows"] += 1
         # the rows are LN(y) rounded once to bf16: what linear(y, ln=...) feeds its GEMM for K = 512
         return y, self.linear(rows, w2, bias2, gate=gate2)
+
+    # ---- the feed-forward half-block (linear_gate_linear)
+    @staticmethod
+    def _ffn_pack1(w1: torch.Tensor) -> torch.Tensor:
+        """w1 [c, 2c] (linear layout) -> clarus_hip_ffn's fragment order:
+        w1p[T][s][l][i] = w1[16 s + 8 (l // 32) + i][32 T + l % 32]."""
+        c = w1.shape[0]
+        dv = w1.device
+        lv = torch.arange(64, device=dv).view(1, 1, 64, 1)
+        t1 = torch.arange(2 * c // 32, device=dv).view(-1, 1, 1, 1)
+        s = torch.arange(c // 16, device=dv).view(1, -1, 1, 1)
+        i = torch.arange(8, device=dv).view(1, 1, 1, 8)
+        return w1[16 * s + 8 * (lv // 32) + i, 32 * t1 + lv % 32].contiguous()
+
+    @staticmethod
+    def _ffn_pack2(w2: torch.Tensor) -> torch.Tensor:
+        """w2 [c, c] (linear layout) -> clarus_hip_ffn's fragment order: w2p[T2][T][l][j] =
+        w2[32 T + 8 (j // 4) + 4 (l // 32) + j % 4][o(T2, l % 32)], o(T2, r) = 32 T2 + 16 (r // 16) +
+        8 ((r // 4) % 2) + 4 ((r // 8) % 2) + r % 4."""
+        c = w2.shape[0]
+        dv = w2.device
+        lv = torch.arange(64, device=dv).view(1, 1, 64, 1)
+        t2 = torch.arange(c // 32, device=dv).view(-1, 1, 1, 1)
+        tg = torch.arange(c // 32, device=dv).view(1, -1, 1, 1)
+        j = torch.arange(16, device=dv).view(1, 1, 1, 16)
+        r = lv % 32
+        o = 32 * t2 + 16 * (r // 16) + 8 * ((r // 4) % 2) + 4 * ((r // 8) % 2) + r % 4
+        return w2[32 * tg + 8 * (j // 4) + 4 * (lv // 32) + j % 4, o].contiguous()
+
+    def linear_gate_linear(self, x, w1, b1=None, w2=None, b2=None, scale=None, ln=False, ln_eps=1e-6,
+                           out_dtype=None):
+        """linear(linear(x, w1, b1, ln=ln, gate=True), w2, b2, scale=scale, residual=x) (the
+        feed-forward half of a NAFNet block; the config-1 chain without LN). One kernel
+        (clarus_hip_ffn) for dense NHWC x with c = 32 or 64 in the backend's dtype, weights of that
+        dtype and an output of it: the gated intermediate stays in registers, rounded as the
+        first linear stores it; with bf16 weights a normalised row is rounded once to bf16 (the
+        reference's in-kernel LayerNorm, kernels/gemm.py:165-175). Otherwise, or with
+        prologue_split, the two linear ops."""
+        c = x.shape[-1] if x.dim() == 4 else 0
+        odt = out_dtype or self.dtype
+        fits = (self.fuse_ffn and c in (32, 64) and x.dtype == self.dtype and odt == x.dtype
+                and ln in (False, True, "rms") and not (ln and self.prologue_split)
+                and w2 is not None and w1.dtype == x.dtype and w2.dtype == x.dtype
+                and tuple(w1.shape) == (c, 2 * c) and tuple(w2.shape) == (c, c)
+                and (b1 is None or tuple(b1.shape) == (2 * c,)) and (b2 is None or tuple(b2.shape) == (c,))
+                and (scale is None or tuple(scale.shape) == (c,))
+                and _dense(x, w1, w2, b1, b2, scale) and _vec16(x))
+        if not fits:
+            return linear_gate_linear_unfused(self, x, w1, b1, w2, b2, scale=scale, ln=ln, ln_eps=ln_eps,
+                                              out_dtype=out_dtype)
+        w1p = self.cached(w1, "ffn1", self._ffn_pack1)
+        w2p = self.cached(w2, "ffn2", self._ffn_pack2)
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        pro = {False: _lib.PRO_NONE, True: _lib.PRO_LN, "rms": _lib.PRO_RMS}[ln]
+        _lib.check(self.lib.clarus_hip_ffn(
+            x.data_ptr(), out.data_ptr(), _lib.dtype_code(x.dtype), w1p.data_ptr(), _lib.ptr(self._bias(b1)),
+            w2p.data_ptr(), _lib.ptr(self._bias(b2)), _lib.ptr(self._bias(scale)), x.numel() // c, c, pro,
+            float(ln_eps), 1.0, self._stream(x)), "linear_gate_linear")
+        self.ffn_launches += 1
+        return out
 
     def down(self, x, w4d, b, out_dtype=None):
         if tuple(w4d.shape[-2:]) != (2, 2) or not _dense(x, b):

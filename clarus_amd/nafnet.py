@@ -91,11 +91,13 @@ class NAFNet:
     def __init__(self, ops, width=64, enc=(1, 1, 1, 28), mid=1, dec=(1, 1, 1, 1), tlc=(256, 256),
                  res_fp32_level=3, seed=0, state_dict=None, fused_pairs=True):
         self.ops = ops
-        # True: each residual GEMM and the LayerNorm GEMM on its output go to ops.linear_ln_linear
-        # (conv3 -> conv4, and conv5 -> the next block's conv1 within a stage), which a backend may
-        # run as one kernel; False: the reference block's five linear calls
-        # (models/nafnet/__init__.py:152-161), unchanged
+        # True: blocks of width pair_width send each residual GEMM and the LayerNorm GEMM on its
+        # output to ops.linear_ln_linear (conv3 -> conv4, and conv5 -> the next block's conv1
+        # within a stage), blocks of other widths their feed-forward half (conv4 -> SimpleGate ->
+        # conv5) to ops.linear_gate_linear; a backend may run each as one kernel. False: the
+        # reference block's five linear calls (models/nafnet/__init__.py:152-161), unchanged
         self.fused_pairs = fused_pairs
+        self.pair_width = 512
         self.dtype = ops.dtype
         self.device = ops.device
         self.width, self.enc, self.mid, self.dec = width, list(enc), mid, list(dec)
@@ -190,6 +192,20 @@ class NAFNet:
         return fn(x, w, bias, scale=scale, residual=residual, mul=mul, out_dtype=out_dtype, w2=w2, bias2=bias2,
                   gate2=gate2, ln=ln)
 
+    def _ffn(self, y, p, level):
+        """ops.linear_gate_linear on the block's running sum y (conv4 with LayerNorm and SimpleGate,
+        then conv5 scaled by gamma on y), or its two linear calls when no backend has the op."""
+        o, w = self.ops, self.w
+        w4, b4, w5, b5 = w[f"{p}.conv4.w"], w[f"{p}.conv4.bias"], w[f"{p}.conv5.w"], w[f"{p}.conv5.bias"]
+        try:
+            fn = o.linear_gate_linear
+        except AttributeError:
+            fn = None
+        if fn is None:
+            u = o.linear(y, w4, b4, ln=True, gate=True)
+            return o.linear(u, w5, b5, scale=w[f"{p}.conv5.scale"], residual=y, out_dtype=self._rdt(level))
+        return fn(y, w4, b4, w5, b5, scale=w[f"{p}.conv5.scale"], ln=True, out_dtype=self._rdt(level))
+
     def _block(self, x, p, level, t=None, nxt=None):
         """One NAFBlock on x. t: its conv1 output when the previous block's fused op already
         computed it. nxt: the next block's key at the same width, whose conv1 (LayerNorm of this
@@ -200,6 +216,10 @@ class NAFNet:
             t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
         t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
         sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
+        if x.shape[-1] != self.pair_width:
+            y = o.linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,
+                         mul=sca, out_dtype=self._rdt(level))
+            return self._ffn(y, p, level), None
         # conv3 (+ residual) and conv4 (LayerNorm of its output, SimpleGate) as one op, which a
         # backend may run as one kernel
         y, u = self._pair(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,
@@ -255,8 +275,9 @@ def bench_forward(dev, reps: int = 20, fused_pairs: bool = True, log=print) -> d
     """NAFNet-GoPro-w64 (NAFNetLocal, enc [1, 1, 1, 28], mid 1, dec [1, 1, 1, 1]) 720p bf16
     forward: GEMM-family ops, depthwise conv and TLC box mean on `hip`, pixel (un)shuffle and
     elementwise adds on torch; captured in a HIP graph after an eager warm-up, median of `reps`
-    event-timed replays. fused_pairs: the harness's paired residual GEMM -> LayerNorm GEMM op
-    (one kernel on `hip`), or the reference block's five linear calls."""
+    event-timed replays. fused_pairs: the harness's fused ops (residual GEMM -> LayerNorm GEMM
+    pairs, the feed-forward half; each one kernel on `hip`), or the reference block's five linear
+    calls."""
     from . import spatial_torch  # noqa: F401  (registers "torch" for the non-GEMM ops)
     from .dispatch import Ops
     ops = Ops(["hip", "torch"], torch.bfloat16, dev, log=lambda *a: None)
@@ -294,7 +315,8 @@ def bench_forward(dev, reps: int = 20, fused_pairs: bool = True, log=print) -> d
     res = {"ms": round(statistics.median(times), 3), "eager_ms": round(statistics.median(eager), 3),
            "reps": reps, "input": "1x3x720x1280 fp32 U(0,1), seeded", "dtype": "bf16",
            "model": "NAFNetLocal w64 enc[1,1,1,28] mid1 dec[1,1,1,1], random init",
-           "block": "paired linear_ln_linear ops" if fused_pairs else "reference block: five linear calls",
+           "block": ("fused ops: linear_ln_linear pairs (width 512), linear_gate_linear (other widths)" if fused_pairs
+                     else "reference block: five linear calls"),
            "served": served, "finite": bool(torch.isfinite(y).all().item())}
     log(f"[bench] NAFNet-w64 720p bf16 forward ({res['block']}): graph {res['ms']} ms, eager {res['eager_ms']} ms")
     return res

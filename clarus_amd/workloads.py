@@ -117,7 +117,9 @@ def config2_cases(hip, device, seed: int = 0, levels=None) -> list[OpCase]:
 
 
 def config1_cases(hip32, device, seed: int = 0) -> list[OpCase]:
-    """fp32 pointwise chain on x [1, 256, 256, 32] (gate op, then scale + residual op)."""
+    """fp32 pointwise chain on x [1, 256, 256, 32]: as two ops (gate op, then scale + residual op;
+    u makes the round trip through HBM: B counts x, u twice, x again and the output) and as one
+    (linear_gate_linear: B = x read once, the output written once)."""
     g = _gen(seed)
     x = torch.randn(1, 256, 256, 32, generator=g)
     w1 = _kaiming_uniform_kn(g, 32, 64)
@@ -133,9 +135,18 @@ def config1_cases(hip32, device, seed: int = 0) -> list[OpCase]:
         r = r or hip32
         uu = r.linear(d[0], d[1], d[2], gate=True)
         return r.linear(uu, d[3], d[4], scale=d[5], residual=d[0])
-    return [OpCase("config1 fp32 chain (gate, scale+res)", 1, "fp32", 2.0 * m * 32 * 64 + 2.0 * m * 32 * 32,
-                   4.0 * m * 32 * 2 + 4.0 * m * 32 * 2 + 4.0 * (32 * 64 + 32 * 32) + 4.0 * (64 + 64), chain,
-                   {"inputs": host}, lambda r: chain(host, r))]
+    def fused(d=d, r=None):
+        from .dispatch import linear_gate_linear_unfused
+        r = r or hip32
+        fn = getattr(r, "linear_gate_linear", None)
+        args = (d[0], d[1], d[2], d[3], d[4])
+        return fn(*args, scale=d[5]) if fn is not None else linear_gate_linear_unfused(r, *args, scale=d[5])
+    flops = 2.0 * m * 32 * 64 + 2.0 * m * 32 * 32
+    wbytes = 4.0 * (32 * 64 + 32 * 32) + 4.0 * (64 + 64)
+    return [OpCase("config1 fp32 chain (gate, scale+res)", 1, "fp32", flops,
+                   4.0 * m * 32 * 2 + 4.0 * m * 32 * 2 + wbytes, chain, {"inputs": host}, lambda r: chain(host, r)),
+            OpCase("config1 fp32 chain, one op (linear_gate_linear)", 1, "fp32", flops, 4.0 * m * 32 * 2 + wbytes,
+                   fused, {"inputs": host}, lambda r: fused(host, r))]
 
 
 def config3_cases(hip32, device, seed: int = 0) -> list[OpCase]:
@@ -257,6 +268,35 @@ def nafnet_pair_case(hip, device, seed: int = 0) -> OpCase:
                   lambda r_: pair(r_, host))
 
 
+def nafnet_ffn_case(hip, device, seed: int = 0) -> OpCase:
+    """The NAFNet-w64 720p level-0 feed-forward half-block as one op (linear_gate_linear: LN ->
+    conv4 64 -> 128 + SimpleGate -> conv5 64 -> 64, * gamma + the block's running sum, bf16),
+    two per forward (encoder and decoder block). M = 921600: F = 2 M 64 (128 + 64);
+    B = 2 M 64 (x) + 2 M 64 (out) + 2 (64 * 128 + 64 * 64) (weights) + 4 (128 + 64 + 64) (vectors)."""
+    g = _gen(seed + 5)
+    m, c = 720 * 1280, 64
+    x = torch.randn(1, 720, 1280, c, generator=g).bfloat16()
+    w4 = _kaiming_uniform_kn(g, c, 2 * c).bfloat16()
+    b4 = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+    w5 = _kaiming_uniform_kn(g, c, c).bfloat16()
+    b5 = torch.rand(c, generator=g) * 0.2 - 0.1
+    gamma = torch.randn(c, generator=g) * 0.1
+    host = dict(x=x, w4=w4, b4=b4, w5=w5, b5=b5, gamma=gamma)
+    d = {n: t.to(device) for n, t in host.items()}
+
+    def run(r_=None, d=d):
+        from .dispatch import linear_gate_linear_unfused
+        be = r_ or hip
+        fn = getattr(be, "linear_gate_linear", None)
+        args = (d["x"], d["w4"], d["b4"], d["w5"], d["b5"])
+        kw = dict(scale=d["gamma"], ln=True)
+        return fn(*args, **kw) if fn is not None else linear_gate_linear_unfused(be, *args, **kw)
+    flops = 2.0 * m * c * (2 * c + c)
+    nbytes = 2.0 * m * c * 2 + 2.0 * (c * 2 * c + c * c) + 4.0 * (2 * c + 2 * c)
+    return OpCase("nafnet L0 LN -> conv4 + gate -> conv5 + res (fused FFN)", 0, "bf16", flops, nbytes, run, host,
+                  lambda r_: run(r_, host))
+
+
 def fftformer_dffn_case(hip, device, seed: int = 0) -> OpCase:
     """FFTformer level-0 DFFN project_in + frequency filter at 720p as one op (linear_patch_filter:
     LayerNorm eps 1e-5 -> 1x1 conv 48 -> 288 + bias -> per-patch rfft2 * filter -> irfft2, bf16),
@@ -332,9 +372,11 @@ def metrics_case(device, seed: int = 0) -> OpCase:
 
 def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
     """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5,
-    the fused FFTformer DFFN op, the fused NAFNet pair, EVSSM's scan and the metrics."""
+    the fused FFTformer DFFN op, the fused NAFNet pair and feed-forward half, EVSSM's scan and the
+    metrics."""
     return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
             + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
             + config5_cases(hip_bf16, device, seed) + [fftformer_dffn_case(hip_bf16, device, seed),
                                                         nafnet_pair_case(hip_bf16, device, seed),
+                                                        nafnet_ffn_case(hip_bf16, device, seed),
                                                         evssm_scan_case(hip_bf16, device, seed), metrics_case(device, seed)])

@@ -142,6 +142,26 @@ int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream)
 int clarus_hip_gemm_wr(const ClarusGemmArgs* args, const void* wp, void* stream);
 
 /*
+ * Fused pointwise feed-forward on dense NHWC rows x [m][c] (c = 32 or 64), one kernel:
+ *   u   = SimpleGate(pro(x) . w1 + b1)          w1 [c][2c]: the product of the two c-halves
+ *   out = x + (u . w2 + b2) * scale * out_scale  w2 [c][c]
+ * pro = CLARUS_PRO_NONE, CLARUS_PRO_LN or CLARUS_PRO_RMS (no affine, eps ln_eps). dtype (bf16 or
+ * fp32) is the type of x, out and both weights; u is rounded to it as a separate GEMM would store
+ * it; with bf16 the normalised row is rounded once to bf16 before the product. b1 [2c], b2 [c],
+ * scale [c]: fp32 or null. out must not overlap x. The weights are passed packed:
+ *   w1p[T][s][l][i]  = w1[16 s + 8 (l / 32) + i][32 T + l % 32]       T < 2c/32, s < c/16, l < 64, i < 8
+ *   w2p[T2][T][l][j] = w2[32 T + 8 (j / 4) + 4 (l / 32) + j % 4][o(T2, l % 32)]     T2, T < c/32, j < 16
+ *   o(T2, r) = 32 T2 + 16 (r / 16) + 8 ((r / 4) % 2) + 4 ((r / 8) % 2) + r % 4
+ * (the host packs each weight once, as the reference's ops cache their transposed weights).
+ * No counterpart in the reference: it composes two `linear` calls (ops/torch_ref.py:103-130 /
+ * ops/triton_cuda.py:84-112), conv4 -> conv5 of the NAFNet block (models/nafnet/__init__.py:
+ * 159-161) and the pointwise benchmark chain, for hosts that run them back to back.
+ */
+int clarus_hip_ffn(const void* x, void* out, int dtype, const void* w1p, const float* b1, const void* w2p,
+                   const float* b2, const float* scale, int64_t m, int64_t c, int pro, float ln_eps,
+                   float out_scale, void* stream);
+
+/*
  * Prologue pass of the split-operand GEMM path. Applies the prologue of args (pro = LN, RMS
  * or the TLC map multiply, with its eps / map geometry; a, lda, m, k, a_dtype) to every row in
  * fp32 and writes out[r] = [hi(0..k) | lo(0..k)], bf16, 2k elements per row, hi = bf16(v),

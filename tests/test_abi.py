@@ -94,6 +94,17 @@ def test_validation_rejects_before_launch(lib):
     assert b"residual" in lib.clarus_hip_last_error()
     a.gate, a.n, a.ldc, a.ldr = 0, 512, 512, 512
     assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 residual, 512 outputs
+    # clarus_hip_ffn: c, dtype, prologue, alignment and overlap are checked before any launch
+    ffn = lib.clarus_hip_ffn
+    assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 128, 1, 1e-6, 1.0, None) == _lib.EINVAL
+    assert b"c = 32 or 64" in lib.clarus_hip_last_error()
+    assert ffn(16, 1 << 20, 7, 16, None, 16, None, None, 64, 64, 1, 1e-6, 1.0, None) == _lib.EINVAL
+    assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 64, 2, 1e-6, 1.0, None) == _lib.EINVAL  # mul
+    assert ffn(16, 1 << 20, _lib.BF16, 24, None, 16, None, None, 64, 64, 1, 1e-6, 1.0, None) == _lib.EINVAL
+    assert b"16-byte" in lib.clarus_hip_last_error()
+    assert ffn(1 << 20, (1 << 20) + 4096, _lib.BF16, 16, None, 16, None, None, 64, 64, 0, 0.0, 1.0, None) == _lib.EINVAL
+    assert b"overlap" in lib.clarus_hip_last_error()
+    assert ffn(None, 16, _lib.F32, 16, None, 16, None, None, 64, 32, 0, 0.0, 1.0, None) == _lib.EINVAL
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
 

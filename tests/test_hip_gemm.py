@@ -1076,6 +1076,108 @@ def test_config1_fp32_chain(hip_f32):
     assert_fp32(y.cpu(), ry, what="config1 chain")
 
 
+def test_config1_fused_chain(hip_f32):
+    """BASELINE config 1 as one op (linear_gate_linear, clarus_hip_ffn): the same chain as
+    test_config1_fp32_chain with the gated intermediate kept on chip, held to the fp32 rule."""
+    from clarus_amd import _lib
+    x, w1, b1, w2, b2, beta = config1_inputs()
+    got = hip_f32.linear_gate_linear(*dev(x, w1, b1, w2, b2), scale=beta.cuda())
+    assert _lib.last_kernel().startswith("ffn_kernel c=32 dt=f32"), _lib.last_kernel()
+    ref = REF.linear(REF.linear(x, w1, b1, gate=True), w2, b2, scale=beta, residual=x)
+    assert_fp32(got.cpu(), ref, what="config1 fused chain")
+
+
+def ffn_oracle(x, w1, b1, w2, b2, sc, ln, round_rows=False, ln_eps=1e-6):
+    """The two linear calls of linear_gate_linear on the oracle, u stored in x's dtype as the first
+    call stores it; round_rows: the normalised rows rounded once to bf16 before the first product
+    (the bf16 kernel's arithmetic, kernels/gemm.py:165-175 in the reference). Returns fp32."""
+    if round_rows:
+        u = REF.linear(_prologue_rows(x, ln=ln, ln_eps=ln_eps).to(torch.bfloat16), w1, b1, gate=True)
+    else:
+        u = REF.linear(x, w1, b1, ln=ln, gate=True, ln_eps=ln_eps)
+    return REF.linear(u.to(x.dtype), w2, b2, scale=sc, residual=x)
+
+
+def check_ffn(got, x, w1, b1, w2, b2, sc, ln, what):
+    """fp32: the fp32 rule against the oracle. bf16: within one bf16 ulp (+ 1e-3 of the output
+    scale for the intermediate's rounding flips) of the oracle with the kernel's roundings
+    emulated, and within 2e-2 of the output scale of the oracle without the row rounding."""
+    if got.dtype == torch.float32:
+        return assert_fp32(got.cpu(), ffn_oracle(x, w1, b1, w2, b2, sc, ln), what=what)
+    g = got.double().cpu()
+    emu = ffn_oracle(x, w1, b1, w2, b2, sc, ln, round_rows=bool(ln)).double()
+    d = (g - emu).abs()
+    slack = bf16_ulp(emu) + 1e-3 * emu.abs().max()
+    assert bool((d <= slack).all()), f"{what}: {int((d > slack).sum())} elements off the emulation; max {d.max():.3e}"
+    ref = ffn_oracle(x, w1, b1, w2, b2, sc, ln).double()
+    scale = max(1.0, ref.abs().max().item())
+    e = (g - ref).abs().max().item()
+    assert e <= BF16_ABS * scale, f"{what}: max|d| {e:.3e} > 2e-2 x {scale:.3g}"
+    return e
+
+
+FFN_CASES = [  # (c, dtype, ln, (n, h, w), with biases and scale)
+    (64, torch.bfloat16, True, (1, 37, 29), True),    # NAFNet level 0 block shape, ragged pixel count
+    (64, torch.bfloat16, "rms", (2, 5, 7), True),     # fewer units than waves
+    (64, torch.bfloat16, False, (1, 3, 11), False),   # no biases / scale, m = 33
+    (32, torch.bfloat16, True, (1, 19, 23), True),
+    (64, torch.float32, True, (1, 33, 31), True),
+    (32, torch.float32, False, (1, 1, 5), False),     # m = 5, one partial unit
+    (64, torch.float32, "rms", (1, 16, 64), True),    # whole units only
+]
+
+
+@pytest.mark.parametrize("c,dt,ln,shape,full", FFN_CASES)
+def test_linear_gate_linear(c, dt, ln, shape, full, hip_bf16, hip_f32):
+    """linear_gate_linear on clarus_hip_ffn: LN / RMS / no prologue, bf16 and fp32, ragged and
+    partial 32-pixel units, optional biases and scale."""
+    from clarus_amd import _lib
+    hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
+    g = gen(40 + c)
+    x = rnd(g, *shape, c, dtype=dt) + (0.5 if ln else 0.0)
+    w1, w2 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=dt), rnd(g, c, c, scale=c ** -0.5, dtype=dt)
+    b1, b2, sc = (rnd(g, 2 * c, scale=0.1), rnd(g, c, scale=0.1), rnd(g, c)) if full else (None, None, None)
+    got = hip.linear_gate_linear(*dev(x, w1, b1, w2, b2), scale=None if sc is None else sc.cuda(), ln=ln)
+    kern = _lib.last_kernel()
+    assert kern.startswith(f"ffn_kernel c={c} dt={'bf16' if dt == torch.bfloat16 else 'f32'}"), kern
+    assert got.dtype == dt and got.shape == x.shape
+    e = check_ffn(got, x, w1, b1, w2, b2, sc, ln, f"ffn c{c} {dt} ln={ln} {shape}")
+    print(f"[ffn] c{c} {dt} ln={ln} {shape}: {kern} max err {e:.3e}")
+
+
+def test_linear_gate_linear_unfused_shapes(hip_bf16):
+    """Shapes clarus_hip_ffn does not take (c = 128, an fp32 output of bf16 activations) run the
+    two linear ops and give the same result class."""
+    from clarus_amd import _lib
+    g = gen(48)
+    for c, odt in ((128, None), (64, torch.float32)):
+        x = rnd(g, 1, 9, 13, c, dtype=torch.bfloat16)
+        w1 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=torch.bfloat16)
+        w2 = rnd(g, c, c, scale=c ** -0.5, dtype=torch.bfloat16)
+        b1, b2, sc = rnd(g, 2 * c, scale=0.1), rnd(g, c, scale=0.1), rnd(g, c)
+        got = hip_bf16.linear_gate_linear(*dev(x, w1, b1, w2, b2), scale=sc.cuda(), ln=True, out_dtype=odt)
+        assert not _lib.last_kernel().startswith("ffn_kernel"), _lib.last_kernel()
+        u = hip_bf16.linear(*dev(x, w1, b1), ln=True, gate=True)
+        want = hip_bf16.linear(u, *dev(w2, b2), scale=sc.cuda(), residual=x.cuda(), out_dtype=odt)
+        assert torch.equal(got, want), f"c{c}: the fallback is the two linear ops"
+
+
+def test_ffn_nafnet_level0_full(hip_bf16):
+    """NAFNet-w64 level 0 at 720p (x [1, 720, 1280, 64] bf16, conv4 64 -> 128 with LN and
+    SimpleGate, conv5 64 -> 64 with gamma and the residual) on clarus_hip_ffn, weights at the
+    scales of the harness's random init."""
+    from clarus_amd import _lib
+    g = gen(49)
+    c = 64
+    x = rnd(g, 1, 720, 1280, c, dtype=torch.bfloat16)
+    w1, w2 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=torch.bfloat16), rnd(g, c, c, scale=c ** -0.5, dtype=torch.bfloat16)
+    b1, b2, gamma = rnd(g, 2 * c, scale=0.1), rnd(g, c, scale=0.1), rnd(g, c, scale=0.1)
+    got = hip_bf16.linear_gate_linear(*dev(x, w1, b1, w2, b2), scale=gamma.cuda(), ln=True)
+    assert _lib.last_kernel().startswith("ffn_kernel c=64 dt=bf16 pro=1"), _lib.last_kernel()
+    e = check_ffn(got, x, w1, b1, w2, b2, gamma, True, "ffn NAFNet level 0 720p")
+    print(f"[ffn] level 0 720p: max err {e:.3e}")
+
+
 CONFIG2 = [(64, 720, 1280), (128, 360, 640), (256, 180, 320), (512, 90, 160), (1024, 45, 80)]
 
 

@@ -290,6 +290,94 @@ def test_wr_weight_padding(gate, n):
     assert int((packed == 0).sum()) == k * (nw - (2 * n if gate else n))
 
 
+def _mfma32(a_lanes: np.ndarray, b_lanes: np.ndarray) -> np.ndarray:
+    """A 32x32 MFMA as the lanes feed it: lane l supplies A[l % 32][kp (l // 32) + i] and
+    B[kp (l // 32) + i][l % 32] for its kp values (kp = 8 for 32x32x16 bf16, 1 for 32x32x2 fp32);
+    returns the lanes' accumulator elements, lane l element j = D[8 (j // 4) + 4 (l // 32) + j % 4][l % 32]."""
+    kp = a_lanes.shape[1]
+    a = np.zeros((32, 2 * kp))
+    b = np.zeros((2 * kp, 32))
+    for l in range(64):
+        a[l % 32, kp * (l // 32):kp * (l // 32) + kp] = a_lanes[l]
+        b[kp * (l // 32):kp * (l // 32) + kp, l % 32] = b_lanes[l]
+    d = a @ b
+    return np.array([[d[8 * (j // 4) + 4 * (l // 32) + j % 4, l % 32] for j in range(16)] for l in range(64)])
+
+
+@pytest.mark.parametrize("c,kp", [(32, 8), (64, 8), (32, 1), (64, 1)])
+def test_ffn_fragment_packing(c, kp):
+    """clarus_hip_ffn's data flow, emulated lane by lane on the packed weights (HipOps._ffn_pack1 /
+    _ffn_pack2) with 32x32 MFMAs as the lanes feed them (kp = 8: the bf16 instructions, kp = 1: the
+    fp32 ones, 8 / 16 per fragment): the gated accumulators of the first product used directly as
+    the second product's B operand, the residual taken from the lane's own x fragments and the
+    output channel of each element as the kernel stores it. In exact arithmetic this must equal
+    x + scale * (SG(x w1 + b1) w2 + b2) for one 32-pixel unit; a wrong k order in w2p, a wrong
+    output permutation or a wrong residual slot fails it."""
+    from clarus_amd.hip_ops import HipOps
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(32, c, generator=g, dtype=torch.float64)
+    w1 = torch.randn(c, 2 * c, generator=g, dtype=torch.float64)
+    w2 = torch.randn(c, c, generator=g, dtype=torch.float64)
+    b1 = torch.randn(2 * c, generator=g, dtype=torch.float64)
+    b2 = torch.randn(c, generator=g, dtype=torch.float64)
+    sc = torch.randn(c, generator=g, dtype=torch.float64)
+    h = x @ w1 + b1
+    want = (x + sc * ((h[:, :c] * h[:, c:]) @ w2 + b2)).numpy()
+    w1p, w2p = HipOps._ffn_pack1(w1).numpy(), HipOps._ffn_pack2(w2).numpy()
+    assert w1p.shape == (2 * c // 32, c // 16, 64, 8) and w2p.shape == (c // 32, c // 32, 64, 16)
+    xn = x.numpy()
+    lanes = np.arange(64)
+    # x fragment s of lane l: channels 16 s + 8 (l // 32) .. + 7 of pixel l % 32
+    xf = np.stack([np.stack([xn[l % 32, 16 * s + 8 * (l // 32):16 * s + 8 * (l // 32) + 8] for l in lanes])
+                   for s in range(c // 16)])                                  # [s, 64, 8]
+
+    def product(wfr, bfr):  # wfr / bfr: [64, 8 * n] lane operands, fed kp values per instruction
+        acc = np.zeros((64, 16))
+        for q in range(0, wfr.shape[1], kp):
+            acc += _mfma32(wfr[:, q:q + kp], bfr[:, q:q + kp])
+        return acc
+
+    tg = c // 32
+    u = []
+    for t in range(tg):
+        ga = product(np.concatenate([w1p[t, s] for s in range(c // 16)], 1), np.concatenate(list(xf), 1))
+        gb = product(np.concatenate([w1p[t + tg, s] for s in range(c // 16)], 1), np.concatenate(list(xf), 1))
+        hid = np.array([[32 * t + 8 * (j // 4) + 4 * (l // 32) + j % 4 for j in range(16)] for l in lanes])
+        u.append((ga + b1.numpy()[hid]) * (gb + b1.numpy()[c + hid]))
+    got = np.zeros((32, c))
+    for t2 in range(tg):
+        acc = product(np.concatenate([w2p[t2, t] for t in range(tg)], 1), np.concatenate(u, 1))
+        for l in lanes:
+            for j in range(16):
+                ch = 32 * t2 + 16 * (j // 8) + 8 * (l // 32) + j % 8
+                res = xf[2 * t2 + j // 8, l, j % 8]
+                assert res == xn[l % 32, ch]
+                got[l % 32, ch] = (acc[l, j] + b2.numpy()[ch]) * sc.numpy()[ch] + res
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10 * np.abs(want).max())  # fp64 summation order
+
+
+def test_linear_gate_linear_unfused_is_two_linears():
+    """Backends without the fused kernel run linear_gate_linear as its two linear ops: the gated
+    LN GEMM, then the second GEMM with the scale and the input as residual."""
+    calls = []
+
+    class B(Backend):
+        name = "rec2"
+
+        def linear(self, x, w, bias=None, **kw):
+            calls.append(kw)
+            y = x @ w
+            return y[:, :4] * y[:, 4:] if kw.get("gate") else y
+
+    b = B(torch.float32, torch.device("cpu"))
+    x, w1, w2, sc = torch.randn(3, 4), torch.randn(4, 8), torch.randn(4, 4), torch.randn(4)
+    out = b.linear_gate_linear(x, w1, None, w2, None, scale=sc, ln="rms", ln_eps=1e-5, out_dtype=torch.float32)
+    h = x @ w1
+    assert torch.equal(out, (h[:, :4] * h[:, 4:]) @ w2)
+    assert calls[0] == {"ln": "rms", "gate": True, "ln_eps": 1e-5}
+    assert calls[1]["residual"] is x and calls[1]["scale"] is sc and calls[1]["out_dtype"] == torch.float32
+
+
 def test_linear_ln_linear_unfused_is_two_linears():
     """Backends without the fused kernel run linear_ln_linear as the two ops."""
     calls = []
@@ -317,6 +405,7 @@ def test_pair_default_for_a_host_backend_base():
 
     dispatch.give_pair_default(HostBase)
     assert HostBase.linear_ln_linear is dispatch.linear_ln_linear_unfused
+    assert HostBase.linear_gate_linear is dispatch.linear_gate_linear_unfused
 
     class Own(HostBase):
         def linear_ln_linear(self, *a, **k):
@@ -334,15 +423,16 @@ class _PlainOracle:
         self._r = TorchRef(dtype, device)
 
     def __getattr__(self, op):
-        if op.startswith("_") or op == "linear_ln_linear":
+        if op.startswith("_") or op in ("linear_ln_linear", "linear_gate_linear"):
             raise AttributeError(op)
         return getattr(self._r, op)
 
 
 def test_nafnet_pairs_match_the_reference_call_pattern():
-    """The harness's paired calls (conv3 -> conv4, conv5 -> next conv1 in a stage of two blocks)
-    give exactly the reference block's five-linear result (fused_pairs=False) on the oracle,
-    and the harness falls back to the two linear calls when no backend has the pair op."""
+    """The harness's fused calls (at the pair width: conv3 -> conv4, conv5 -> next conv1 in a
+    stage of two blocks; at other widths the feed-forward half conv4 -> conv5) give exactly the
+    reference block's five-linear result (fused_pairs=False) on the oracle, and the harness falls
+    back to the linear calls when no backend has the fused ops."""
     from clarus_amd.nafnet import NAFNet, random_state_dict
     register_backend("plain_oracle")(_PlainOracle)
     enc, mid, dec = [2, 1], 2, [1, 2]
@@ -352,7 +442,9 @@ def test_nafnet_pairs_match_the_reference_call_pattern():
     for backend, fused in (("oracle_by_path", True), ("oracle_by_path", False), ("plain_oracle", True)):
         ops = Ops([backend], torch.float32, torch.device("cpu"), log=lambda *a: None)
         model = NAFNet(ops, width=8, enc=enc, mid=mid, dec=dec, tlc=(24, 40), state_dict=sd, fused_pairs=fused)
+        model.pair_width = 16  # the enc1 / dec0 width of this model (512 at NAFNet-w64 level 3)
         outs.append(model.forward(x))
         calls = ops.report()["ops"]
-        assert ("linear_ln_linear" in calls) == (fused and backend == "oracle_by_path"), calls
+        for op in ("linear_ln_linear", "linear_gate_linear"):
+            assert (op in calls) == (fused and backend == "oracle_by_path"), (op, calls)
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
