@@ -193,20 +193,53 @@ def test_config5_upconv(h, w, hip_bf16):
 
 
 # ------------------------------------------------------------------ depthwise 3x3 (next op on the NAFNet path)
-@pytest.mark.parametrize("c", [96, 528])
+@pytest.mark.parametrize("c", [96, 528, 640])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("gate,act,dil", [(True, None, 1), ("gelu", None, 1), (False, None, 1),
                                           (False, "gelu", 1), (False, None, 2)])
 def test_dwconv(dt, gate, act, dil, c, hip_bf16, hip_f32):
     """Depthwise 3x3 + SimpleGate / GELU gate / GELU / dilation 2 (tools/test_kernels.py:110-121,
-    193-199), odd sizes; 96 channels take the sliding-window kernel (dilation 1), 528 the
-    per-pixel one."""
+    193-199), odd sizes (two images of 37 x 53); 96 channels take the sliding-window kernel
+    (dilation 1), 528 and 640 the per-pixel one."""
     hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
     g = gen(8)
     x, w, b = rnd(g, 2, 37, 53, c, dtype=dt), rnd(g, c, 1, 3, 3), rnd(g, c)
     got = hip.dwconv(x.cuda(), w.cuda(), b.cuda(), dil=dil, gate=gate, act=act)
     ref = TorchRef(torch.float32, "cpu").dwconv(x, w, b, dil=dil, gate=gate, act=act)
     check(got.cpu(), ref, f"dwconv gate={gate} act={act} dil={dil} {dt}")
+
+
+@pytest.mark.parametrize("h,w,c", [(90, 160, 1024), (45, 80, 2048), (180, 320, 512)])
+def test_dwconv_nafnet_wide_levels(h, w, c, hip_bf16):
+    """NAFNet-w64 720p levels 3, 4 and 2 (dwconv of conv1's 2c channels -> SimpleGate -> c) on the
+    per-pixel kernel."""
+    from clarus_amd import _lib
+    g = gen(11)
+    x, wt, b = rnd(g, 1, h, w, c, dtype=torch.bfloat16), rnd(g, c, 1, 3, 3), rnd(g, c)
+    got = hip_bf16.dwconv(x.cuda(), wt.cuda(), b.cuda(), gate=True)
+    check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=True), f"dwconv {h}x{w}x{c} gate")
+
+
+def test_dwconv_bf16_in_fp32_out(hip_bf16):
+    """bf16 input with an fp32 output (a combination HipOps does not produce), through the C ABI:
+    640 channels, no gate and with the gate, two images of 37 x 53, against the oracle's fp32
+    result."""
+    import ctypes
+    from clarus_amd import _lib
+    g = gen(12)
+    n, h, w, c = 2, 37, 53, 640
+    x, wt, b = rnd(g, n, h, w, c, dtype=torch.bfloat16), rnd(g, c, 1, 3, 3), rnd(g, c)
+    taps = wt.float().reshape(c, 9).t().contiguous().cuda()
+    for gate in (0, 1):
+        cout = c // 2 if gate else c
+        out = torch.empty(n, h, w, cout, device="cuda", dtype=torch.float32)
+        xc, bc = x.cuda(), b.cuda()
+        _lib.check(hip_bf16.lib.clarus_hip_dwconv3x3(
+            xc.data_ptr(), _lib.BF16, taps.data_ptr(), bc.data_ptr(), out.data_ptr(), _lib.F32, n, h, w, c, 1, gate, 0,
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "dwconv3x3")
+        torch.cuda.synchronize()
+        ref = TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=bool(gate))
+        assert_fp32(out.cpu(), ref, what=f"dwconv bf16 -> fp32 gate={gate}")
 
 
 def test_dwconv_nafnet_720p(hip_bf16):
