@@ -3,7 +3,7 @@
 //   u   = SG(W1^T . pro(x) + b1)                 (2c hidden channels -> c by SimpleGate)
 //   out = x + (W2^T . u + b2) * scale * out_scale
 //
-// for dense NHWC rows x [m][c], c = 32 or 64, with pro the row LayerNorm (no affine), the RMS
+// for dense NHWC rows x [m][c], c = 32, 64 or 128 (bf16), with pro the row LayerNorm (no affine), the RMS
 // norm or nothing. This is NAFNet's feed-forward half-block (conv4 -> SimpleGate -> conv5, the
 // conv5 output scaled by gamma and added to the block input) and the fp32 pointwise chain of the
 // benchmark (32 -> 64 + SimpleGate -> 32, beta * . + x).
@@ -63,18 +63,21 @@ __host__ __device__ constexpr int ff_fixed_bytes(int c, int dt) {
 // read from HBM / from the last-level cache (back-to-back calls): 8 waves, ring 3: 56.7 / 49.8;
 // ring 4: 58.2 / 51.6; 10 waves, ring 3: 66.3 / 51.7; 12 waves, ring 2: 64.3 / 45.4; 4 waves:
 // 80 / 89. The fp32 config-1 chain (c = 32): 11.6 / 10.5 with 8 waves, 13.3 / 11.9 with 12.
+// c = 128 (bf16): the weights and tables take 98 KiB, which leaves one 8 KiB slot for each of 7
+// waves; a wave copies its fragments of the slot's unit into registers and refills the slot with
+// the next unit at once, so one unit is in flight while one is computed.
 __host__ __device__ constexpr int ff_waves(int c, int dt) {
-  return (160 * 1024 - ff_fixed_bytes(c, dt)) / (8 * ff_unit_bytes(c, dt)) >= 3 ? 8 : 4;
+  return c == 128 ? 7 : (160 * 1024 - ff_fixed_bytes(c, dt)) / (8 * ff_unit_bytes(c, dt)) >= 3 ? 8 : 4;
 }
 __host__ __device__ constexpr int ff_depth(int c, int dt) {
   const int d = (160 * 1024 - ff_fixed_bytes(c, dt)) / (ff_waves(c, dt) * ff_unit_bytes(c, dt));
-  return d > 3 ? 3 : d;
+  return c == 128 ? 1 : d > 3 ? 3 : d;
 }
 __host__ __device__ constexpr int ff_lds_bytes(int c, int dt) {
   return ff_fixed_bytes(c, dt) + ff_waves(c, dt) * ff_depth(c, dt) * ff_unit_bytes(c, dt);
 }
 static_assert(ff_depth(64, DT_F32) >= 2 && ff_depth(64, DT_BF16) >= 2 && ff_depth(32, DT_F32) >= 2 &&
-                  ff_depth(32, DT_BF16) >= 2,
+                  ff_depth(32, DT_BF16) >= 2 && ff_lds_bytes(128, DT_BF16) <= 160 * 1024,
               "LDS");
 
 struct FfP {
@@ -94,6 +97,191 @@ __device__ __forceinline__ f32x16 mfma32_f32(float a, float b, const f32x16& c) 
 }
 
 __device__ __forceinline__ int ff_swz(int row, int unit, int u, int rpb) { return unit ^ ((row / rpb) & (u - 1)); }
+
+// One 32-pixel unit from its x fragments (xr[s]: channels 16 s + 8 (lane / 32) .. + 7 of pixel
+// q0 + lane % 32): the prologue, both products with the gate between them, the epilogue and
+// NS buffer stores (rows past M dropped by the range).
+// a lane's raw x fragment (8 consecutive channels): packed bf16, or fp32
+template <int DT> struct XFragT;
+template <> struct XFragT<DT_BF16> { using T = u32x4; };
+template <> struct XFragT<DT_F32> { using T = f32x8; };
+template <int DT>
+__device__ __forceinline__ float xel(const typename XFragT<DT>::T& f, int i) {
+  if constexpr (DT == DT_BF16) return __uint_as_float((i & 1) ? (f[i >> 1] & 0xffff0000u) : (f[i >> 1] << 16));
+  else return f.v[i];
+}
+
+template <int C, int DT, int PRO>
+__device__ __forceinline__ void ffn_unit(const typename XFragT<DT>::T (&xr)[C / 16], const unsigned char* w1l,
+                                         const unsigned char* w2l, const float* tab, const FfP& p, int64_t q0,
+                                         int lane) {
+  constexpr int ES = ff_es(DT), RB = C * ES, KS = C / 16, TG = C / 32;
+  const int px = lane & 31, hf = lane >> 5;
+  // the first product's B operand: the row, LayerNorm'd ((x - mean) * rstd, two-pass) or RMS
+  // normalised over the pixel's c channels (two lanes hold half each), rounded to bf16 for bf16
+  // weights; the raw fragments themselves without a prologue
+  f32x8 xa[KS];
+  bf16x8 xb[KS];
+  if constexpr (PRO == PRO_NONE) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (DT == DT_BF16) xb[s] = __builtin_bit_cast(bf16x8, xr[s]);
+      else xa[s] = xr[s];
+    }
+  } else {
+    const float invc = 1.0f / (float)C;
+    float mean = 0.f;
+    if constexpr (PRO == PRO_LN) {
+      float sum = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += xel<DT>(xr[s], i);
+      sum += __shfl_xor(sum, 32, 64);
+      mean = sum * invc;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        xa[s].v[i] = PRO == PRO_LN ? xel<DT>(xr[s], i) - mean : xel<DT>(xr[s], i);
+        ss += xa[s].v[i] * xa[s].v[i];
+      }
+    ss += __shfl_xor(ss, 32, 64);
+    const float rstd = rsqrtf(ss * invc + p.ln_eps);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xa[s].v[i] *= rstd;
+      if constexpr (DT == DT_BF16) xb[s] = pack_bf16(xa[s]);  // RNE
+    }
+  }
+
+  // ---- first product, its bias in the accumulators' start values, and the gate: uf[T] holds
+  // the lane's 16 gated values of hidden tile T (element 4 q + jj: hidden channel
+  // 32 T + 8 q + 4 hf + jj, its gate partner c channels on)
+  using UFrag = typename std::conditional<DT == DT_BF16, u32x4, f32x4>::type;
+  UFrag uf[TG][DT == DT_BF16 ? 2 : 4];
+#pragma unroll
+  for (int T = 0; T < TG; ++T) {
+    f32x16 ga, gb;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 ba = *reinterpret_cast<const f32x4*>(tab + 32 * T + 8 * q + 4 * hf);
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(tab + C + 32 * T + 8 * q + 4 * hf);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        ga[4 * q + jj] = ba[jj];
+        gb[4 * q + jj] = bb[jj];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (DT == DT_BF16) {
+        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(w1l + ((T * KS + s) * 64 + lane) * 16);
+        const bf16x8 wb = *reinterpret_cast<const bf16x8*>(w1l + (((T + TG) * KS + s) * 64 + lane) * 16);
+        ga = mfma32_bf16(wa, xb[s], ga);
+        gb = mfma32_bf16(wb, xb[s], gb);
+      } else {
+        const unsigned char* pa = w1l + ((T * KS + s) * 64 + lane) * 32;
+        const unsigned char* pb = w1l + (((T + TG) * KS + s) * 64 + lane) * 32;
+        const f32x4 wa0 = *reinterpret_cast<const f32x4*>(pa), wa1 = *reinterpret_cast<const f32x4*>(pa + 16);
+        const f32x4 wb0 = *reinterpret_cast<const f32x4*>(pb), wb1 = *reinterpret_cast<const f32x4*>(pb + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ga = mfma32_f32(wa0[i], xa[s].v[i], ga);
+          gb = mfma32_f32(wb0[i], xa[s].v[i], gb);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ga = mfma32_f32(wa1[i], xa[s].v[4 + i], ga);
+          gb = mfma32_f32(wb1[i], xa[s].v[4 + i], gb);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float g[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) g[jj] = ga[4 * q + jj] * gb[4 * q + jj];
+      if constexpr (DT == DT_BF16) {
+        uf[T][q / 2][2 * (q & 1)] = (unsigned)f32_to_bf16_bits(g[0]) | ((unsigned)f32_to_bf16_bits(g[1]) << 16);
+        uf[T][q / 2][2 * (q & 1) + 1] = (unsigned)f32_to_bf16_bits(g[2]) | ((unsigned)f32_to_bf16_bits(g[3]) << 16);
+      } else {
+        uf[T][q] = f32x4{g[0], g[1], g[2], g[3]};
+      }
+    }
+    // c = 128: keep the scheduler from hoisting the next tiles' weight fragments (spills)
+    if constexpr (C >= 128) __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // ---- second product (bias in the start values), epilogue and stores per output tile
+  const int rows = p.m - q0 < FF_P ? (int)(p.m - q0) : FF_P;
+  const __amdgpu_buffer_rsrc_t orsrc = buf_rsrc_n((unsigned char*)p.out + q0 * RB, (uint32_t)(rows * RB));
+#pragma unroll
+  for (int T2 = 0; T2 < TG; ++T2) {
+    // element j: channel 32 T2 + 16 (j / 8) + 8 hf + j % 8 = x fragment 2 T2 + j / 8, slot j % 8
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int ch = 32 * T2 + 16 * r + 8 * hf;
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(tab + 2 * C + ch);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(tab + 2 * C + ch + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[8 * r + i] = b0[i];
+        acc[8 * r + 4 + i] = b1[i];
+      }
+    }
+#pragma unroll
+    for (int T = 0; T < TG; ++T) {
+      const unsigned char* wp = w2l + ((T2 * TG + T) * 64 + lane) * (16 * ES);
+      if constexpr (DT == DT_BF16) {
+        const bf16x8 w0 = *reinterpret_cast<const bf16x8*>(wp);
+        const bf16x8 w1 = *reinterpret_cast<const bf16x8*>(wp + 16);
+        acc = mfma32_bf16(w0, __builtin_bit_cast(bf16x8, uf[T][0]), acc);
+        acc = mfma32_bf16(w1, __builtin_bit_cast(bf16x8, uf[T][1]), acc);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(wp + 16 * q);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) acc = mfma32_f32(w[jj], uf[T][q][jj], acc);
+        }
+      }
+    }
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int ch = 32 * T2 + 16 * r + 8 * hf;
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(tab + 3 * C + ch);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(tab + 3 * C + ch + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[8 * r + i] = acc[8 * r + i] * s0[i] + xel<DT>(xr[2 * T2 + r], i);
+        v[8 * r + 4 + i] = acc[8 * r + 4 + i] * s1[i] + xel<DT>(xr[2 * T2 + r], 4 + i);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int off = px * RB + (32 * T2 + 16 * r + 8 * hf) * ES;
+      if constexpr (DT == DT_BF16) {
+        u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = (unsigned)f32_to_bf16_bits(v[8 * r + 2 * i]) | ((unsigned)f32_to_bf16_bits(v[8 * r + 2 * i + 1]) << 16);
+        __builtin_amdgcn_raw_buffer_store_b128(o, orsrc, off, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{v[8 * r], v[8 * r + 1], v[8 * r + 2], v[8 * r + 3]}), orsrc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{v[8 * r + 4], v[8 * r + 5], v[8 * r + 6], v[8 * r + 7]}), orsrc,
+            off + 16, 0, 0);
+      }
+    }
+  }
+}
 
 template <int C, int DT, int PRO>
 __global__ void __launch_bounds__(64 * ff_waves(C, DT)) ffn_kernel(const FfP p) {
@@ -162,191 +350,28 @@ __global__ void __launch_bounds__(64 * ff_waves(C, DT)) ffn_kernel(const FfP p) 
     }
   };
 
-  auto compute = [&](int j, int slot) __attribute__((always_inline)) {
-    const int unit = wid + j * stride;
+  // the lane's x fragments of the unit in `slot`: channels 16 s + 8 hf .. + 7 of pixel px
+  auto read_frags = [&](int slot, typename XFragT<DT>::T (&xr)[KS]) __attribute__((always_inline)) {
     const unsigned char* xrow = ring + slot * UB + px * RB;
-    // x fragments: channels 16 s + 8 hf .. + 7 of pixel px, as fp32
-    f32x8 xv[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       if constexpr (DT == DT_BF16) {
-        const u32x4 q = *reinterpret_cast<const u32x4*>(xrow + ff_swz(px, 2 * s + hf, U, RPB) * 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          xv[s].v[2 * i] = __uint_as_float(q[i] << 16);
-          xv[s].v[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
-        }
+        xr[s] = *reinterpret_cast<const u32x4*>(xrow + ff_swz(px, 2 * s + hf, U, RPB) * 16);
       } else {
         const f32x4 a = *reinterpret_cast<const f32x4*>(xrow + ff_swz(px, 4 * s + 2 * hf, U, RPB) * 16);
         const f32x4 b = *reinterpret_cast<const f32x4*>(xrow + ff_swz(px, 4 * s + 2 * hf + 1, U, RPB) * 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          xv[s].v[i] = a[i];
-          xv[s].v[4 + i] = b[i];
+          xr[s].v[i] = a[i];
+          xr[s].v[4 + i] = b[i];
         }
       }
     }
-    // the first product's B operand: the row, LayerNorm'd ((x - mean) * rstd, two-pass) or RMS
-    // normalised over the pixel's c channels (two lanes hold half each), rounded to bf16 for bf16
-    f32x8 xa[KS];
-    if constexpr (PRO == PRO_NONE) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) xa[s] = xv[s];
-    } else {
-      const float invc = 1.0f / (float)C;
-      float mean = 0.f;
-      if constexpr (PRO == PRO_LN) {
-        float sum = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) sum += xv[s].v[i];
-        sum += __shfl_xor(sum, 32, 64);
-        mean = sum * invc;
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          xa[s].v[i] = PRO == PRO_LN ? xv[s].v[i] - mean : xv[s].v[i];
-          ss += xa[s].v[i] * xa[s].v[i];
-        }
-      ss += __shfl_xor(ss, 32, 64);
-      const float rstd = rsqrtf(ss * invc + p.ln_eps);
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xa[s].v[i] *= rstd;
-    }
-    bf16x8 xb[KS];
-    if constexpr (DT == DT_BF16) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) xb[s] = pack_bf16(xa[s]);  // exact for raw bf16 x, RNE otherwise
-    }
-
-    // ---- first product, its bias in the accumulators' start values, and the gate: uf[T] holds
-    // the lane's 16 gated values of hidden tile T (element 4 q + jj: hidden channel
-    // 32 T + 8 q + 4 hf + jj, its gate partner c channels on)
-    using UFrag = typename std::conditional<DT == DT_BF16, u32x4, f32x4>::type;
-    UFrag uf[TG][DT == DT_BF16 ? 2 : 4];
-#pragma unroll
-    for (int T = 0; T < TG; ++T) {
-      f32x16 ga, gb;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 ba = *reinterpret_cast<const f32x4*>(tab + 32 * T + 8 * q + 4 * hf);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(tab + C + 32 * T + 8 * q + 4 * hf);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          ga[4 * q + jj] = ba[jj];
-          gb[4 * q + jj] = bb[jj];
-        }
-      }
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        if constexpr (DT == DT_BF16) {
-          const bf16x8 wa = *reinterpret_cast<const bf16x8*>(w1l + ((T * KS + s) * 64 + lane) * 16);
-          const bf16x8 wb = *reinterpret_cast<const bf16x8*>(w1l + (((T + TG) * KS + s) * 64 + lane) * 16);
-          ga = mfma32_bf16(wa, xb[s], ga);
-          gb = mfma32_bf16(wb, xb[s], gb);
-        } else {
-          const unsigned char* pa = w1l + ((T * KS + s) * 64 + lane) * 32;
-          const unsigned char* pb = w1l + (((T + TG) * KS + s) * 64 + lane) * 32;
-          const f32x4 wa0 = *reinterpret_cast<const f32x4*>(pa), wa1 = *reinterpret_cast<const f32x4*>(pa + 16);
-          const f32x4 wb0 = *reinterpret_cast<const f32x4*>(pb), wb1 = *reinterpret_cast<const f32x4*>(pb + 16);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ga = mfma32_f32(wa0[i], xa[s].v[i], ga);
-            gb = mfma32_f32(wb0[i], xa[s].v[i], gb);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ga = mfma32_f32(wa1[i], xa[s].v[4 + i], ga);
-            gb = mfma32_f32(wb1[i], xa[s].v[4 + i], gb);
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float g[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) g[jj] = ga[4 * q + jj] * gb[4 * q + jj];
-        if constexpr (DT == DT_BF16) {
-          uf[T][q / 2][2 * (q & 1)] = (unsigned)f32_to_bf16_bits(g[0]) | ((unsigned)f32_to_bf16_bits(g[1]) << 16);
-          uf[T][q / 2][2 * (q & 1) + 1] = (unsigned)f32_to_bf16_bits(g[2]) | ((unsigned)f32_to_bf16_bits(g[3]) << 16);
-        } else {
-          uf[T][q] = f32x4{g[0], g[1], g[2], g[3]};
-        }
-      }
-    }
-
-    // ---- second product (bias in the start values), epilogue and stores per output tile
-    const int64_t q0 = (int64_t)unit * FF_P;
-    const int rows = p.m - q0 < FF_P ? (int)(p.m - q0) : FF_P;
-    const __amdgpu_buffer_rsrc_t orsrc = buf_rsrc_n((unsigned char*)p.out + q0 * RB, (uint32_t)(rows * RB));
-#pragma unroll
-    for (int T2 = 0; T2 < TG; ++T2) {
-      // element j: channel 32 T2 + 16 (j / 8) + 8 hf + j % 8 = x fragment 2 T2 + j / 8, slot j % 8
-      f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int ch = 32 * T2 + 16 * r + 8 * hf;
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(tab + 2 * C + ch);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(tab + 2 * C + ch + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[8 * r + i] = b0[i];
-          acc[8 * r + 4 + i] = b1[i];
-        }
-      }
-#pragma unroll
-      for (int T = 0; T < TG; ++T) {
-        const unsigned char* wp = w2l + ((T2 * TG + T) * 64 + lane) * (16 * ES);
-        if constexpr (DT == DT_BF16) {
-          const bf16x8 w0 = *reinterpret_cast<const bf16x8*>(wp);
-          const bf16x8 w1 = *reinterpret_cast<const bf16x8*>(wp + 16);
-          acc = mfma32_bf16(w0, __builtin_bit_cast(bf16x8, uf[T][0]), acc);
-          acc = mfma32_bf16(w1, __builtin_bit_cast(bf16x8, uf[T][1]), acc);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4 w = *reinterpret_cast<const f32x4*>(wp + 16 * q);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) acc = mfma32_f32(w[jj], uf[T][q][jj], acc);
-          }
-        }
-      }
-      float v[16];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int ch = 32 * T2 + 16 * r + 8 * hf;
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(tab + 3 * C + ch);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(tab + 3 * C + ch + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[8 * r + i] = acc[8 * r + i] * s0[i] + xv[2 * T2 + r].v[i];
-          v[8 * r + 4 + i] = acc[8 * r + 4 + i] * s1[i] + xv[2 * T2 + r].v[4 + i];
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int off = px * RB + (32 * T2 + 16 * r + 8 * hf) * ES;
-        if constexpr (DT == DT_BF16) {
-          u32x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            o[i] = (unsigned)f32_to_bf16_bits(v[8 * r + 2 * i]) | ((unsigned)f32_to_bf16_bits(v[8 * r + 2 * i + 1]) << 16);
-          __builtin_amdgcn_raw_buffer_store_b128(o, orsrc, off, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, f32x4{v[8 * r], v[8 * r + 1], v[8 * r + 2], v[8 * r + 3]}), orsrc, off, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, f32x4{v[8 * r + 4], v[8 * r + 5], v[8 * r + 6], v[8 * r + 7]}), orsrc,
-              off + 16, 0, 0);
-        }
-      }
-    }
+  };
+  auto compute = [&](int j, int slot) __attribute__((always_inline)) {
+    typename XFragT<DT>::T xr[KS];
+    read_frags(slot, xr);
+    ffn_unit<C, DT, PRO>(xr, w1l, w2l, tab, p, (int64_t)(wid + j * stride) * FF_P, lane);
   };
 
   // ---- the ring: units 0 .. D - 2 in flight before the first is computed, issued behind the
@@ -363,15 +388,31 @@ __global__ void __launch_bounds__(64 * ff_waves(C, DT)) ffn_kernel(const FfP p) 
   }
   barrier_keep_vm();  // every wave's weight copies and table writes are in LDS
   if (nmine == 0) return;
-  int sc = 0, si = D - 1;  // slots of the unit computed / issued in this iteration
-  for (int j = 0; j < nmine; ++j) {
-    if (j >= D - 1) wait_vmcnt<(D - 2) * CP + (D - 1) * NS>();
-    else wait_vmcnt<(D - 2) * CP>();  // stricter than needed for j > 0
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads follow the wait; slot si is free
-    issue(j + D - 1, si);
-    compute(j, sc);
-    sc = sc == D - 1 ? 0 : sc + 1;
-    si = si == D - 1 ? 0 : si + 1;
+  if constexpr (D == 1) {
+    // one slot: unit j's fragments go to registers, then unit j + 1's copies refill the slot, so
+    // when unit j + 1 is waited for only unit j's NS stores were issued after its copies
+    issue(0, 0);
+    for (int j = 0; j < nmine; ++j) {
+      if (j > 0) wait_vmcnt<NS>();
+      else wait_vmem_all();
+      asm volatile("" ::: "memory");  // slot reads follow the wait
+      typename XFragT<DT>::T xr[KS];
+      read_frags(0, xr);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is free
+      issue(j + 1, 0);
+      ffn_unit<C, DT, PRO>(xr, w1l, w2l, tab, p, (int64_t)(wid + j * stride) * FF_P, lane);
+    }
+  } else {
+    int sc = 0, si = D - 1;  // slots of the unit computed / issued in this iteration
+    for (int j = 0; j < nmine; ++j) {
+      if (j >= D - 1) wait_vmcnt<(D - 2) * CP + (D - 1) * NS>();
+      else wait_vmcnt<(D - 2) * CP>();  // stricter than needed for j > 0
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads follow the wait; slot si is free
+      issue(j + D - 1, si);
+      compute(j, sc);
+      sc = sc == D - 1 ? 0 : sc + 1;
+      si = si == D - 1 ? 0 : si + 1;
+    }
   }
   wait_vmem_all();
 }
@@ -407,7 +448,8 @@ extern "C" int clarus_hip_ffn(const void* x, void* out, int dtype, const void* w
   clear_error();
   CLARUS_REQUIRE(x && out && w1p && w2p, "ffn: null operand");
   CLARUS_REQUIRE(dtype == DT_BF16 || dtype == DT_F32, "ffn: bf16 or fp32 activations and weights");
-  CLARUS_REQUIRE(c == 32 || c == 64, "ffn: c = 32 or 64 (c=%lld)", (long long)c);
+  CLARUS_REQUIRE(c == 32 || c == 64 || (c == 128 && dtype == DT_BF16), "ffn: c = 32 or 64, or 128 in bf16 (c=%lld)",
+                 (long long)c);
   CLARUS_REQUIRE(m > 0 && m < ((int64_t)1 << 35), "ffn: m out of range (m=%lld)", (long long)m);
   CLARUS_REQUIRE(pro == PRO_NONE || pro == PRO_LN || pro == PRO_RMS, "ffn: prologue none, LN or RMS");
   CLARUS_REQUIRE(aligned(x, 16) && aligned(out, 16) && aligned(w1p, 16) && aligned(w2p, 16),
@@ -416,7 +458,8 @@ extern "C" int clarus_hip_ffn(const void* x, void* out, int dtype, const void* w
   const char* xb = (const char*)x;
   const char* ob = (const char*)out;
   CLARUS_REQUIRE(ob + m * rb <= xb || xb + m * rb <= ob, "ffn: out must not overlap x");
-  const int nw = dtype == DT_BF16 ? (c == 32 ? ff_waves(32, DT_BF16) : ff_waves(64, DT_BF16))
+  const int nw = dtype == DT_BF16 ? (c == 32 ? ff_waves(32, DT_BF16) : c == 64 ? ff_waves(64, DT_BF16)
+                                                                            : ff_waves(128, DT_BF16))
                                   : (c == 32 ? ff_waves(32, DT_F32) : ff_waves(64, DT_F32));
   const int64_t units = cdiv(m, FF_P);
   int64_t nblk = device_cus();
@@ -428,7 +471,8 @@ extern "C" int clarus_hip_ffn(const void* x, void* out, int dtype, const void* w
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DT_BF16) {
     if (c == 32) launch_pro<32, DT_BF16>(p, pro, (int)nblk, s);
-    else launch_pro<64, DT_BF16>(p, pro, (int)nblk, s);
+    else if (c == 64) launch_pro<64, DT_BF16>(p, pro, (int)nblk, s);
+    else launch_pro<128, DT_BF16>(p, pro, (int)nblk, s);
   } else {
     if (c == 32) launch_pro<32, DT_F32>(p, pro, (int)nblk, s);
     else launch_pro<64, DT_F32>(p, pro, (int)nblk, s);

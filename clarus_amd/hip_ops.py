@@ -100,8 +100,8 @@ class HipOps(Backend):
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
     # linear_gate_linear (NAFNet's feed-forward half-block and the config-1 chain, an explicit op
-    # the caller asks for) as one kernel (clarus_hip_ffn) for c = 32 / 64 channels with weights of
-    # the activation dtype; False (or other shapes) runs its two linear ops.
+    # the caller asks for) as one kernel (clarus_hip_ffn) for c = 32 / 64 channels (and 128 in bf16)
+    # with weights of the activation dtype; False (or other shapes) runs its two linear ops.
     fuse_ffn = True
     # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
     # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
@@ -438,14 +438,15 @@ class HipOps(Backend):
                            out_dtype=None):
         """linear(linear(x, w1, b1, ln=ln, gate=True), w2, b2, scale=scale, residual=x) (the
         feed-forward half of a NAFNet block; the config-1 chain without LN). One kernel
-        (clarus_hip_ffn) for dense NHWC x with c = 32 or 64 in the backend's dtype, weights of that
+        (clarus_hip_ffn) for dense NHWC x with c = 32 or 64 (or 128 in bf16) in the backend's dtype, weights of that
         dtype and an output of it: the gated intermediate stays in registers, rounded as the
         first linear stores it; with bf16 weights a normalised row is rounded once to bf16 (the
         reference's in-kernel LayerNorm, kernels/gemm.py:165-175). Otherwise, or with
         prologue_split, the two linear ops."""
         c = x.shape[-1] if x.dim() == 4 else 0
         odt = out_dtype or self.dtype
-        fits = (self.fuse_ffn and c in (32, 64) and x.dtype == self.dtype and odt == x.dtype
+        fits = (self.fuse_ffn and (c in (32, 64) or (c == 128 and x.dtype == torch.bfloat16))
+                and x.dtype == self.dtype and odt == x.dtype
                 and ln in (False, True, "rms") and not (ln and self.prologue_split)
                 and w2 is not None and w1.dtype == x.dtype and w2.dtype == x.dtype
                 and tuple(w1.shape) == (c, 2 * c) and tuple(w2.shape) == (c, c)

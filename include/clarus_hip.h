@@ -142,7 +142,7 @@ int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream)
 int clarus_hip_gemm_wr(const ClarusGemmArgs* args, const void* wp, void* stream);
 
 /*
- * Fused pointwise feed-forward on dense NHWC rows x [m][c] (c = 32 or 64), one kernel:
+ * Fused pointwise feed-forward on dense NHWC rows x [m][c] (c = 32 or 64, or 128 with bf16), one kernel:
  *   u   = SimpleGate(pro(x) . w1 + b1)          w1 [c][2c]: the product of the two c-halves
  *   out = x + (u . w2 + b2) * scale * out_scale  w2 [c][c]
  * pro = CLARUS_PRO_NONE, CLARUS_PRO_LN or CLARUS_PRO_RMS (no affine, eps ln_eps). dtype (bf16 or

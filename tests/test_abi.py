@@ -96,8 +96,9 @@ def test_validation_rejects_before_launch(lib):
     assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 residual, 512 outputs
     # clarus_hip_ffn: c, dtype, prologue, alignment and overlap are checked before any launch
     ffn = lib.clarus_hip_ffn
-    assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 128, 1, 1e-6, 1.0, None) == _lib.EINVAL
-    assert b"c = 32 or 64" in lib.clarus_hip_last_error()
+    assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 256, 1, 1e-6, 1.0, None) == _lib.EINVAL
+    assert b"c = 32 or 64, or 128 in bf16" in lib.clarus_hip_last_error()
+    assert ffn(16, 1 << 20, _lib.F32, 16, None, 16, None, None, 64, 128, 1, 1e-6, 1.0, None) == _lib.EINVAL
     assert ffn(16, 1 << 20, 7, 16, None, 16, None, None, 64, 64, 1, 1e-6, 1.0, None) == _lib.EINVAL
     assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 64, 2, 1e-6, 1.0, None) == _lib.EINVAL  # mul
     assert ffn(16, 1 << 20, _lib.BF16, 24, None, 16, None, None, 64, 64, 1, 1e-6, 1.0, None) == _lib.EINVAL

@@ -1124,6 +1124,8 @@ FFN_CASES = [  # (c, dtype, ln, (n, h, w), with biases and scale)
     (64, torch.float32, True, (1, 33, 31), True),
     (32, torch.float32, False, (1, 1, 5), False),     # m = 5, one partial unit
     (64, torch.float32, "rms", (1, 16, 64), True),    # whole units only
+    (128, torch.bfloat16, True, (1, 23, 41), True),   # NAFNet level 1 width: the one-slot ring
+    (128, torch.bfloat16, False, (2, 3, 5), False),   # m = 30: one partial unit
 ]
 
 
@@ -1146,11 +1148,11 @@ def test_linear_gate_linear(c, dt, ln, shape, full, hip_bf16, hip_f32):
 
 
 def test_linear_gate_linear_unfused_shapes(hip_bf16):
-    """Shapes clarus_hip_ffn does not take (c = 128, an fp32 output of bf16 activations) run the
+    """Shapes clarus_hip_ffn does not take (c = 256, an fp32 output of bf16 activations) run the
     two linear ops and give the same result class."""
     from clarus_amd import _lib
     g = gen(48)
-    for c, odt in ((128, None), (64, torch.float32)):
+    for c, odt in ((256, None), (64, torch.float32)):
         x = rnd(g, 1, 9, 13, c, dtype=torch.bfloat16)
         w1 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=torch.bfloat16)
         w2 = rnd(g, c, c, scale=c ** -0.5, dtype=torch.bfloat16)
@@ -1160,6 +1162,21 @@ def test_linear_gate_linear_unfused_shapes(hip_bf16):
         u = hip_bf16.linear(*dev(x, w1, b1), ln=True, gate=True)
         want = hip_bf16.linear(u, *dev(w2, b2), scale=sc.cuda(), residual=x.cuda(), out_dtype=odt)
         assert torch.equal(got, want), f"c{c}: the fallback is the two linear ops"
+
+
+def test_ffn_nafnet_level1_full(hip_bf16):
+    """NAFNet-w64 level 1 at 720p (x [1, 360, 640, 128] bf16, conv4 128 -> 256 with LN and
+    SimpleGate, conv5 128 -> 128 with gamma and the residual) on clarus_hip_ffn."""
+    from clarus_amd import _lib
+    g = gen(50)
+    c = 128
+    x = rnd(g, 1, 360, 640, c, dtype=torch.bfloat16)
+    w1, w2 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=torch.bfloat16), rnd(g, c, c, scale=c ** -0.5, dtype=torch.bfloat16)
+    b1, b2, gamma = rnd(g, 2 * c, scale=0.1), rnd(g, c, scale=0.1), rnd(g, c, scale=0.1)
+    got = hip_bf16.linear_gate_linear(*dev(x, w1, b1, w2, b2), scale=gamma.cuda(), ln=True)
+    assert _lib.last_kernel().startswith("ffn_kernel c=128 dt=bf16 pro=1"), _lib.last_kernel()
+    e = check_ffn(got, x, w1, b1, w2, b2, gamma, True, "ffn NAFNet level 1 720p")
+    print(f"[ffn] level 1 720p: max err {e:.3e}")
 
 
 def test_ffn_nafnet_level0_full(hip_bf16):

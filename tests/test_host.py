@@ -304,7 +304,7 @@ def _mfma32(a_lanes: np.ndarray, b_lanes: np.ndarray) -> np.ndarray:
     return np.array([[d[8 * (j // 4) + 4 * (l // 32) + j % 4, l % 32] for j in range(16)] for l in range(64)])
 
 
-@pytest.mark.parametrize("c,kp", [(32, 8), (64, 8), (32, 1), (64, 1)])
+@pytest.mark.parametrize("c,kp", [(32, 8), (64, 8), (128, 8), (32, 1), (64, 1)])
 def test_ffn_fragment_packing(c, kp):
     """clarus_hip_ffn's data flow, emulated lane by lane on the packed weights (HipOps._ffn_pack1 /
     _ffn_pack2) with 32x32 MFMAs as the lanes feed them (kp = 8: the bf16 instructions, kp = 1: the
