@@ -377,7 +377,7 @@ def main() -> None:
     others = [] if args.no_ops else (wl.config1_cases(hip32, dev) + wl.config3_cases(hip32, dev)
                                      + wl.config4_cases(hip, hip32, dev) + wl.config5_cases(hip, dev)
                                      + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev),
-                                        wl.nafnet_ffn_case(hip, dev),
+                                        wl.nafnet_ffn_case(hip, dev), wl.nafnet_lndw_case(hip, dev),
                                         wl.evssm_scan_case(hip, dev), wl.metrics_case(dev)])
     if args.pmc_pass:  # the last dispatches: two markers, the copy, then a marker before each op and one after
         cases = wl.all_cases(hip, hip32, dev)

@@ -67,6 +67,7 @@ SIGNATURES = {
     "clarus_hip_gemm_wp": (_i32, [ctypes.POINTER(GemmArgs), _vp, _vp]),
     "clarus_hip_gemm_wr": (_i32, [ctypes.POINTER(GemmArgs), _vp, _vp]),
     "clarus_hip_ffn": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _f32, _vp]),
+    "clarus_hip_ln_gemm_dwconv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp]),
     "clarus_hip_gemm_ln_gemm_w1p": (_i32, [ctypes.POINTER(GemmArgs), _vp, _f32, _i32, _vp, _vp, _vp, _i64, _i32, _vp]),
     "clarus_hip_conv3x3": (_i32, [ctypes.POINTER(ConvArgs), _vp]),
     "clarus_hip_intro3x3": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp]),

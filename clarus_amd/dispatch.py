@@ -106,13 +106,22 @@ def linear_gate_linear_unfused(self, x, w1, b1=None, w2=None, b2=None, scale=Non
     return self.linear(u, w2, b2, scale=scale, residual=x, out_dtype=out_dtype)
 
 
-_FUSED_DEFAULTS = {"linear_ln_linear": linear_ln_linear_unfused, "linear_gate_linear": linear_gate_linear_unfused}
+def linear_dwconv_unfused(self, x, w, bias=None, dw_w=None, dw_b=None, ln=True, gate=True, ln_eps=1e-6):
+    """t = linear(x, w, bias, ln=ln) followed by dwconv(t, dw_w, dw_b, gate=gate): the first half of
+    a NAFNet block (conv1 with LayerNorm -> depthwise 3x3 -> SimpleGate,
+    python/clarus/models/nafnet/__init__.py:155-156). Backends without a fused kernel run the two
+    ops."""
+    return self.dwconv(self.linear(x, w, bias, ln=ln, ln_eps=ln_eps), dw_w, dw_b, gate=gate)
+
+
+_FUSED_DEFAULTS = {"linear_ln_linear": linear_ln_linear_unfused, "linear_gate_linear": linear_gate_linear_unfused,
+                   "linear_dwconv": linear_dwconv_unfused}
 
 
 def give_pair_default(backend_cls) -> None:
-    """Attach the unfused defaults (linear_ln_linear_unfused, linear_gate_linear_unfused) to a
-    backend base class that lacks those ops, so every backend derived from it answers them with
-    their linear calls."""
+    """Attach the unfused defaults (linear_ln_linear_unfused, linear_gate_linear_unfused,
+    linear_dwconv_unfused) to a backend base class that lacks those ops, so every backend derived
+    from it answers them with their two calls."""
     for name, fn in _FUSED_DEFAULTS.items():
         if not callable(getattr(backend_cls, name, None)):
             setattr(backend_cls, name, fn)

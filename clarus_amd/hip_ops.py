@@ -25,8 +25,8 @@ import torch
 
 from . import _lib
 from .dft import dft_matrices
-from .dispatch import (Backend, BackendUnavailable, Unsupported, linear_gate_linear_unfused, linear_ln_linear_unfused,
-                       register_backend)
+from .dispatch import (Backend, BackendUnavailable, Unsupported, linear_dwconv_unfused, linear_gate_linear_unfused,
+                       linear_ln_linear_unfused, register_backend)
 from .geometry import box_geometry, is_small, make_small
 
 _KDT = (torch.bfloat16, torch.float32)
@@ -103,6 +103,10 @@ class HipOps(Backend):
     # the caller asks for) as one kernel (clarus_hip_ffn) for c = 32 / 64 channels (and 128 in bf16)
     # with weights of the activation dtype; False (or other shapes) runs its two linear ops.
     fuse_ffn = True
+    # linear_dwconv (NAFNet's conv1 with LayerNorm -> depthwise 3x3 -> SimpleGate, an explicit op the
+    # caller asks for) as one kernel (clarus_hip_ln_gemm_dwconv) for bf16 x of 64 channels; False (or
+    # other shapes) runs its two ops.
+    fuse_ln_dwconv = True
     # Short-K prologue GEMMs (K < split_min_k) on the ring streaming kernel round the prologue
     # output once to bf16 too (CLARUS_PRO_ROUND) instead of taking hi + lo pairs.
     round_short_prologue = False
@@ -132,6 +136,7 @@ class HipOps(Backend):
         # (clarus_hip_gemm_ln_rows) made by linear_ln_linear; counters only, never read by the dispatch
         self.pair_launches = {"gemm_ln_gemm": 0, "gemm_ln_rows": 0}
         self.ffn_launches = 0  # linear_gate_linear calls served by clarus_hip_ffn
+        self.ln_dw_launches = 0  # linear_dwconv calls served by clarus_hip_ln_gemm_dwconv
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -465,6 +470,45 @@ class HipOps(Backend):
             w2p.data_ptr(), _lib.ptr(self._bias(b2)), _lib.ptr(self._bias(scale)), x.numel() // c, c, pro,
             float(ln_eps), 1.0, self._stream(x)), "linear_gate_linear")
         self.ffn_launches += 1
+        return out
+
+    # ---- the first half of a NAFNet block (linear_dwconv)
+    @staticmethod
+    def _ln_dw_pack(w: torch.Tensor) -> torch.Tensor:
+        """w [64, 128] (linear layout) -> clarus_hip_ln_gemm_dwconv's fragment order:
+        w1p[T][s][l][i] = w[16 s + 8 (l // 32) + i][o(T, l % 32)], o(T, r) = 32 T + 16 (r // 16) +
+        8 ((r // 4) % 2) + 4 ((r // 8) % 2) + r % 4."""
+        k, n = w.shape
+        dv = w.device
+        lv = torch.arange(64, device=dv).view(1, 1, 64, 1)
+        t = torch.arange(n // 32, device=dv).view(-1, 1, 1, 1)
+        s = torch.arange(k // 16, device=dv).view(1, -1, 1, 1)
+        i = torch.arange(8, device=dv).view(1, 1, 1, 8)
+        r = lv % 32
+        o = 32 * t + 16 * (r // 16) + 8 * ((r // 4) % 2) + 4 * ((r // 8) % 2) + r % 4
+        return w[16 * s + 8 * (lv // 32) + i, o].contiguous()
+
+    def linear_dwconv(self, x, w, bias=None, dw_w=None, dw_b=None, ln=True, gate=True, ln_eps=1e-6):
+        """dwconv(linear(x, w, bias, ln=ln), dw_w, dw_b, gate=gate) (the first half of a NAFNet
+        block). One kernel (clarus_hip_ln_gemm_dwconv) for dense bf16 NHWC x with 64 channels, a
+        bf16 [64, 128] weight, LayerNorm and SimpleGate: the 128-channel intermediate stays in LDS,
+        rounded to bf16 as the 1x1 conv stores it. Otherwise the two ops."""
+        c = x.shape[-1] if x.dim() == 4 else 0
+        fits = (self.fuse_ln_dwconv and self.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and c == 64
+                and ln is True and gate is True and w.dtype == torch.bfloat16 and tuple(w.shape) == (64, 128)
+                and dw_w is not None and tuple(dw_w.shape) == (128, 1, 3, 3)
+                and (bias is None or tuple(bias.shape) == (128,)) and (dw_b is None or tuple(dw_b.shape) == (128,))
+                and _dense(x, w, bias, dw_b) and _vec16(x) and x.numel() * 2 < (1 << 31))
+        if not fits:
+            return linear_dwconv_unfused(self, x, w, bias, dw_w, dw_b, ln=ln, gate=gate, ln_eps=ln_eps)
+        w1p = self.cached(w, "lndw", self._ln_dw_pack)
+        taps = self.cached(dw_w, "dw9", lambda t: t.float().reshape(t.shape[0], 9).t().contiguous())
+        n, h, wd, _ = x.shape
+        out = torch.empty((n, h, wd, 64), device=x.device, dtype=torch.bfloat16)
+        _lib.check(self.lib.clarus_hip_ln_gemm_dwconv(
+            x.data_ptr(), out.data_ptr(), w1p.data_ptr(), _lib.ptr(self._bias(bias)), taps.data_ptr(),
+            _lib.ptr(self._bias(dw_b)), n, h, wd, c, float(ln_eps), self._stream(x)), "linear_dwconv")
+        self.ln_dw_launches += 1
         return out
 
     def down(self, x, w4d, b, out_dtype=None):

@@ -94,8 +94,9 @@ class NAFNet:
         # True: blocks of width pair_width send each residual GEMM and the LayerNorm GEMM on its
         # output to ops.linear_ln_linear (conv3 -> conv4, and conv5 -> the next block's conv1
         # within a stage), blocks of other widths their feed-forward half (conv4 -> SimpleGate ->
-        # conv5) to ops.linear_gate_linear; a backend may run each as one kernel. False: the
-        # reference block's five linear calls (models/nafnet/__init__.py:152-161), unchanged
+        # conv5) to ops.linear_gate_linear, and a conv1 not computed by such a pair goes with the
+        # depthwise conv after it to ops.linear_dwconv; a backend may run each as one kernel.
+        # False: the reference block's five linear calls (models/nafnet/__init__.py:152-161)
         self.fused_pairs = fused_pairs
         self.pair_width = 512
         self.dtype = ops.dtype
@@ -206,6 +207,19 @@ class NAFNet:
             return o.linear(u, w5, b5, scale=w[f"{p}.conv5.scale"], residual=y, out_dtype=self._rdt(level))
         return fn(y, w4, b4, w5, b5, scale=w[f"{p}.conv5.scale"], ln=True, out_dtype=self._rdt(level))
 
+    def _conv1_dw(self, x, p):
+        """ops.linear_dwconv on the block input (conv1 with LayerNorm, then the depthwise conv with
+        SimpleGate), or its two calls when no backend has the op."""
+        o, w = self.ops, self.w
+        args = (w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], w[f"{p}.dw.w"], w[f"{p}.dw.bias"])
+        try:
+            fn = o.linear_dwconv
+        except AttributeError:
+            fn = None
+        if fn is None:
+            return o.dwconv(o.linear(x, args[0], args[1], ln=True), args[2], args[3], gate=True)
+        return fn(x, *args, ln=True, gate=True)
+
     def _block(self, x, p, level, t=None, nxt=None):
         """One NAFBlock on x. t: its conv1 output when the previous block's fused op already
         computed it. nxt: the next block's key at the same width, whose conv1 (LayerNorm of this
@@ -213,8 +227,9 @@ class NAFNet:
         block's conv1 output or None)."""
         o, w = self.ops, self.w
         if t is None:
-            t = o.linear(x, w[f"{p}.conv1.w"], w[f"{p}.conv1.bias"], ln=True)
-        t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
+            t = self._conv1_dw(x, p)
+        else:
+            t = o.dwconv(t, w[f"{p}.dw.w"], w[f"{p}.dw.bias"], gate=True)
         sca = o.linear(o.boxmean(t, self.tlc_kernel(level)), w[f"{p}.sca.w"], w[f"{p}.sca.bias"])
         if x.shape[-1] != self.pair_width:
             y = o.linear(t, w[f"{p}.conv3.w"], w[f"{p}.conv3.bias"], scale=w[f"{p}.conv3.scale"], residual=x,

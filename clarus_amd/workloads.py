@@ -297,6 +297,33 @@ def nafnet_ffn_case(hip, device, seed: int = 0) -> OpCase:
                   lambda r_: run(r_, host))
 
 
+def nafnet_lndw_case(hip, device, seed: int = 0) -> OpCase:
+    """The NAFNet-w64 720p level-0 first half-block as one op (linear_dwconv: LN -> conv1 64 -> 128
+    -> depthwise 3x3 -> SimpleGate, bf16), two per forward. M = 921600: F = 2 M 64 128 (conv1) +
+    2 M 128 9 (depthwise) + M 64 (gate); B = 2 M 64 (x) + 2 M 64 (out) + 2 * 64 * 128 (weight) +
+    4 (128 + 9 * 128 + 128) (vectors, taps)."""
+    g = _gen(seed + 7)
+    m, c = 720 * 1280, 64
+    x = torch.randn(1, 720, 1280, c, generator=g).bfloat16()
+    w1 = _kaiming_uniform_kn(g, c, 2 * c).bfloat16()
+    b1 = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+    dw = (torch.rand(2 * c, 1, 3, 3, generator=g) * 2 - 1) / 3.0
+    dwb = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+    host = dict(x=x, w1=w1, b1=b1, dw=dw, dwb=dwb)
+    d = {n: t.to(device) for n, t in host.items()}
+
+    def run(r_=None, d=d):
+        from .dispatch import linear_dwconv_unfused
+        be = r_ or hip
+        fn = getattr(be, "linear_dwconv", None)
+        args = (d["x"], d["w1"], d["b1"], d["dw"], d["dwb"])
+        return fn(*args) if fn is not None else linear_dwconv_unfused(be, *args)
+    flops = 2.0 * m * c * 2 * c + 2.0 * m * 2 * c * 9 + m * c
+    nbytes = 2.0 * m * c * 2 + 2.0 * c * 2 * c + 4.0 * (2 * c + 9 * 2 * c + 2 * c)
+    return OpCase("nafnet L0 LN -> conv1 -> dwconv + gate (fused first half)", 0, "bf16", flops, nbytes, run, host,
+                  lambda r_: run(r_, host))
+
+
 def fftformer_dffn_case(hip, device, seed: int = 0) -> OpCase:
     """FFTformer level-0 DFFN project_in + frequency filter at 720p as one op (linear_patch_filter:
     LayerNorm eps 1e-5 -> 1x1 conv 48 -> 288 + bias -> per-patch rfft2 * filter -> irfft2, bf16),
@@ -372,11 +399,12 @@ def metrics_case(device, seed: int = 0) -> OpCase:
 
 def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
     """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5,
-    the fused FFTformer DFFN op, the fused NAFNet pair and feed-forward half, EVSSM's scan and the
-    metrics."""
+    the fused FFTformer DFFN op, the fused NAFNet pair, feed-forward half and first half, EVSSM's
+    scan and the metrics."""
     return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
             + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
             + config5_cases(hip_bf16, device, seed) + [fftformer_dffn_case(hip_bf16, device, seed),
                                                         nafnet_pair_case(hip_bf16, device, seed),
                                                         nafnet_ffn_case(hip_bf16, device, seed),
+                                                        nafnet_lndw_case(hip_bf16, device, seed),
                                                         evssm_scan_case(hip_bf16, device, seed), metrics_case(device, seed)])

@@ -162,6 +162,23 @@ int clarus_hip_ffn(const void* x, void* out, int dtype, const void* w1p, const f
                    float out_scale, void* stream);
 
 /*
+ * The first half of a NAFNet block at width 64 as one kernel, for bf16 NHWC x [n][h][w][64]:
+ *   t   = LN(x) . w1 + b1                 w1 [64][128] (linear layout), t rounded to bf16
+ *   out = SimpleGate(dwconv3x3(t) + dwb)  taps [9][128] fp32 (tap = 3 ky + kx), 'same' zero
+ *                                         padding, out [n][h][w][64] bf16
+ * The LayerNorm (no affine, eps ln_eps) enters the product as bf16 hi + lo pairs; b1, dwb: fp32
+ * [128] or null. out must not overlap x; n h w 64 bf16 elements must fit 2 GiB. w1p is w1 packed:
+ *   w1p[T][s][l][i] = w1[16 s + 8 (l / 32) + i][o(T, l % 32)]   T < 4, s < 4, l < 64, i < 8
+ *   o(T, r) = 32 T + 16 (r / 16) + 8 ((r / 4) % 2) + 4 ((r / 8) % 2) + r % 4
+ * No counterpart in the reference: it composes `linear` (ln=True) and `dwconv` (gate=True),
+ * models/nafnet/__init__.py:155-156 (ops/triton_cuda.py:84-112 and the dwconv op), for hosts
+ * that run them back to back.
+ */
+int clarus_hip_ln_gemm_dwconv(const void* x, void* out, const void* w1p, const float* b1, const float* taps,
+                              const float* dwb, int64_t n, int64_t h, int64_t w, int64_t c, float ln_eps,
+                              void* stream);
+
+/*
  * Prologue pass of the split-operand GEMM path. Applies the prologue of args (pro = LN, RMS
  * or the TLC map multiply, with its eps / map geometry; a, lda, m, k, a_dtype) to every row in
  * fp32 and writes out[r] = [hi(0..k) | lo(0..k)], bf16, 2k elements per row, hi = bf16(v),

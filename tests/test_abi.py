@@ -106,6 +106,16 @@ def test_validation_rejects_before_launch(lib):
     assert ffn(1 << 20, (1 << 20) + 4096, _lib.BF16, 16, None, 16, None, None, 64, 64, 0, 0.0, 1.0, None) == _lib.EINVAL
     assert b"overlap" in lib.clarus_hip_last_error()
     assert ffn(None, 16, _lib.F32, 16, None, 16, None, None, 64, 32, 0, 0.0, 1.0, None) == _lib.EINVAL
+    # clarus_hip_ln_gemm_dwconv: 64 channels only, alignment, overlap, size
+    lndw = lib.clarus_hip_ln_gemm_dwconv
+    assert lndw(16, 1 << 24, 16, None, 16, None, 1, 8, 8, 128, 1e-6, None) == _lib.EINVAL
+    assert b"c = 64 only" in lib.clarus_hip_last_error()
+    assert lndw(24, 1 << 24, 16, None, 16, None, 1, 8, 8, 64, 1e-6, None) == _lib.EINVAL
+    assert b"16-byte" in lib.clarus_hip_last_error()
+    assert lndw(1 << 20, (1 << 20) + 4096, 16, None, 16, None, 1, 8, 8, 64, 1e-6, None) == _lib.EINVAL
+    assert b"overlap" in lib.clarus_hip_last_error()
+    assert lndw(16, 1 << 24, 16, None, 16, None, 1, 1 << 14, 1 << 14, 64, 1e-6, None) == _lib.EINVAL
+    assert lndw(16, 1 << 24, None, None, 16, None, 1, 8, 8, 64, 1e-6, None) == _lib.EINVAL
     assert lib.clarus_hip_channel_attention_workspace(1, 0, 48, 1) == 0
     assert lib.clarus_hip_channel_attention_workspace(1, 921600, 48, 1) > 0
 

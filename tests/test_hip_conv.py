@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _tol import assert_bf16, assert_fp32
+from _tol import BF16_ABS, assert_bf16, assert_fp32, bf16_ulp
 from oracle.torch_ref import TorchRef
 
 pytestmark = pytest.mark.gpu
@@ -240,6 +240,62 @@ def test_dwconv_bf16_in_fp32_out(hip_bf16):
         torch.cuda.synchronize()
         ref = TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=bool(gate))
         assert_fp32(out.cpu(), ref, what=f"dwconv bf16 -> fp32 gate={gate}")
+
+
+@pytest.mark.parametrize("n,h,w,full", [(2, 13, 37, True), (1, 5, 3, False), (1, 6, 30, True),
+                                        (1, 720, 1280, True)])
+def test_linear_dwconv(n, h, w, full, hip_bf16):
+    """linear_dwconv on clarus_hip_ln_gemm_dwconv (NAFNet level-0 first half: LN -> 64 -> 128 ->
+    depthwise 3x3 -> SimpleGate): partial tiles at both image edges, an image smaller than one
+    tile, exactly one tile, two images, biases absent, and 720p. The oracle runs the two ops with
+    the 1x1 conv's output rounded to bf16 as the unfused path stores it (fp32 products: the kernel
+    feeds the LayerNorm rows as hi + lo pairs)."""
+    from clarus_amd import _lib
+    g = gen(14)
+    x = (rnd(g, n, h, w, 64) + 0.3).bfloat16()
+    wt = (rnd(g, 64, 128) / 8).bfloat16()
+    b = rnd(g, 128, scale=0.1) if full else None
+    dw, dwb = rnd(g, 128, 1, 3, 3, scale=0.3), (rnd(g, 128, scale=0.1) if full else None)
+    got = hip_bf16.linear_dwconv(x.cuda(), wt.cuda(), None if b is None else b.cuda(), dw.cuda(),
+                                 None if dwb is None else dwb.cuda())
+    assert _lib.last_kernel().startswith("ln_dw_kernel"), _lib.last_kernel()
+    check_linear_dwconv(got.cpu(), x, wt, b, dw, dwb, f"linear_dwconv {n}x{h}x{w}")
+
+
+def check_linear_dwconv(got, x, wt, b, dw, dwb, what):
+    """got (bf16) against the oracle's two ops with t rounded to bf16. The kernel rounds its own t,
+    summed in another order, so an element of t may sit one bf16 step from the oracle's (a rounding
+    flip of the intermediate); elementwise the difference is held to what such flips can cause,
+    |a1| e2 + |a2| e1 + e1 e2 with e = |taps| * ulp(t) through the depthwise conv (a1, a2: the gate
+    halves), plus one output rounding step. Elements beyond 2e-2 of the output scale may only be
+    such flips, at most 1e-3 of them."""
+    ref32 = TorchRef(torch.float32, "cpu")
+    t32 = ref32.linear(x, wt, b, ln=True)
+    t = t32.bfloat16()
+    ref = ref32.dwconv(t, dw, dwb, gate=True).double()
+    a = ref32.dwconv(t, dw, dwb, gate=False).double()
+    e = ref32.dwconv(bf16_ulp(t32.float()), dw.abs(), None, gate=False).double()
+    c = a.shape[-1] // 2
+    a1, a2, e1, e2 = a[..., :c], a[..., c:], e[..., :c], e[..., c:]
+    bound = a1.abs() * e2 + a2.abs() * e1 + e1 * e2 + bf16_ulp(ref.float()).double() + 1e-5 * ref.abs().max()
+    d = (got.double() - ref).abs()
+    assert bool((d <= bound).all()), f"{what}: {int((d > bound).sum())} elements beyond the bound; max {d.max():.3e}"
+    far = int((d > BF16_ABS * ref.abs().clamp_min(1.0)).sum())
+    assert far <= max(1, 1e-3 * d.numel()), f"{what}: {far} elements beyond 2e-2 of their scale"
+    print(f"[linear_dwconv] {what}: max |d| {d.max():.3e}, {far} beyond 2e-2 of their scale")
+
+
+def test_linear_dwconv_unfused_shapes(hip_bf16):
+    """Shapes the fused kernel does not take (128 channels) run the two ops, bit for bit."""
+    from clarus_amd import _lib
+    g = gen(15)
+    x = rnd(g, 1, 9, 11, 128, dtype=torch.bfloat16).cuda()
+    wt, b = (rnd(g, 128, 256) / 11).bfloat16().cuda(), rnd(g, 256).cuda()
+    dw, dwb = rnd(g, 256, 1, 3, 3).cuda(), rnd(g, 256).cuda()
+    got = hip_bf16.linear_dwconv(x, wt, b, dw, dwb)
+    assert not _lib.last_kernel().startswith("ln_dw_kernel")
+    want = hip_bf16.dwconv(hip_bf16.linear(x, wt, b, ln=True), dw, dwb, gate=True)
+    assert torch.equal(got, want)
 
 
 def test_dwconv_nafnet_720p(hip_bf16):

@@ -356,6 +356,32 @@ def test_ffn_fragment_packing(c, kp):
     np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10 * np.abs(want).max())  # fp64 summation order
 
 
+def test_ln_dw_fragment_packing():
+    """clarus_hip_ln_gemm_dwconv's 1x1 conv, emulated lane by lane on the packed weight
+    (HipOps._ln_dw_pack) with 32x32x16 MFMAs as the lanes feed them: B operand = the lane's x
+    fragments (pixel l % 32, channels 16 s + 8 (l // 32) ..), accumulator element j of output block
+    T = channel 32 T + 16 (j // 8) + 8 (l // 32) + j % 8 of the lane's pixel, as the kernel writes
+    the t tile. Exact arithmetic must give x w for one 32-pixel row."""
+    from clarus_amd.hip_ops import HipOps
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(32, 64, generator=g, dtype=torch.float64)
+    w = torch.randn(64, 128, generator=g, dtype=torch.float64)
+    want = (x @ w).numpy()
+    wp = HipOps._ln_dw_pack(w).numpy()
+    assert wp.shape == (4, 4, 64, 8)
+    xn = x.numpy()
+    xf = np.concatenate([np.stack([xn[l % 32, 16 * s + 8 * (l // 32):16 * s + 8 * (l // 32) + 8] for l in range(64)])
+                         for s in range(4)], 1)  # [64, 32]: step s in columns 8 s .. 8 s + 7
+    got = np.zeros((32, 128))
+    for t in range(4):
+        wt = np.concatenate([wp[t, s] for s in range(4)], 1)
+        acc = sum(_mfma32(wt[:, q:q + 8], xf[:, q:q + 8]) for q in range(0, 32, 8))
+        for l in range(64):
+            for j in range(16):
+                got[l % 32, 32 * t + 16 * (j // 8) + 8 * (l // 32) + j % 8] = acc[l, j]
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10 * np.abs(want).max())
+
+
 def test_linear_gate_linear_unfused_is_two_linears():
     """Backends without the fused kernel run linear_gate_linear as its two linear ops: the gated
     LN GEMM, then the second GEMM with the scale and the input as residual."""
@@ -406,6 +432,7 @@ def test_pair_default_for_a_host_backend_base():
     dispatch.give_pair_default(HostBase)
     assert HostBase.linear_ln_linear is dispatch.linear_ln_linear_unfused
     assert HostBase.linear_gate_linear is dispatch.linear_gate_linear_unfused
+    assert HostBase.linear_dwconv is dispatch.linear_dwconv_unfused
 
     class Own(HostBase):
         def linear_ln_linear(self, *a, **k):
@@ -423,7 +450,7 @@ class _PlainOracle:
         self._r = TorchRef(dtype, device)
 
     def __getattr__(self, op):
-        if op.startswith("_") or op in ("linear_ln_linear", "linear_gate_linear"):
+        if op.startswith("_") or op in ("linear_ln_linear", "linear_gate_linear", "linear_dwconv"):
             raise AttributeError(op)
         return getattr(self._r, op)
 
@@ -445,6 +472,6 @@ def test_nafnet_pairs_match_the_reference_call_pattern():
         model.pair_width = 16  # the enc1 / dec0 width of this model (512 at NAFNet-w64 level 3)
         outs.append(model.forward(x))
         calls = ops.report()["ops"]
-        for op in ("linear_ln_linear", "linear_gate_linear"):
+        for op in ("linear_ln_linear", "linear_gate_linear", "linear_dwconv"):
             assert (op in calls) == (fused and backend == "oracle_by_path"), (op, calls)
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])

@@ -8,9 +8,9 @@ Every GEMM-family op of the forward must have been served by `hip`. With the har
 calls, every level-3 pair (linear_ln_linear) must have run as one fused kernel: 29 conv3 -> conv4
 pairs (28 encoder blocks and one decoder block at width 512) and 27 conv5 -> next conv1 pairs
 (within the 28-block encoder stage), 56 per forward; and so must the feed-forward half
-(linear_gate_linear) of the level-0 and level-1 blocks (widths 64 and 128), 4 per forward. The
-reference's unchanged block (five linear calls, fused_pairs=False) is held to the same PSNR
-criterion.
+(linear_gate_linear) of the level-0 and level-1 blocks (widths 64 and 128), 4 per forward, and
+the level-0 conv1 -> depthwise conv (linear_dwconv), 2 per forward. The reference's unchanged
+block (five linear calls, fused_pairs=False) is held to the same PSNR criterion.
 """
 from __future__ import annotations
 
@@ -28,6 +28,7 @@ pytestmark = pytest.mark.gpu
 GEMM_OPS = {"linear", "down", "up", "intro", "ending"}
 FUSED_PAIRS_PER_FORWARD = 29 + 27
 FUSED_FFN_PER_FORWARD = 4  # levels 0 and 1: encoder block and decoder block each
+FUSED_LN_DW_PER_FORWARD = 2  # level 0 conv1 -> depthwise conv: encoder block and decoder block
 
 
 class _OracleBackend(Backend):
@@ -65,10 +66,11 @@ def test_nafnet_w64_psnr_parity(h, w, fused, gpu_device):
     print(f"NAFNet-w64 {h}x{w}: PSNR hip {p_hip:.5f} dB, oracle {p_ref:.5f} dB, |dPSNR| {abs(p_hip - p_ref):.2e}, "
           f"max|dy| {diff:.3e}, output range [{y_ref.min().item():.3f}, {y_ref.max().item():.3f}]")
     served = ops_hip.report()["ops"]
-    for op in GEMM_OPS | ({"linear_ln_linear", "linear_gate_linear"} if fused else set()):
+    for op in GEMM_OPS | ({"linear_ln_linear", "linear_gate_linear", "linear_dwconv"} if fused else set()):
         assert list(served.get(op, {"hip": 0})) == ["hip"], (op, served.get(op))
     launches = ops_hip.by_name["hip"].pair_launches
     assert launches == {"gemm_ln_gemm": FUSED_PAIRS_PER_FORWARD if fused else 0, "gemm_ln_rows": 0}, launches
     assert ops_hip.by_name["hip"].ffn_launches == (FUSED_FFN_PER_FORWARD if fused else 0)
+    assert ops_hip.by_name["hip"].ln_dw_launches == (FUSED_LN_DW_PER_FORWARD if fused else 0)
     assert ("linear_ln_linear" in served) == fused and ("linear_gate_linear" in served) == fused
     assert abs(p_hip - p_ref) <= 1e-3
