@@ -249,6 +249,20 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                          cdiv(a->m, 128) * cdiv(a->n, a->gate ? 64 : 128) < 192;
   const bool auto_dma = a->tile == 0 && plain_bf16 && a->k > 128 && a->k % 32 == 0 && (a->lda * 2) % 16 == 0 &&
                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0) && !few_tiles;
+  // W-slice kernel (tile 18 forces it): plain problems without residual, gate or activation and
+  // up to 80 K rows (the NAFNet SCA GEMMs on the TLC map, us, HIP events, cold / warm:
+  // M = 4859, K = N = 512: 15.5 / 13.6 against 16.8 / 15.5 on the best tiled kernel;
+  // 19125 x 256: 13.7 / 11.9 vs 16.8 / 14.4; 75881 x 128: 14.0 / 12.8 vs 17.4 / 16.4)
+  {
+    const bool slice_shape = plain_bf16 && !a->gate && !a->res && a->act == ACT_NONE &&
+                             a->c_mode == CLARUS_C_ROWS && gemm_slice_fits(p);
+    CLARUS_REQUIRE(a->tile != 18 || slice_shape, "gemm: the W-slice kernel does not take this problem");
+    if (a->tile == 18 || (a->tile == 0 && slice_shape && a->m <= 80000)) {
+      note_kernel("gemm_slice_kernel k=%lld c=%s", (long long)a->k, a->c_dtype == DT_BF16 ? "bf16" : "f32");
+      CLARUS_REQUIRE(launch_gemm_slice(p, (hipStream_t)stream), "gemm: W-slice launch");
+      return check_launch("gemm");
+    }
+  }
   int tile_override = 0;
   if (a->tile == 0 && plain_bf16 && a->res && a->k <= 128 && (!run_div || run_div % 16 == 0)) tile_override = 3;
   if (few_tiles) tile_override = 3;

@@ -22,6 +22,12 @@ void launch_gemm_big(GemmP& p, bool gate, int wp, hipStream_t s);
 // number of gemm_big_kernel tiles of a problem
 int64_t gemm_big_tiles(int64_t m, int64_t n, bool gate, int wp);
 
+// gemm_slice_kernel (bf16 A and W rows, no prologue / gate / act / residual, row output): K of
+// 128, 256 or 512, N % 64 == 0, 16-byte output vectors. launch_gemm_slice returns false when p
+// does not fit.
+bool gemm_slice_fits(const GemmP& p);
+bool launch_gemm_slice(const GemmP& p, hipStream_t s);
+
 // Launches conv_halo_kernel for p (bf16 x and weights, cin % 32 == 0, row output). Returns
 // false when the resident weights of even a 32-channel tile do not fit in LDS.
 bool launch_conv_halo(GemmP& p, hipStream_t s);

@@ -109,7 +109,8 @@ typedef struct ClarusGemmArgs {
                          13 DMA-pipelined 32x32-MFMA tile (bf16 A, no prologue, K % 64 == 0),
                          14 / 15 the same with 256 / 128 pixels x 256 channels per tile,
                          16 / 17 streaming with a per-wave LDS ring (K <= 128 bf16 / 64 fp32;
-                         17: 4 channel blocks per workgroup) */
+                         17: 4 channel blocks per workgroup), 18 W-slice (bf16 A and W, no
+                         prologue / gate / act / residual, K = 128 / 256 / 512, N % 64 == 0) */
 } ClarusGemmArgs;
 
 /* replaces kernels/gemm.py:353-400 fused_gemm and :403-429 _gemm_wide */

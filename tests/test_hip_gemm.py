@@ -420,6 +420,48 @@ def test_ring_streaming_kernel(adt, wdt, gate, rdt, k, nout, batch, hip_bf16):
     assert_fp32(out.cpu(), ref, rel=1e-5, what=f"ring streaming A {adt} W {wdt} gate {gate} res {rdt} K{k} N{nout}")
 
 
+@pytest.mark.parametrize("m,k,n,cdt,lda,ldc,bias,scale,tile", [
+    (4859, 512, 512, torch.bfloat16, 512, 512, True, False, 0),      # NAFNet level-3 SCA GEMM (auto)
+    (37, 128, 64, torch.float32, 128, 80, True, True, 18),          # one group, wider output rows
+    (1, 256, 128, torch.bfloat16, 256, 128, False, False, 18),       # a single row
+    (3001, 512, 192, torch.float32, 528, 192, True, True, 18),      # wider A rows, 3 slices
+    (20000, 256, 256, torch.bfloat16, 256, 256, True, False, 18),    # several groups per workgroup
+    (75881, 128, 128, torch.bfloat16, 128, 128, True, False, 0),     # NAFNet level-1 SCA GEMM (auto)
+])
+def test_slice_kernel(m, k, n, cdt, lda, ldc, bias, scale, tile, hip_bf16):
+    """Through the C ABI, the W-slice kernel (tile 18, and the library's own choice for the SCA
+    shape): K = 128 / 256 / 512, bias, per-channel scale times out_scale, bf16 / fp32 output,
+    ragged pixel counts (partial last unit and unit group), strided A and C rows."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(47)
+    xa = rnd(g, m, lda, dtype=torch.bfloat16)
+    wt = rnd(g, n, k, scale=k ** -0.5, dtype=torch.bfloat16)
+    b = rnd(g, n) if bias else None
+    sc = rnd(g, n) if scale else None
+    out_scale = 0.5 if scale else 1.0
+    ref = REF.linear(xa[:, :k].contiguous(), wt.t().contiguous(), b, scale=sc) * out_scale
+    out = torch.full((m, ldc), 7.0, device="cuda", dtype=cdt)
+    xd, wd = xa.cuda(), wt.cuda()
+    bd, sd = (b.cuda() if b is not None else None), (sc.cuda() if sc is not None else None)
+    args = _lib.GemmArgs(a=xd.data_ptr(), wt=wd.data_ptr(), c=out.data_ptr(), bias=_lib.ptr(bd),
+                         scale=_lib.ptr(sd), m=m, n=n, k=k, batch=1, lda=lda, ldc=ldc,
+                         a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(cdt),
+                         out_scale=out_scale, tile=tile)
+    _lib.check(lib.clarus_hip_gemm(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "gemm")
+    assert _lib.last_kernel().startswith("gemm_slice_kernel"), _lib.last_kernel()
+    got = out.cpu()
+    assert torch.all(got[:, n:] == 7.0), "columns past N written"
+    what = f"W-slice GEMM M{m} K{k} N{n} {cdt}"
+    if cdt == torch.bfloat16:
+        assert_bf16(got[:, :n], ref, what)
+    else:
+        assert_fp32(got[:, :n], ref, rel=1e-5, what=what)
+
+
 def test_up_long_k(hip_bf16):
     """1x1 conv + PixelShuffle(2) with K = 256 (the DMA-pipelined kernels' store addressing)."""
     g = gen(36)
