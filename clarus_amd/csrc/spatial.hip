@@ -153,7 +153,6 @@ struct BoxPass {
   double scale;       // 1 / (k1 k2) on the final pass, 1 otherwise
 };
 
-constexpr int BOX_BATCH = 8;  // rows loaded per batch and stream (loads in flight per thread)
 
 // channel c of a raw 16-byte load: 8 bf16 or 4 fp32
 template <int DT>
@@ -166,8 +165,11 @@ __device__ __forceinline__ float raw_elem(const u32x4& q, int c) {
   }
 }
 
-template <int XDT, int YDT>
+// NB: rows loaded per batch and stream (loads in flight per thread); with NB >= R a thread's
+// rows are loaded once and stay in registers through the recurrence
+template <int XDT, int YDT, int NB>
 __global__ void __launch_bounds__(256) box_pass_kernel(const BoxPass p) {
+  constexpr int BOX_BATCH = NB;
   constexpr int E = XDT == DT_BF16 ? 8 : 4;  // channels per 16-byte load
   constexpr int XES = XDT == DT_BF16 ? 2 : 4;
   constexpr int YES = YDT == DT_BF16 ? 2 : 4;
@@ -316,9 +318,19 @@ extern "C" int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int
     q.scale = scale;
     const int64_t blocks = outer * q.nblk * q.nqg;
     if (blocks >= ((int64_t)1 << 31)) return false;
-    if (sdt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_BF16, DT_F32>), dim3((unsigned)blocks), dim3(256), 0, s, q);
-    else if (ddt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_BF16>), dim3((unsigned)blocks), dim3(256), 0, s, q);
-    else hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_F32>), dim3((unsigned)blocks), dim3(256), 0, s, q);
+    // rows per batch: 8, the rows reloaded for the recurrence when R > 8; all R rows kept in
+    // registers (one wave per SIMD) where that measured faster, us: bf16 rows with R = 24 (NAFNet
+    // level 0, vertical pass) 64.0 vs 70-74, fp32 rows with R = 12 (level 1, horizontal) 28.3 vs
+    // 30.4; not kept: bf16 R = 12 (level 1 vertical) 39.1 vs 30-31, fp32 R = 24 64.1 vs 59.4
+    const int nb = (sdt == DT_BF16 && q.R > 16 && q.R <= 24) ? 24 : (sdt == DT_F32 && q.R > 8 && q.R <= 16) ? 16 : 8;
+#define CLARUS_BOX_LAUNCH(NB_)                                                                             \
+  if (sdt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_BF16, DT_F32, NB_>), dim3((unsigned)blocks), dim3(256), 0, s, q); \
+  else if (ddt == DT_BF16) hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_BF16, NB_>), dim3((unsigned)blocks), dim3(256), 0, s, q); \
+  else hipLaunchKernelGGL((box_pass_kernel<DT_F32, DT_F32, NB_>), dim3((unsigned)blocks), dim3(256), 0, s, q);
+    if (nb == 8) { CLARUS_BOX_LAUNCH(8) }
+    else if (nb == 16) { CLARUS_BOX_LAUNCH(16) }
+    else { CLARUS_BOX_LAUNCH(24) }
+#undef CLARUS_BOX_LAUNCH
     return true;
   };
   // vertical: planes are images, lines the (x, c) columns; horizontal: planes are V rows

@@ -336,11 +336,14 @@ def test_boxmean_exact_float64():
     assert ((got - ref).abs() / ref.abs()).max().item() < 2e-7
 
 
-def test_boxmean_nafnet_level0(hip_bf16):
-    """NAFNet-w64 level 0: 1 x 720 x 1280 x 64 bf16, window 384 (map 337 x 897)."""
+@pytest.mark.parametrize("h,w,c,k", [(720, 1280, 64, 384), (360, 640, 128, 192)])
+def test_boxmean_nafnet_levels(h, w, c, k, hip_bf16):
+    """NAFNet-w64 levels 0 and 1 at 720p: windows 384 / 192 (maps 337 x 897 / 169 x 449); the
+    passes that keep all of a thread's rows in registers (24 bf16 rows of the vertical pass at
+    level 0, 12 fp32 rows of the horizontal pass at level 1)."""
     g = gen(12)
-    x = rnd(g, 1, 720, 1280, 64, dtype=torch.bfloat16)
-    got = hip_bf16.boxmean(x.cuda(), 384)
-    ref = TorchRef(torch.float32, "cpu").boxmean(x, 384)
-    assert got.data.shape == (1, 337, 897, 64)
-    check(got.data.cpu(), ref.data.float(), "boxmean level 0")
+    x = rnd(g, 1, h, w, c, dtype=torch.bfloat16)
+    got = hip_bf16.boxmean(x.cuda(), k)
+    ref = TorchRef(torch.float32, "cpu").boxmean(x, k)
+    assert got.data.shape == (1, h - k + 1, w - k + 1, c)
+    check(got.data.cpu(), ref.data.float(), f"boxmean {h}x{w} k={k}")
