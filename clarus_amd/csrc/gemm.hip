@@ -251,8 +251,9 @@ extern "C" int clarus_hip_gemm(const ClarusGemmArgs* a, void* stream) {
                         (!run_div || run_div % gemm_lds_run(a->gate != 0) == 0) && !few_tiles;
   // W-slice kernel (tile 18 forces it): plain problems without residual, gate or activation and
   // up to 80 K rows (the NAFNet SCA GEMMs on the TLC map, us, HIP events, cold / warm:
-  // M = 4859, K = N = 512: 15.5 / 13.6 against 16.8 / 15.5 on the best tiled kernel;
-  // 19125 x 256: 13.7 / 11.9 vs 16.8 / 14.4; 75881 x 128: 14.0 / 12.8 vs 17.4 / 16.4)
+  // M = 4859, K = N = 512: 12.8 / 11.2 against 17.0 / 15.4 on the DMA tile kernel and 15.8 / 13.6
+  // on the weight-streaming one; 19125 x 256: 14.0 / 12.1 vs 15.6 / 13.7 (W-resident kernel);
+  // 75881 x 128: 16.0 / 12.9 vs 17.4 / 16.4 (streaming kernel))
   {
     const bool slice_shape = plain_bf16 && !a->gate && !a->res && a->act == ACT_NONE &&
                              a->c_mode == CLARUS_C_ROWS && gemm_slice_fits(p);

@@ -6,9 +6,9 @@
 // problem has too few 128 x 128 output tiles to fill 256 CUs, and every K = 512 tile spends
 // most of its time filling and draining a copy pipeline that never reaches a steady state.
 //
-// Here a workgroup (4 waves, one per CU) holds one slice of 64 output channels of W^T in LDS
+// Here a workgroup (8 waves, one per CU) holds one slice of 64 output channels of W^T in LDS
 // (64 rows x K bf16, 64 KiB at K = 512) and each wave computes whole 32-pixel units against it.
-// A unit's A rows reach the wave's LDS slot in pieces of up to 256 k (16 KiB) by direct
+// A unit's A rows reach the wave's LDS slot in pieces of up to 128 k (8 KiB) by direct
 // global -> LDS copies of whole row segments, the wave reads its fragments of a piece into
 // registers and refills the slot with the next piece at once, so one piece is in flight while
 // one is computed. The W rows are copied the same way, row by row. (Loading the fragments
@@ -31,10 +31,10 @@ namespace {
 
 constexpr int GS_P = 32;  // pixels per unit
 constexpr int GS_N = 64;  // output channels per workgroup
-constexpr int GS_W = 4;   // waves per workgroup
+constexpr int GS_W = 8;   // waves per workgroup (two per SIMD)
 
 // k per A piece, pieces per unit, bytes per piece, LDS bytes (W slice | tables | 4 slots)
-__host__ __device__ constexpr int gs_pk(int ks) { return ks * 16 < 256 ? ks * 16 : 256; }
+__host__ __device__ constexpr int gs_pk(int ks) { return ks * 16 < 128 ? ks * 16 : 128; }
 __host__ __device__ constexpr int gs_piece_bytes(int ks) { return GS_P * gs_pk(ks) * 2; }
 __host__ __device__ constexpr int gs_lds_bytes(int ks) {
   return GS_N * ks * 16 * 2 + 2 * GS_N * 4 + GS_W * gs_piece_bytes(ks);
