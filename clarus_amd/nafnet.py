@@ -330,8 +330,8 @@ def bench_forward(dev, reps: int = 20, fused_pairs: bool = True, log=print) -> d
     res = {"ms": round(statistics.median(times), 3), "eager_ms": round(statistics.median(eager), 3),
            "reps": reps, "input": "1x3x720x1280 fp32 U(0,1), seeded", "dtype": "bf16",
            "model": "NAFNetLocal w64 enc[1,1,1,28] mid1 dec[1,1,1,1], random init",
-           "block": ("fused ops: linear_ln_linear pairs (width 512), linear_gate_linear (other widths)" if fused_pairs
-                     else "reference block: five linear calls"),
+           "block": ("fused ops: linear_ln_linear pairs (width 512), linear_gate_linear (other widths), "
+                     "linear_dwconv (width 64)" if fused_pairs else "reference block: five linear calls"),
            "served": served, "finite": bool(torch.isfinite(y).all().item())}
     log(f"[bench] NAFNet-w64 720p bf16 forward ({res['block']}): graph {res['ms']} ms, eager {res['eager_ms']} ms")
     return res
