@@ -523,16 +523,66 @@ def main() -> None:
             e2e["cpu"] = legs["e2e"]
         log(f"[bench] cpu baseline {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['ms_per_step']} ms/step)")
 
-    line = {
+    head = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) activations, random-init weights)",
         "config": {"workload": "BASELINE config 2: NAFNet-w64 720p pointwise GEMMs (expand+gate and c->c+scale+res "
                                "at c=64..1024), bf16 operands, fp32 accumulate", "global_batch": 1,
                    "parallelism": "none (1 GPU)"},
-        "roofline": roofline, "cpu_baseline": cpu, "per_op": rows, "nafnet_e2e": e2e,
+        "roofline": roofline, "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    detail = os.path.join(ROOT, "gpurun_out", "bench_per_op.json")
+    try:
+        os.makedirs(os.path.dirname(detail), exist_ok=True)
+        with open(detail, "w") as fh:
+            json.dump(_finite({**head, "per_op": rows, "nafnet_e2e": e2e}), fh, indent=1)
+    except OSError as e:
+        log(f"[bench] could not write {detail}: {e}")
+        detail = None
+    print(final_line(head, rows, e2e, detail), flush=True)
+
+
+LINE_LIMIT = 7000  # the driver keeps the last 8000 characters of stdout; the line must fit whole
+PER_OP_COLS = ["op", "us", "tflops", "bound", "frac", "traffic_ratio", "cpu_ms"]
+
+
+def _finite(obj):
+    """obj with every non-finite float replaced by None (strict JSON has no NaN / Infinity)."""
+    if isinstance(obj, float):
+        return obj if obj == obj and abs(obj) != float("inf") else None
+    if isinstance(obj, dict):
+        return {k: _finite(v) for k, v in obj.items()}
+    if isinstance(obj, (list, tuple)):
+        return [_finite(v) for v in obj]
+    return obj
+
+
+def final_line(head: dict, rows: list, e2e: dict | None, detail: str | None) -> str:
+    """The one JSON line bench.py prints: the required keys, roofline and cpu_baseline, the per-op
+    rows as short tuples (PER_OP_COLS) and the NAFNet e2e figures, kept under LINE_LIMIT
+    characters (op names are shortened first, then the per-op rows dropped, if it does not fit).
+    The full rows go to `detail`."""
+    line = dict(head)
+    if e2e is not None:
+        ref, fused, cpu = e2e.get("reference_block"), e2e.get("fused_pairs"), e2e.get("cpu")
+        line["nafnet_e2e"] = {
+            "ms": ref and ref["ms"], "eager_ms": ref and ref["eager_ms"],
+            "block": "reference block (five linear calls), graph replay median",
+            "fused_ops_ms": fused and fused["ms"], "cpu_ms": cpu and cpu["ms"],
+            "cpu_threads": cpu and cpu["threads"],
+            "all_hip": all(v == ["hip"] for p in (ref, fused) if p for k, v in p["served"].items()
+                           if k not in ("pixel_shuffle", "pixel_unshuffle", "add_scaled")),
+        }
+    line["per_op_cols"] = PER_OP_COLS
+    line["per_op_file"] = detail and os.path.relpath(detail, ROOT)
+    for width in (60, 32, 0):
+        line["per_op"] = [[r["op"][:width] if c == "op" else r.get(c) for c in PER_OP_COLS] for r in rows] \
+            if width else None
+        text = json.dumps(_finite(line), allow_nan=False, separators=(",", ":"))
+        if len(text) <= LINE_LIMIT:
+            return text
+    raise RuntimeError(f"bench line of {len(text)} characters even without per-op rows")
 
 
 if __name__ == "__main__":

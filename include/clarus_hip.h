@@ -291,7 +291,7 @@ int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, vo
  * dtype qkv_dtype; out fp32 [batch, heads, c_h, c_h]; temperature fp32 [heads].
  * The pixel reduction is split over workgroups (deterministic two-stage sum); scratch must
  * hold clarus_hip_channel_attention_workspace(...) bytes.
- * replaces kernels/attention.py:252-270 gram + ops/triton_cuda.py:174-181
+ * replaces kernels/attention.py:48-66 gram (gram_kernel :14-45) + ops/triton_cuda.py:174-181
  */
 size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads);
 int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature,
