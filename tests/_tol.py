@@ -54,3 +54,24 @@ def assert_bf16(got, ref32, what="", max_flip_frac=1e-3):
                                      f"rounding flips; max |d| {d.max().item():.3e}")
         assert n_over <= max(1, max_flip_frac * d.numel()), f"{what}: {n_over} rounding flips"
     return d.max().item(), n_over
+
+
+def assert_abs(got, ref32, tol=BF16_ABS, what="", ulps=0.5):
+    """The bf16 tolerance stated against the fp32 oracle: |got - ref32| <= tol absolute for every
+    element, on top of the output's own rounding when got is bf16 (`ulps` bf16 ulps of ref32:
+    half an ulp for one rounding of the output; no rounding of a bf16 output can stay within 2e-2
+    of an fp32 value above 8, whose bf16 neighbours are 1/16 apart). Returns max|got - ref32|."""
+    assert got.shape == ref32.shape, f"{what}: shape {tuple(got.shape)} vs {tuple(ref32.shape)}"
+    g = got.reshape(-1).cpu()
+    r = ref32.reshape(-1).cpu()
+    worst, excess = 0.0, 0
+    step = 1 << 24
+    for i in range(0, g.numel(), step):  # float64 in chunks: the full-size cases hold 10^8 elements
+        gi, ri = g[i:i + step].double(), r[i:i + step].double()
+        assert torch.isfinite(gi).all(), f"{what}: non-finite output"
+        d = (gi - ri).abs()
+        lim = tol + (ulps * bf16_ulp(ri) if got.dtype == torch.bfloat16 else 0.0)
+        excess += int((d > lim).sum())
+        worst = max(worst, d.max().item())
+    assert excess == 0, f"{what}: {excess} elements beyond {tol:.0e} absolute; max|d| {worst:.3e}"
+    return worst

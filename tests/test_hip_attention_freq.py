@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _tol import assert_bf16, assert_fp32
+from _tol import assert_abs, assert_bf16, assert_fp32
 from oracle.torch_ref import TorchRef
 
 pytestmark = pytest.mark.gpu
@@ -208,9 +208,8 @@ def test_config3_patch_filter(c, h, w, hip_f32):
 def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
     """tools/test_kernels.py:237-245 cases. With LN over K >= HipOps.split_min_k the normalised
     rows are rounded once to bf16, as the reference's GPU path does (ops/triton_cuda.py:269-271):
-    then the bf16 rule holds against that rounding emulated on the oracle, and the fp32 oracle is
-    met within the reference's own bound for this op, 2e-2 of the output scale
-    (tools/test_kernels.py:28-32, :242)."""
+    then the bf16 rule holds against that rounding emulated on the oracle, and the fp32 oracle
+    (rows not rounded) is met within 2e-2 absolute beyond the output's own rounding to bf16."""
     from clarus_amd.hip_ops import HipOps
     g = gen(4)
     x, f = rnd(g, 1, h, w, k).bfloat16(), rnd(g, nout, 8, 5)
@@ -226,8 +225,9 @@ def test_linear_patch_filter(h, w, k, nout, ln, res, hip_bf16):
         return
     xr = REF.ln(x.float(), 1e-5, rms=(ln == "rms")).to(torch.bfloat16)  # the rows the GPU path rounds
     assert_bf16(got.cpu(), REF.linear_patch_filter(xr, wl, b, f, ln=False, residual=rr), what + " (rounded rows)")
-    err = (got.cpu().double() - ref.double()).abs().max().item() / ref.abs().max().item()
-    assert err < 2e-2, f"{what}: {err:.3e} of the output scale against the fp32 oracle"
+    ref32 = TorchRef(torch.float32, "cpu").linear_patch_filter(x, wl, b, f, ln=ln, ln_eps=1e-5, residual=rr)
+    d = assert_abs(got, ref32, what=what + " vs the fp32 oracle")
+    print(f"[lpf] {what}: max|d| vs the fp32 oracle {d:.3e} (2e-2 absolute beyond the output rounding)")
 
 
 # FFTformer DFFN project_in + filter (python/clarus/models/fftformer/__init__.py:160-161): K = c,
@@ -274,8 +274,29 @@ def test_linear_patch_filter_fused_model_shapes(h, w, k, nout, ln, res, dt, hip_
         ref32 = REF.linear(xr, wl, b, ln=False if rounded else ln, ln_eps=1e-5, out_dtype=torch.float32)
         ref32 = TorchRef(torch.float32, "cpu").patch_filter(ref32, f, residual=rr)
         assert_bf16(got.cpu(), ref32, what)
-        d = (got.float() - two.float()).abs().max().item()
-        assert d <= 2e-2 * max(1.0, ref32.abs().max().item()), f"{what} vs two ops: {d:.3e}"
+        # both outputs rounded to bf16 from fp32 values that differ by summation order only
+        assert_abs(got, two.float(), what=what + " vs two ops", ulps=1.0)
+
+
+def test_linear_patch_filter_bench_shape(hip_bf16):
+    """The bench's FFTformer level-0 DFFN row as timed (workloads.fftformer_dffn_case: 720 x 1280,
+    LayerNorm eps 1e-5, 48 -> 288, bf16, its seeded inputs) against the fp32 oracle: the bf16 rule
+    (2e-2 absolute up to rounding flips, checked per 1/8 of the output), and 2e-2 absolute beyond
+    the output's rounding."""
+    from clarus_amd import _lib, workloads as wl
+    case = wl.fftformer_dffn_case(hip_bf16, "cuda")
+    print(f"[lpf] bench workload {case.name}", flush=True)
+    got = case.run().cpu()
+    kern = _lib.last_kernel()
+    h = case.cpu
+    ref32 = TorchRef(torch.float32, "cpu").linear_patch_filter(h["x"], h["w"], h["b"], h["f"], ln=True, ln_eps=1e-5)
+    assert got.dtype == torch.bfloat16 and got.shape == ref32.shape == (1, 720, 1280, 288)
+    flips = 0
+    for part in range(8):  # 90 image rows at a time
+        sl = slice(90 * part, 90 * (part + 1))
+        flips += assert_bf16(got[:, sl], ref32[:, sl], what=f"lpf bench shape rows {sl}")[1]
+    d = assert_abs(got, ref32, what="lpf bench shape")
+    print(f"[lpf] bench workload ({kern}): max|d| {d:.3e}, rounding flips {flips}")
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])

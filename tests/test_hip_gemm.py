@@ -18,7 +18,7 @@ import math
 import pytest
 import torch
 
-from _tol import BF16_ABS, assert_bf16, assert_fp32, bf16_ulp
+from _tol import BF16_ABS, assert_abs, assert_bf16, assert_fp32, bf16_ulp
 from oracle.torch_ref import Small, TorchRef, box_geometry
 
 pytestmark = pytest.mark.gpu
@@ -83,7 +83,8 @@ def rounding_bound(a, wt, b=None, gate=False, act=None, scale=None):
     return e
 
 
-def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6, rel=1e-5, rounded=None, **kw):
+def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6, rel=1e-5, rounded=None,
+                   scaled=False, **kw):
     """fp32-output prologue GEMM against the oracle. With the prologue rounded once to bf16
     (rounds_prologue): within 2e-3 relative of that rounding emulated on the oracle (the
     reference GPU path's numerics, kernels/gemm.py:164-186; elements whose fp32 prologue value
@@ -101,10 +102,15 @@ def check_prologue(got, k, what, x, wt, b=None, ln=False, mul=None, ln_eps=1e-6,
     slack = bound + 1e-5 * ref.abs().max().item()
     assert bool((d <= slack).all()), (f"{what}: {int((d > slack).sum())} elements beyond the bf16 rounding "
                                       f"bound; max|d| {d.max().item():.3e}")
-    # and the stated bf16 tolerance against the fp32 oracle: 2e-2 absolute for outputs of unit
-    # scale (the same rule on the output's own scale for the large-magnitude range cases)
-    scale = max(1.0, ref.abs().max().item())
+    # and the stated bf16 tolerance against the fp32 oracle: 2e-2 absolute. scaled=True: 2e-2 of
+    # max(1, max|ref|) for the stress cases whose rounded prologue values are not unit-scale
+    # (offset rows through a gate, x * map products of offset rows, the |x w| ~ 1e5 range case):
+    # one bf16 rounding of each prologue element moves such outputs by more than 2e-2 (the
+    # reference's GPU path rounds the same way); unit-scale data at the NAFNet shapes meets 2e-2
+    # absolute (test_rounded_operands_at_nafnet_shapes)
+    scale = max(1.0, ref.abs().max().item()) if scaled else 1.0
     assert d.max().item() <= BF16_ABS * scale, f"{what}: max|d| {d.max().item():.3e} > 2e-2 x {scale:.3g}"
+    print(f"[prologue] {what}: max|d| vs fp32 oracle {d.max().item():.3e}")
     return d.max().item()
 
 
@@ -164,7 +170,8 @@ def test_linear_layernorm_fp32_rows(k, mode, hip_bf16):
     wt, b = rnd(g, k, 96, scale=k ** -0.5, dtype=torch.bfloat16), rnd(g, 96)
     for gate in (False, True):
         got = hip_bf16.linear(*dev(x, wt, b), ln=mode, gate=gate, out_dtype=torch.float32)
-        check_prologue(got.cpu(), k, f"linear fp32 rows ln={mode} k{k} gate={gate}", x, wt, b, ln=mode, gate=gate)
+        check_prologue(got.cpu(), k, f"linear fp32 rows ln={mode} k{k} gate={gate}", x, wt, b, ln=mode, gate=gate,
+                       scaled=gate)
 
 
 @pytest.mark.parametrize("k,nout,gate", [(288, 40, False), (512, 200, True), (1024, 72, False), (576, 64, True)])
@@ -517,7 +524,7 @@ def test_linear_mul_prologue(k, hip_bf16):
     sc = torch.full((32,), 1e-4)
     got = hip_bf16.linear(x.cuda(), wt.cuda(), mul=Small(s.data.cuda(), pt, pl, 8, 12), scale=sc.cuda(),
                           out_dtype=torch.float32)
-    check_prologue(got.cpu(), k, f"linear mul large k{k}", x, wt, mul=s, scale=sc)
+    check_prologue(got.cpu(), k, f"linear mul large k{k}", x, wt, mul=s, scale=sc, scaled=True)
 
 
 @pytest.mark.parametrize("split", [True, False])
@@ -552,9 +559,9 @@ def test_split_operand_path(pro, adt, split, hip_bf16):
                                   out_dtype=torch.float32, **kwd)
             what = f"linear {pro} A {adt} split {split} split_min_k {thr}"
             if pro == "mul":
-                check_prologue(got.cpu(), k, what, x, wt, b, mul=s, **kw)
+                check_prologue(got.cpu(), k, what, x, wt, b, mul=s, scaled=True, **kw)
             else:
-                check_prologue(got.cpu(), k, what, x, wt, b, ln=mode, **kw)
+                check_prologue(got.cpu(), k, what, x, wt, b, ln=mode, scaled=True, **kw)
     finally:
         HipOps.split_min_k, HipOps.prologue_split = saved
 
@@ -585,7 +592,7 @@ def test_short_prologue_rounded(pro, hip_bf16):
         got = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), residual=res.cuda(), out_dtype=torch.float32, **kwd)
     finally:
         HipOps.round_short_prologue = saved
-    check_prologue(got.cpu(), k, f"short prologue {pro} rounded", x, wt, b, rounded=True, **kwr, **kw)
+    check_prologue(got.cpu(), k, f"short prologue {pro} rounded", x, wt, b, rounded=True, scaled=True, **kwr, **kw)
     # the default keeps hi + lo pairs: the fp32 rule; and the rounded run is really rounded (it
     # differs from the pairs by more than fp32 summation noise)
     got2 = hip_bf16.linear(*dev(x, wt, b), scale=sc.cuda(), residual=res.cuda(), out_dtype=torch.float32, **kwd)
@@ -1140,10 +1147,11 @@ def ffn_oracle(x, w1, b1, w2, b2, sc, ln, round_rows=False, ln_eps=1e-6):
     return REF.linear(u.to(x.dtype), w2, b2, scale=sc, residual=x)
 
 
-def check_ffn(got, x, w1, b1, w2, b2, sc, ln, what):
+def check_ffn(got, x, w1, b1, w2, b2, sc, ln, what, scaled=False):
     """fp32: the fp32 rule against the oracle. bf16: within one bf16 ulp (+ 1e-3 of the output
     scale for the intermediate's rounding flips) of the oracle with the kernel's roundings
-    emulated, and within 2e-2 of the output scale of the oracle without the row rounding."""
+    emulated, and within 2e-2 absolute (beyond the output's own bf16 rounding) of the oracle
+    without the row rounding."""
     if got.dtype == torch.float32:
         return assert_fp32(got.cpu(), ffn_oracle(x, w1, b1, w2, b2, sc, ln), what=what)
     g = got.double().cpu()
@@ -1151,10 +1159,14 @@ def check_ffn(got, x, w1, b1, w2, b2, sc, ln, what):
     d = (g - emu).abs()
     slack = bf16_ulp(emu) + 1e-3 * emu.abs().max()
     assert bool((d <= slack).all()), f"{what}: {int((d > slack).sum())} elements off the emulation; max {d.max():.3e}"
-    ref = ffn_oracle(x, w1, b1, w2, b2, sc, ln).double()
-    scale = max(1.0, ref.abs().max().item())
-    e = (g - ref).abs().max().item()
-    assert e <= BF16_ABS * scale, f"{what}: max|d| {e:.3e} > 2e-2 x {scale:.3g}"
+    # and 2e-2 absolute against the fp32 oracle without the row rounding (beyond the output's
+    # own rounding to bf16); scaled=True (the synthetic offset-row cases, whose gated
+    # intermediates reach |u| ~ 10): 2e-2 of max(1, max|ref|)
+    ref = ffn_oracle(x, w1, b1, w2, b2, sc, ln)
+    if not scaled:
+        return assert_abs(got, ref, what=what)
+    e = (g - ref.double()).abs().max().item()
+    assert e <= BF16_ABS * max(1.0, ref.abs().max().item()), f"{what}: max|d| {e:.3e}"
     return e
 
 
@@ -1185,7 +1197,7 @@ def test_linear_gate_linear(c, dt, ln, shape, full, hip_bf16, hip_f32):
     kern = _lib.last_kernel()
     assert kern.startswith(f"ffn_kernel c={c} dt={'bf16' if dt == torch.bfloat16 else 'f32'}"), kern
     assert got.dtype == dt and got.shape == x.shape
-    e = check_ffn(got, x, w1, b1, w2, b2, sc, ln, f"ffn c{c} {dt} ln={ln} {shape}")
+    e = check_ffn(got, x, w1, b1, w2, b2, sc, ln, f"ffn c{c} {dt} ln={ln} {shape}", scaled=bool(ln))
     print(f"[ffn] c{c} {dt} ln={ln} {shape}: {kern} max err {e:.3e}")
 
 
@@ -1204,6 +1216,32 @@ def test_linear_gate_linear_unfused_shapes(hip_bf16):
         u = hip_bf16.linear(*dev(x, w1, b1), ln=True, gate=True)
         want = hip_bf16.linear(u, *dev(w2, b2), scale=sc.cuda(), residual=x.cuda(), out_dtype=odt)
         assert torch.equal(got, want), f"c{c}: the fallback is the two linear ops"
+
+
+@pytest.mark.parametrize("ln", [True, "rms"])
+def test_linear_gate_linear_fused_vs_unfused_c64(ln, hip_bf16):
+    """The fused feed-forward at c = 64 rounds the normalised rows once to bf16 (the reference
+    GPU path's in-kernel LayerNorm, kernels/gemm.py:165-175); the two linear ops keep K = 64 rows
+    as fp32-accurate hi + lo pairs. The two results stay within 2e-2 absolute of each other beyond
+    one bf16 ulp of the outputs (both are bf16 roundings), at the NAFNet level-0 block scale."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(51)
+    c = 64
+    x = rnd(g, 1, 180, 320, c, dtype=torch.bfloat16)
+    w1, w2 = rnd(g, c, 2 * c, scale=c ** -0.5, dtype=torch.bfloat16), rnd(g, c, c, scale=c ** -0.5, dtype=torch.bfloat16)
+    b1, b2, gamma = rnd(g, 2 * c, scale=0.1), rnd(g, c, scale=0.1), rnd(g, c, scale=0.1)
+    args = (*dev(x, w1, b1, w2, b2),)
+    fused = hip_bf16.linear_gate_linear(*args, scale=gamma.cuda(), ln=ln)
+    assert _lib.last_kernel().startswith("ffn_kernel c=64"), _lib.last_kernel()
+    saved = HipOps.fuse_ffn
+    try:
+        HipOps.fuse_ffn = False
+        two = hip_bf16.linear_gate_linear(*args, scale=gamma.cuda(), ln=ln)
+    finally:
+        HipOps.fuse_ffn = saved
+    d = assert_abs(fused, two.float(), what=f"fused vs unfused ffn c64 ln={ln}", ulps=1.0)
+    print(f"[ffn] c64 ln={ln}: fused vs two linear ops max|d| {d:.3e}")
 
 
 def test_ffn_nafnet_level1_full(hip_bf16):

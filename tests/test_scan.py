@@ -97,3 +97,19 @@ def test_hip_scan_evssm_level0_crop(gpu_device):
     e = rel(got, recurrence64(*args))
     print(f"[scan] EVSSM level 0: {kernel}, rel err vs float64 {e:.2e}")
     assert e < 1e-5, e
+
+
+@pytest.mark.gpu
+def test_hip_scan_bench_workload(gpu_device):
+    """The bench's EVSSM row as timed: all 8 crops of 384 x 384, 96 channels, r = 3 (the seeded
+    inputs of workloads.evssm_scan_case), against the float64 recurrence on every crop."""
+    from clarus_amd import _lib, workloads as wl
+    from clarus_amd.hip_ops import HipOps
+    case = wl.evssm_scan_case(HipOps(torch.bfloat16, gpu_device), gpu_device)
+    print(f"[scan] bench workload {case.name}", flush=True)
+    got = case.run().cpu()
+    kernel = _lib.last_kernel()
+    h = case.cpu
+    e = rel(got, recurrence64(h["u"], h["dbl"], h["dtw"], h["dtb"], h["A"], h["dsk"]))
+    print(f"[scan] bench workload: {kernel}, rel err vs float64 {e:.2e}")
+    assert got.shape == (8, 384, 384, 96) and e < 1e-5, e

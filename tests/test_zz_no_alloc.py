@@ -5,6 +5,9 @@ Two calls in a row on the same device, the second on a smaller input, so the sec
 runs on partials the first one left in the shared static array; both must equal the workspace
 entry point's output bit for bit (same kernels, fixed summation order). The size limit is
 checked on the host before anything launches (tests/test_abi.py covers it without a GPU).
+The no-allocation property itself: the device's free memory (hipMemGetInfo through torch) is
+the same before and after further calls, and the call captured in a HIP graph replays to the
+same result.
 """
 from __future__ import annotations
 
@@ -58,3 +61,41 @@ def test_channel_attention_noalloc_matches_workspace_entry(dt, gpu_device):
         # rows of a softmax sum to one (catches a result read from stale partials that happens to
         # match a stale workspace too)
         assert torch.allclose(got.sum(-1), torch.ones_like(got.sum(-1)), atol=1e-5)
+
+
+def test_channel_attention_noalloc_allocates_nothing(gpu_device):
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(6)
+    n, h, w, c, heads = 1, 180, 320, 192, 4
+    qkv = torch.randn(n, h, w, 3 * c, generator=g).bfloat16().to(gpu_device)
+    temp = (torch.rand(heads, generator=g) * 1.5 + 0.5).to(gpu_device)
+    want = _with_workspace(lib, qkv, temp, n, h * w, c, heads)
+    out = torch.empty_like(want)
+
+    def call():
+        _lib.check(lib.clarus_hip_channel_attention_noalloc(qkv.data_ptr(), _lib.dtype_code(qkv.dtype),
+                                                            temp.data_ptr(), out.data_ptr(), n, h * w, c, heads,
+                                                            torch.cuda.current_stream().cuda_stream),
+                   "channel_attention_noalloc")
+    call()  # the first call on the device resolves the static array's address
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(gpu_device)[0]
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info(gpu_device)[0]
+    print(f"[noalloc] device free bytes before {free0}, after {free1}", flush=True)
+    assert free1 == free0 and torch.equal(out, want)
+    # captured in a HIP graph (no allocation may happen inside a capture) and replayed
+    side = torch.cuda.Stream(gpu_device)
+    side.wait_stream(torch.cuda.current_stream(gpu_device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+    assert torch.cuda.mem_get_info(gpu_device)[0] >= free1 - (64 << 20)  # the graph object itself only
