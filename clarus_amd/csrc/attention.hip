@@ -1,20 +1,26 @@
 // Restormer MDTA attention map on gfx950:
 //   A[n, hd] = softmax( (q / |q|) (k / |k|)^T * t[hd] ),  q, k: [HW, c_h] head slices of qkv.
 //
-// Stage 1 (gram_partial_kernel), grid (nsplit, batch * heads): each workgroup reduces a
-// contiguous pixel range in chunks of 128 pixels. A thread owns one unit of every chunk: 8
-// consecutive pixels x one 16-byte channel group of q or k. It loads them one chunk AHEAD into
-// registers (two units for fp32), accumulates their squares (the norms, fp32 VALU), transposes the block in
-// registers and writes 8 rows of 16 bytes into the LDS tile [channel][pixel] (no bank
-// conflicts). Each wave then contracts its 32 pixels with MFMA: the cross blocks Q^T K (NB x NB
-// blocks of 16 x 16). bf16 inputs use one bf16 MFMA per block (products exact in fp32); fp32
-// inputs are split into bf16 hi + lo and use three (hi hi + hi lo + lo hi, error <= 2^-16
-// relative per product). The 4 waves' partials are summed in LDS (the tile's memory, reused)
-// in a fixed order and written to scratch as one record per split.
-// Stage 2 (gram_reduce_kernel): RS slices of the splits summed per element, in split order.
-// Stage 3 (gram_finish_kernel), one workgroup per (image, head): sums the RS slices in order,
-// scales by rsqrt(max(|.|^2, 1e-24)) and the temperature, and applies a row softmax.
-// The result is deterministic (fixed summation order for a given shape).
+// One launch, gram_kernel, grid (nsplit, images * heads), 256 threads.
+// Pixel phase: each workgroup reduces a contiguous pixel range (a split) in chunks of 128
+// pixels. A thread owns one unit of every chunk: 8 consecutive pixels x one 16-byte channel group
+// of q or k (two units for fp32), loaded one chunk ahead through a buffer descriptor whose range
+// ends at the split's end, so every load is issued and reads past the end return zero.
+// A unit's squares feed the norms (fp32 VALU); the unit is transposed in registers and written
+// as 8 rows of 16 bytes into the LDS tile [channel][pixel] (no bank conflicts). Each wave then
+// contracts its 32 pixels with MFMA: the cross blocks Q^T K (NB x NB blocks of 16 x 16). bf16
+// inputs use one bf16 MFMA per block (products exact in fp32); fp32 inputs are split into bf16
+// hi + lo and use three (hi hi + hi lo + lo hi, error <= 2^-16 relative per product). The 4
+// waves' partials are summed in LDS in a fixed order and written as the split's record.
+// Reduction, in the same launch: the splits of an (image, head) form at most CA_MAX_GROUPS
+// groups. After its record is visible (device-scope fence), a workgroup counts its arrival on
+// its group's counter; the last to arrive sums the group's records in split order and, with
+// more than one group, writes a group record and counts on the head's counter; the last group
+// sums the group records in group order, scales by rsqrt(max(|.|^2, 1e-24)) and the temperature
+// and applies the row softmax. Nothing waits for another workgroup, and every sum has a fixed
+// order whichever workgroup performs it, so the result is deterministic. The arrival counters
+// sit at the start of the scratch: zero when a call starts, reset to zero by the workgroups
+// that saw them complete.
 #include <mutex>
 
 #include "capi.hpp"
@@ -22,23 +28,36 @@
 
 namespace clarus {
 
-constexpr int GP_CHUNK = 128;  // pixels per chunk (32 per wave)
-constexpr int GP_RS = 16;      // reduce slices
+constexpr int GP_CHUNK = 128;                                  // pixels per chunk (32 per wave)
+constexpr int CA_MAX_GROUPS = 32;                              // split groups per (image, head)
+constexpr int CA_COUNTERS = 16384;                             // arrival counters per scratch
+constexpr int CA_MAX_NH = CA_COUNTERS / (CA_MAX_GROUPS + 1);   // (image, head) pairs per launch
+constexpr int64_t CA_COUNTER_BYTES = (int64_t)CA_COUNTERS * 4;
 
-// partial record per (image*head, split): [NB*16][NB*16] cross, [NB*16] |q|^2, [NB*16] |k|^2
+// record per (image*head, split): [NB*16][NB*16] cross, [NB*16] |q|^2, [NB*16] |k|^2
 __host__ __device__ inline int64_t gram_rec_floats(int nb) {
   const int cp = nb * 16;
   return (int64_t)cp * cp + 2 * cp;
 }
 
-// LDS of the partial kernel: the transposed chunk [2 CP rows][GP_CHUNK pixels] (+16 B per row),
-// reused after the pixel loop as the 4-wave reduction buffer
+// LDS: the transposed chunk [2 CP rows][GP_CHUNK pixels] (+16 B per row), reused after the
+// pixel loop as the 4-wave reduction buffer and the running sums of the reduction
 template <int NB, int DT>
 __host__ __device__ constexpr int gram_lds_bytes() {
   return (2 * NB * 16 * (GP_CHUNK * (DT == DT_BF16 ? 2 : 4) + 16)) > (4 * (NB * 16 * NB * 16 + 2 * NB * 16) * 4)
              ? (2 * NB * 16 * (GP_CHUNK * (DT == DT_BF16 ? 2 : 4) + 16))
              : (4 * (NB * 16 * NB * 16 + 2 * NB * 16) * 4);
 }
+
+struct GramP {
+  const void* qkv;
+  float* part;          // [nh][nsplit + ngroups][rec]: split records, then group records
+  unsigned* cnt;        // [nh][CA_MAX_GROUPS + 1]: group counters, then the head's counter
+  const float* temp;    // [heads]
+  float* out;           // [nh][ch][ch]
+  int64_t hw, split_len;
+  int c, ch, heads, nsplit, gsize, ngroups;
+};
 
 // 8 x 8 transpose of bf16: in[i] = 8 channels of pixel i (u32 pairs), out[c] = 8 pixels of channel c
 __device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
@@ -53,10 +72,76 @@ __device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&
   }
 }
 
+// Records are exchanged between workgroups through device-scope accesses: stores written
+// through to the device's point of coherence and loads that miss the per-CU and per-XCD caches
+// (cache policy SC1), so no cache-wide writeback or invalidate is needed between them.
+constexpr int CA_SC1 = 1 << 4;  // cache-policy operand of the raw buffer loads / stores: SC1
+
+// dst[e] (LDS, e < REC) = sum over records r = 0 .. count - 1 of rec[r * REC + e] (records at
+// record index r0 of rs, a descriptor whose range is exactly rs_bytes), in record order (the
+// first record added to zero); loads 8 records deep. Lanes without a slot load at offset
+// rs_bytes, past the range, and read zero.
+template <int REC>
+__device__ __forceinline__ void sum_records(__amdgpu_buffer_rsrc_t rs, uint32_t rs_bytes, int r0, int count,
+                                            float* dst, int tid) {
+  static_assert(REC % 4 == 0, "records of whole 16-byte groups");
+  constexpr int SLOTS = REC / 4;
+  constexpr int PER = (SLOTS + 255) / 256;
+  f32x4 acc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto ld = [&](int r, int i) __attribute__((always_inline)) {
+    const int e4 = tid + 256 * i;
+    const uint32_t o = e4 < SLOTS ? (uint32_t)(((r0 + r) * REC + e4 * 4) * 4) : rs_bytes;
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, CA_SC1));
+  };
+  int r = 0;
+  for (; r + 8 <= count; r += 8) {
+    f32x4 v[8][PER];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) v[j][i] = ld(r + j, i);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) acc[i] += v[j][i];
+  }
+  for (; r < count; ++r)
+#pragma unroll
+    for (int i = 0; i < PER; ++i) acc[i] += ld(r, i);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e4 = tid + 256 * i;
+    if (e4 < SLOTS) *reinterpret_cast<f32x4*>(dst + e4 * 4) = acc[i];
+  }
+}
+
+// record index r of rs = src[0 .. REC) (LDS), device-scope stores
+template <int REC>
+__device__ __forceinline__ void store_record(__amdgpu_buffer_rsrc_t rs, int r, const float* src, int tid) {
+  for (int e4 = tid; e4 < REC / 4; e4 += 256)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const f32x4*>(src + e4 * 4)),
+                                           rs, (r * REC + e4 * 4) * 4, 0, CA_SC1);
+}
+
+// One arrival on *counter by this workgroup, after every wave's device-scope record stores have
+// completed: true in every thread of the workgroup that arrived last of `members`, which also
+// resets the counter for the next call
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned members, int* flag, int tid) {
+  wait_vmcnt<0>();  // this wave's record stores are complete (written through)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned old = atomicAdd(counter, 1u);
+    *flag = old == members - 1u;
+    if (old == members - 1u) atomicExch(counter, 0u);  // every member has arrived: the next call starts at zero
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
 template <int NB, int DT>
-__global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restrict__ qkv, float* __restrict__ part,
-                                                           int64_t hw, int c, int ch, int heads,
-                                                           int64_t split_len, int nsplit) {
+__global__ void __launch_bounds__(256) gram_kernel(GramP p) {
   constexpr int CP = NB * 16;                      // padded head channels
   constexpr int ES = (DT == DT_BF16) ? 2 : 4;
   constexpr int CG = (DT == DT_BF16) ? 8 : 4;      // channels per 16-byte load
@@ -64,25 +149,30 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
   constexpr int REC = CP * CP + 2 * CP;
   constexpr int OCT = GP_CHUNK / 8;                // 8-pixel octets per chunk
   __shared__ __attribute__((aligned(16))) unsigned char smem[gram_lds_bytes<NB, DT>()];
+  __shared__ int s_flag;
   unsigned char* tl = smem;                        // rows [0, CP) q, [CP, 2 CP) k
   float* red = reinterpret_cast<float*>(smem);     // reused after the pixel loop
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 15, lg = lane >> 4;
-  const int nh = blockIdx.y;
-  const int img = nh / heads, hd = nh - img * heads;
-  const int64_t p_begin = (int64_t)blockIdx.x * split_len;
-  int64_t p_end = p_begin + split_len;
-  if (p_end > hw) p_end = hw;
-  const int64_t row_stride = 3LL * c;  // elements per pixel
-  const unsigned char* base = (const unsigned char*)qkv + (int64_t)img * hw * row_stride * ES;
+  const int nh = blockIdx.y, split = blockIdx.x;
+  const int img = nh / p.heads, hd = nh - img * p.heads;
+  const int ch = p.ch;
+  const int64_t p_begin = (int64_t)split * p.split_len;
+  const int64_t p_end = p_begin + p.split_len < p.hw ? p_begin + p.split_len : p.hw;
+  const int64_t len = p_end - p_begin;
+  const int64_t row_bytes = 3LL * p.c * ES;
+  // the split's rows as a buffer range: loads at or past the split's end read zero
+  const uint32_t nbytes = (uint32_t)(len * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs =
+      buf_rsrc_n((const unsigned char*)p.qkv + ((int64_t)img * p.hw + p_begin) * row_bytes, nbytes);
   const int groups = ch / CG;          // load groups per head slice
   // units of a chunk: u = tid + 256 t = (which, group) * OCT + octet, octets in consecutive
   // lanes; 2 * groups * OCT <= 256 * UPT (head width <= 64)
   constexpr int UPT = (DT == DT_BF16) ? 1 : 2;
   int octet[UPT], row0[UPT];
   bool active[UPT];
-  int64_t coff[UPT];
+  uint32_t uoff[UPT];  // byte offset of the unit's first pixel in chunk 0 (past the range: inactive)
 #pragma unroll
   for (int t = 0; t < UPT; ++t) {
     const int u = tid + 256 * t;
@@ -91,8 +181,9 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
     active[t] = wg_ < 2 * groups;
     const int which = active[t] ? wg_ / groups : 0;
     const int grp = active[t] ? wg_ - which * groups : 0;
-    coff[t] = (which ? c : 0) + hd * ch + grp * CG;  // channel offset of the unit
-    row0[t] = which * CP + grp * CG;                // its first LDS row
+    const int64_t coff = (which ? p.c : 0) + hd * ch + grp * CG;  // channel offset of the unit
+    row0[t] = which * CP + grp * CG;                             // its first LDS row
+    uoff[t] = active[t] ? (uint32_t)(octet[t] * 8 * row_bytes + coff * ES) : 0x80000000u;
   }
 
   // zero the padded channel rows once (never written by the units)
@@ -113,19 +204,19 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
 #pragma unroll
     for (int i = 0; i < CG; ++i) sq[t][i] = 0.f;
 
-  u32x4 rq[UPT][8];
-  auto fetch = [&](int64_t p0) __attribute__((always_inline)) {
+  // chunk starting at pixel r0 of the split into r (every load issued; inactive units and
+  // pixels past the split read zero)
+  auto fetch = [&](u32x4 (&r)[UPT][8], int64_t r0) __attribute__((always_inline)) {
+    const uint32_t cb = (uint32_t)(r0 * row_bytes);
 #pragma unroll
     for (int t = 0; t < UPT; ++t)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int64_t p = p0 + octet[t] * 8 + i;
-        rq[t][i] = (active[t] && p < p_end)
-                       ? *reinterpret_cast<const u32x4*>(base + (p * row_stride + coff[t]) * ES)
-                       : u32x4{0u, 0u, 0u, 0u};
+        const uint32_t o = uoff[t] + cb + (uint32_t)(i * row_bytes);
+        r[t][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, 0));
       }
   };
-  auto store_t = [&]() __attribute__((always_inline)) {
+  auto store_t = [&](const u32x4 (&rq)[UPT][8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < UPT; ++t) {
       if (!active[t]) continue;
@@ -160,14 +251,8 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
       }
     }
   };
-
-  if (p_begin < p_end) fetch(p_begin);
-  for (int64_t p0 = p_begin; p0 < p_end; p0 += GP_CHUNK) {
-    __syncthreads();  // previous chunk's MFMA reads are done
-    store_t();
-    __syncthreads();
-    if (p0 + GP_CHUNK < p_end) fetch(p0 + GP_CHUNK);  // next chunk streams in during the products
-    // ---- this wave's 32 pixels: k = wave * 32 + 8 lg + s
+  // this wave's 32 pixels of the tile: k = wave * 32 + 8 lg + s
+  auto products = [&]() __attribute__((always_inline)) {
     const int kcol = wave * 32 + lg * 8;
     if constexpr (DT == DT_BF16) {
       bf16x8 qf[NB], kf[NB];
@@ -206,6 +291,19 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
           cross[i][j] = mfma_bf16(ql[i], kh[j], cross[i][j]);
         }
     }
+  };
+
+  // pixel loop: the next chunk loads while this one is transposed and contracted (a chunk past
+  // the split's end reads zero and adds nothing). Measured against two chunks in flight per
+  // thread (a second register buffer, barriers that keep loads outstanding): equal or slower.
+  u32x4 ra[UPT][8];
+  fetch(ra, 0);
+  for (int64_t r0 = 0; r0 < len; r0 += GP_CHUNK) {
+    __syncthreads();  // the previous chunk's fragment reads are done
+    store_t(ra);
+    __syncthreads();
+    fetch(ra, r0 + GP_CHUNK);
+    products();
   }
 
   // ---- reduce the 4 waves (fixed order) and write this split's record
@@ -235,76 +333,54 @@ __global__ void __launch_bounds__(256) gram_partial_kernel(const void* __restric
     }
   }
   __syncthreads();
-  float* out = part + ((int64_t)nh * nsplit + blockIdx.x) * REC;
-  for (int e = tid; e < REC; e += 256)
-    out[e] = e < CP * CP ? ((red[e] + red[REC + e]) + red[2 * REC + e]) + red[3 * REC + e] : red[e];
-}
-
-// part [nh][nsplit][rec] -> part2 [nh][RS][rec]: slice s sums splits [s * per, (s + 1) * per)
-__global__ void __launch_bounds__(256) gram_reduce_kernel(const float* __restrict__ part, float* __restrict__ part2,
-                                                          int64_t rec, int nsplit) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int nh = blockIdx.y, sl = blockIdx.z;
-  if (e >= rec) return;
-  const int per = (nsplit + GP_RS - 1) / GP_RS;
-  const int s0 = sl * per;
-  const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
-  const float* src = part + ((int64_t)nh * nsplit) * rec + e;
-  float s = 0.f;
-#pragma unroll 8
-  for (int sp = s0; sp < s1; ++sp) s += src[(int64_t)sp * rec];
-  part2[((int64_t)nh * GP_RS + sl) * rec + e] = s;
-}
-
-template <int NB>
-__global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restrict__ part2, const float* __restrict__ temp,
-                                                          float* __restrict__ out, int ch, int heads) {
-  constexpr int CP = NB * 16;
-  constexpr int REC = CP * CP + 2 * CP;
-  static_assert(REC % 4 == 0, "record of whole 16-byte groups");
-  constexpr int PER = (REC / 4 + 255) / 256;  // 16-byte groups per thread
-  __shared__ __attribute__((aligned(16))) float g[CP * CP + 2 * CP];  // cross, then |q|^2, |k|^2
-  __shared__ float nq[CP], nk[CP];
-  const int nh = blockIdx.x;
-  const int hd = nh % heads;
-  const float* src = part2 + (int64_t)nh * GP_RS * REC;
-  // every slice load is issued before any sum is used: one memory latency, 16-byte loads
-  f32x4 v[PER][GP_RS];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e4 = threadIdx.x + 256 * i;
-#pragma unroll
-    for (int sl = 0; sl < GP_RS; ++sl)
-      v[i][sl] = e4 < REC / 4 ? *reinterpret_cast<const f32x4*>(src + sl * REC + e4 * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nrec = p.nsplit + p.ngroups;
+  const uint32_t recs_bytes = (uint32_t)(nrec * REC * 4);  // this (image, head)'s records
+  const __amdgpu_buffer_rsrc_t recs = buf_rsrc_n(p.part + (int64_t)nh * nrec * REC, recs_bytes);
+  {
+    // the 4 waves' cross blocks summed in wave order into wave 0's slot (norms already there)
+    for (int e = tid; e < CP * CP; e += 256) red[e] = ((red[e] + red[REC + e]) + red[2 * REC + e]) + red[3 * REC + e];
+    __syncthreads();
+    store_record<REC>(recs, split, red, tid);
   }
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e4 = threadIdx.x + 256 * i;
-    f32x4 s4 = v[i][0];
-#pragma unroll
-    for (int sl = 1; sl < GP_RS; ++sl) s4 += v[i][sl];
-    if (e4 < REC / 4) *reinterpret_cast<f32x4*>(g + e4 * 4) = s4;
+
+  // ---- the reduction over splits: the last arrival of a group sums the group, the last group
+  // the head (each in a fixed order)
+  unsigned* cnt = p.cnt + (int64_t)nh * (CA_MAX_GROUPS + 1);
+  const int g = split / p.gsize;
+  const int g0 = g * p.gsize;
+  const int g1 = g0 + p.gsize < p.nsplit ? g0 + p.gsize : p.nsplit;
+  if (!arrive_last(cnt + g, (unsigned)(g1 - g0), &s_flag, tid)) return;
+  sum_records<REC>(recs, recs_bytes, g0, g1 - g0, red, tid);
+  if (p.ngroups > 1) {
+    __syncthreads();
+    store_record<REC>(recs, p.nsplit + g, red, tid);
+    if (!arrive_last(cnt + CA_MAX_GROUPS, (unsigned)p.ngroups, &s_flag, tid)) return;
+    sum_records<REC>(recs, recs_bytes, p.nsplit, p.ngroups, red, tid);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < 2 * CP; e += 256) {
-    const float sq = g[CP * CP + e];
-    if (e < CP) nq[e] = rsqrtf(fmaxf(sq, 1e-24f));
-    else nk[e - CP] = rsqrtf(fmaxf(sq, 1e-24f));
+
+  // ---- norms, temperature and the row softmax of this (image, head)
+  float* nq = red + REC;
+  float* nk = nq + CP;
+  for (int e = tid; e < 2 * CP; e += 256) {
+    const float s2 = red[CP * CP + e];
+    if (e < CP) nq[e] = rsqrtf(fmaxf(s2, 1e-24f));
+    else nk[e - CP] = rsqrtf(fmaxf(s2, 1e-24f));
   }
   __syncthreads();
-  const float t = temp[hd];
+  const float tt = p.temp[hd];
   // four threads per row, CP / 4 columns each (interleaved: column 4 m + q of thread q); max
   // and sum over the four lanes with two butterfly steps
   constexpr int CPT = CP / 4;
-  const int i = threadIdx.x >> 2, q = threadIdx.x & 3;
+  const int i = tid >> 2, q = tid & 3;
   if (i < CP) {
     float v[CPT];
     float mx = -INFINITY;
-    const float si = nq[i] * t;
+    const float si = nq[i] * tt;
 #pragma unroll
     for (int m = 0; m < CPT; ++m) {
       const int j = 4 * m + q;
-      v[m] = (i < ch && j < ch) ? g[i * CP + j] * si * nk[j] : -INFINITY;
+      v[m] = (i < ch && j < ch) ? red[i * CP + j] * si * nk[j] : -INFINITY;
       mx = fmaxf(mx, v[m]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
@@ -319,7 +395,7 @@ __global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restric
     sum += __shfl_xor(sum, 2, 64);
     if (i < ch) {
       const float inv = 1.0f / sum;
-      float* o = out + ((int64_t)nh * ch + i) * ch;
+      float* o = p.out + ((int64_t)nh * ch + i) * ch;
 #pragma unroll
       for (int m = 0; m < CPT; ++m)
         if (4 * m + q < ch) o[4 * m + q] = v[m] * inv;
@@ -329,50 +405,85 @@ __global__ void __launch_bounds__(256) gram_finish_kernel(const float* __restric
 
 static int pick_nb(int64_t ch) { return (int)((ch + 15) / 16); }
 
-static int64_t split_len_for(int64_t batch, int64_t heads, int64_t hw) {
-  // ~2 workgroups per CU in total, whole chunks per split: long splits amortise the per-split
-  // reduction epilogue
-  const int64_t wgs = 2LL * device_cus();
-  int64_t want = (wgs + batch * heads - 1) / (batch * heads);
-  if (want < 1) want = 1;
-  int64_t len = (hw + want - 1) / want;
-  len = (len + GP_CHUNK - 1) / GP_CHUNK * GP_CHUNK;
-  return len < GP_CHUNK ? GP_CHUNK : len;
+struct GramPlan {
+  int64_t nh;         // (image, head) pairs per launch
+  int64_t split_len;  // pixels per split (a multiple of 2 chunks)
+  int nsplit, gsize, ngroups;
+};
+
+// Splits: about 2 workgroups per CU over the launch (measured at the config-4 levels against 3
+// and 4: fewer records to sum, same pixel rate), at least two chunks per split, a split's bytes
+// (plus the chunks read past it) addressable with 32-bit offsets; groups: about sqrt(nsplit)
+// of them, at most CA_MAX_GROUPS.
+static GramPlan gram_plan(int64_t batch, int64_t heads, int64_t hw, int64_t c) {
+  GramPlan g;
+  const int64_t imgs = batch < CA_MAX_NH / heads ? batch : CA_MAX_NH / heads;
+  g.nh = imgs * heads;
+  const int64_t chunks = cdiv(hw, GP_CHUNK);
+  const int64_t row_bytes = 3 * c * 4;  // fp32 rows: the same plan (and workspace) for both dtypes
+  const int64_t want = cdiv(2LL * device_cus(), g.nh);
+  int64_t per = cdiv(chunks, want);
+  per = per < 2 ? 2 : (per + 1) / 2 * 2;
+  const int64_t max_per = ((((int64_t)1 << 30) / (GP_CHUNK * row_bytes)) / 2) * 2;
+  if (per > max_per) per = max_per < 2 ? 2 : max_per;
+  g.split_len = per * GP_CHUNK;
+  g.nsplit = (int)cdiv(hw, g.split_len);
+  int ng = 1;
+  if (g.nsplit > 8) {
+    ng = 1;
+    while ((int64_t)ng * ng < g.nsplit) ++ng;
+    if (ng > CA_MAX_GROUPS) ng = CA_MAX_GROUPS;
+  }
+  g.gsize = (int)cdiv(g.nsplit, ng);
+  g.ngroups = (int)cdiv(g.nsplit, g.gsize);
+  return g;
 }
 
-// Launches the three stages with `scratch` as the partials (already checked to be large enough).
+static int64_t gram_workspace_bytes(const GramPlan& g, int64_t ch) {
+  return CA_COUNTER_BYTES + g.nh * (int64_t)(g.nsplit + g.ngroups) * gram_rec_floats(pick_nb(ch)) * 4;
+}
+
+// Launches gram_kernel per batch slice of at most CA_MAX_NH (image, head) pairs, with `scratch`
+// as counters (zero on entry) + partials (already checked to be large enough).
 static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,
                                     int64_t batch, int64_t hw, int64_t c, int64_t heads, void* scratch,
                                     hipStream_t s) {
   const int64_t ch = c / heads;
-  const int64_t len = split_len_for(batch, heads, hw);
-  const int nsplit = (int)cdiv(hw, len);
+  const GramPlan g = gram_plan(batch, heads, hw, c);
   const int nb = pick_nb(ch);
-  const int64_t rec = gram_rec_floats(nb);
-  dim3 g1((unsigned)nsplit, (unsigned)(batch * heads));
-  dim3 g2((unsigned)cdiv(rec, 256), (unsigned)(batch * heads), GP_RS);
-  float* part = (float*)scratch;
-  float* part2 = part + batch * heads * nsplit * rec;
-#define CLARUS_GRAM(NB)                                                                                       \
-  do {                                                                                                        \
-    if (qkv_dtype == DT_BF16)                                                                                 \
-      hipLaunchKernelGGL((gram_partial_kernel<NB, DT_BF16>), g1, dim3(256), 0, s, qkv, part, hw, (int)c,      \
-                         (int)ch, (int)heads, len, nsplit);                                                   \
-    else                                                                                                      \
-      hipLaunchKernelGGL((gram_partial_kernel<NB, DT_F32>), g1, dim3(256), 0, s, qkv, part, hw, (int)c,       \
-                         (int)ch, (int)heads, len, nsplit);                                                   \
-    hipLaunchKernelGGL(gram_reduce_kernel, g2, dim3(256), 0, s, part, part2, rec, nsplit);                     \
-    hipLaunchKernelGGL((gram_finish_kernel<NB>), dim3((unsigned)(batch * heads)), dim3(256), 0, s, part2,     \
-                       temperature, out, (int)ch, (int)heads);                                                \
+  const int64_t imgs = g.nh / heads;
+  const int64_t img_bytes = hw * 3 * c * (qkv_dtype == DT_BF16 ? 2 : 4);
+  note_kernel("gram_kernel nb=%d nsplit=%d groups=%d", nb, g.nsplit, g.ngroups);
+  for (int64_t i0 = 0; i0 < batch; i0 += imgs) {
+    const int64_t ni = batch - i0 < imgs ? batch - i0 : imgs;
+    GramP p;
+    p.qkv = (const unsigned char*)qkv + i0 * img_bytes;
+    p.cnt = (unsigned*)scratch;
+    p.part = (float*)((unsigned char*)scratch + CA_COUNTER_BYTES);
+    p.temp = temperature;
+    p.out = out + i0 * heads * ch * ch;
+    p.hw = hw;
+    p.split_len = g.split_len;
+    p.c = (int)c;
+    p.ch = (int)ch;
+    p.heads = (int)heads;
+    p.nsplit = g.nsplit;
+    p.gsize = g.gsize;
+    p.ngroups = g.ngroups;
+    dim3 grid((unsigned)g.nsplit, (unsigned)(ni * heads));
+#define CLARUS_GRAM(NB)                                                                                   \
+  do {                                                                                                    \
+    if (qkv_dtype == DT_BF16) hipLaunchKernelGGL((gram_kernel<NB, DT_BF16>), grid, dim3(256), 0, s, p);  \
+    else hipLaunchKernelGGL((gram_kernel<NB, DT_F32>), grid, dim3(256), 0, s, p);                        \
   } while (0)
-  note_kernel("gram_partial_kernel + gram_reduce_kernel + gram_finish_kernel nb=%d", nb);
-  switch (nb) {
-    case 1: CLARUS_GRAM(1); break;
-    case 2: CLARUS_GRAM(2); break;
-    case 3: CLARUS_GRAM(3); break;
-    default: CLARUS_GRAM(4); break;
-  }
+    switch (nb) {
+      case 1: CLARUS_GRAM(1); break;
+      case 2: CLARUS_GRAM(2); break;
+      case 3: CLARUS_GRAM(3); break;
+      default: CLARUS_GRAM(4); break;
+    }
 #undef CLARUS_GRAM
+  }
   return check_launch("channel_attention");
 }
 
@@ -380,6 +491,7 @@ static int check_channel_attention(const void* qkv, int32_t qkv_dtype, const flo
                                    int64_t batch, int64_t hw, int64_t c, int64_t heads) {
   CLARUS_REQUIRE(qkv && temperature && out, "channel_attention: null operand");
   CLARUS_REQUIRE(batch > 0 && hw > 0 && c > 0 && heads > 0 && c % heads == 0, "channel_attention: bad sizes");
+  CLARUS_REQUIRE(heads <= CA_MAX_NH, "channel_attention: at most %d heads", CA_MAX_NH);
   CLARUS_REQUIRE(qkv_dtype == DT_BF16 || qkv_dtype == DT_F32, "channel_attention: bad dtype");
   const int64_t ch = c / heads;
   CLARUS_REQUIRE(ch % 8 == 0 && ch <= 64, "channel_attention: head width %lld must be a multiple of 8, <= 64",
@@ -428,10 +540,8 @@ static void* device_scratch() {
 using namespace clarus;
 
 extern "C" size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads) {
-  if (batch <= 0 || hw <= 0 || c <= 0 || heads <= 0 || c % heads) return 0;
-  const int64_t ch = c / heads;
-  const int64_t nsplit = cdiv(hw, split_len_for(batch, heads, hw));
-  return (size_t)(batch * heads * (nsplit + GP_RS) * gram_rec_floats(pick_nb(ch)) * sizeof(float));
+  if (batch <= 0 || hw <= 0 || c <= 0 || heads <= 0 || c % heads || heads > CA_MAX_NH) return 0;
+  return (size_t)gram_workspace_bytes(gram_plan(batch, heads, hw, c), c / heads);
 }
 
 extern "C" int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float* temperature, float* out,

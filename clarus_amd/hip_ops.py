@@ -137,6 +137,7 @@ class HipOps(Backend):
         self.pair_launches = {"gemm_ln_gemm": 0, "gemm_ln_rows": 0}
         self.ffn_launches = 0  # linear_gate_linear calls served by clarus_hip_ffn
         self.ln_dw_launches = 0  # linear_dwconv calls served by clarus_hip_ln_gemm_dwconv
+        self._ca_ws = {}  # (device, stream) -> zeroed channel-attention workspace (counters stay zero)
 
     # ------------------------------------------------------------------ plumbing
     def cached(self, t: torch.Tensor, tag: str, fn):
@@ -656,12 +657,27 @@ class HipOps(Backend):
         t = temperature.reshape(heads)
         t = t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous()
         need = self.lib.clarus_hip_channel_attention_workspace(n, h * wd, c, heads)
-        scratch = torch.empty(max(need, 16), dtype=torch.uint8, device=qkv.device)
+        scratch = self._attention_workspace(need, qkv.device)
         out = torch.empty((n, heads, ch, ch), dtype=torch.float32, device=qkv.device)
         _lib.check(self.lib.clarus_hip_channel_attention(qkv.data_ptr(), _lib.dtype_code(qkv.dtype), t.data_ptr(),
                                                          out.data_ptr(), n, h * wd, c, heads, scratch.data_ptr(),
                                                          scratch.numel(), self._stream(qkv)), "channel_attention")
         return out
+
+    def _attention_workspace(self, need: int, device) -> torch.Tensor:
+        """Workspace of clarus_hip_channel_attention: its leading arrival counters must be zero when
+        a call starts, and every call leaves them zero. Eager calls reuse one zeroed buffer per
+        stream (grown, zeroed again, when a call needs more); a call under graph capture gets a
+        fresh zeroed buffer of the graph's own pool, its fill recorded before the launch, so every
+        replay starts from zero."""
+        if torch.cuda.is_current_stream_capturing():
+            return torch.zeros(need, dtype=torch.uint8, device=device)
+        key = (str(device), torch.cuda.current_stream(device).cuda_stream)
+        ws = self._ca_ws.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+            self._ca_ws[key] = ws
+        return ws
 
     def linear_per_image(self, x, w, residual=None, out_dtype=None, bias=None):
         n, h, wd, k = x.shape

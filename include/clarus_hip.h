@@ -289,8 +289,12 @@ int clarus_hip_intro3x3(const float* inp, const float* wt, const float* bias, vo
  *   A[n, hd] = softmax((q / |q|) (k / |k|)^T * temperature[hd]) over c_h x c_h,
  * norms over all pixels. qkv [batch, h, w, 3c] contiguous (q | k | v channel blocks),
  * dtype qkv_dtype; out fp32 [batch, heads, c_h, c_h]; temperature fp32 [heads].
- * The pixel reduction is split over workgroups (deterministic two-stage sum); scratch must
- * hold clarus_hip_channel_attention_workspace(...) bytes.
+ * One launch: the pixel reduction is split over workgroups, whose partials are summed in the
+ * same launch in a fixed order (deterministic). scratch must hold
+ * clarus_hip_channel_attention_workspace(...) bytes; its first 64 KiB are arrival counters
+ * that must be zero when a call starts, and every call leaves them zero (zero a new workspace
+ * once, e.g. with a fill kernel, then reuse it call after call). Calls that overlap in time
+ * must not share a workspace. At most 496 heads.
  * replaces kernels/attention.py:48-66 gram (gram_kernel :14-45) + ops/triton_cuda.py:174-181
  */
 size_t clarus_hip_channel_attention_workspace(int64_t batch, int64_t hw, int64_t c, int64_t heads);
@@ -303,7 +307,8 @@ int clarus_hip_channel_attention(const void* qkv, int32_t qkv_dtype, const float
  * clarus_hip_channel_attention without a workspace argument and without allocating: the split-K
  * partials live in a static device array of CLARUS_CHANNEL_ATTENTION_SCRATCH_MAX bytes, one per
  * device, held until the process ends (its address is looked up on the first call on each
- * device, with that device current). Same arguments, results and rules otherwise; shapes whose
+ * device, with that device current). Its arrival counters are zero when the library loads and
+ * every call leaves them zero. Same arguments, results and rules otherwise; shapes whose
  * clarus_hip_channel_attention_workspace(...) exceeds the maximum return CLARUS_EINVAL. Every
  * call on a device shares that device's array: calls that overlap in time on one device (other
  * streams, other threads) race and give wrong results. Calls no hipMalloc / hipFree.

@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 def _with_workspace(lib, qkv, temp, n, hw, c, heads):
     out = torch.empty((n, heads, c // heads, c // heads), dtype=torch.float32, device=qkv.device)
     need = lib.clarus_hip_channel_attention_workspace(n, hw, c, heads)
-    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=qkv.device)
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=qkv.device)  # the counters start at zero
     _lib.check(lib.clarus_hip_channel_attention(qkv.data_ptr(), _lib.dtype_code(qkv.dtype), temp.data_ptr(),
                                                 out.data_ptr(), n, hw, c, heads, ws.data_ptr(), ws.numel(),
                                                 torch.cuda.current_stream().cuda_stream), "channel_attention")
