@@ -12,15 +12,15 @@
 // inputs use one bf16 MFMA per block (products exact in fp32); fp32 inputs are split into bf16
 // hi + lo and use three (hi hi + hi lo + lo hi, error <= 2^-16 relative per product). The 4
 // waves' partials are summed in LDS in a fixed order and written as the split's record.
-// Reduction, in the same launch: the splits of an (image, head) form at most CA_MAX_GROUPS
-// groups. After its record is visible (device-scope fence), a workgroup counts its arrival on
-// its group's counter; the last to arrive sums the group's records in split order and, with
-// more than one group, writes a group record and counts on the head's counter; the last group
-// sums the group records in group order, scales by rsqrt(max(|.|^2, 1e-24)) and the temperature
-// and applies the row softmax. Nothing waits for another workgroup, and every sum has a fixed
-// order whichever workgroup performs it, so the result is deterministic. The arrival counters
-// sit at the start of the scratch: zero when a call starts, reset to zero by the workgroups
-// that saw them complete.
+// Reduction, in the same launch, up a tree of fan-in CA_FAN over the splits of an (image, head):
+// after its record is stored (device-scope stores, complete before the arrival), a workgroup
+// counts its arrival at its tree node; the last of the node's children to arrive sums their
+// records in child order (every load issued before the first add) and carries the sum one
+// level up. The last arrival at the root holds the sums: it scales by rsqrt(max(|.|^2, 1e-24))
+// and the temperature and applies the row softmax. Nothing waits for another workgroup, and
+// every sum has one order whoever performs it, so the result is deterministic. The arrival
+// counters sit at the start of the scratch: zero when a call starts, reset to zero by the
+// workgroups that saw them complete.
 #include <mutex>
 
 #include "capi.hpp"
@@ -29,9 +29,9 @@
 namespace clarus {
 
 constexpr int GP_CHUNK = 128;                                  // pixels per chunk (32 per wave)
-constexpr int CA_MAX_GROUPS = 32;                              // split groups per (image, head)
+constexpr int CA_FAN = 8;                                      // records summed per tree node
 constexpr int CA_COUNTERS = 16384;                             // arrival counters per scratch
-constexpr int CA_MAX_NH = CA_COUNTERS / (CA_MAX_GROUPS + 1);   // (image, head) pairs per launch
+constexpr int CA_MAX_NH = 496;                                 // (image, head) pairs per launch, at most
 constexpr int64_t CA_COUNTER_BYTES = (int64_t)CA_COUNTERS * 4;
 
 // record per (image*head, split): [NB*16][NB*16] cross, [NB*16] |q|^2, [NB*16] |k|^2
@@ -49,14 +49,27 @@ __host__ __device__ constexpr int gram_lds_bytes() {
              : (4 * (NB * 16 * NB * 16 + 2 * NB * 16) * 4);
 }
 
+// The reduction tree of one (image, head): level 0 holds the nsplit split records, level l + 1
+// one record per group of CA_FAN consecutive level-l records; the level with one node is the
+// result. tree_nodes(n) = records of all levels, tree_counters(n) = nodes above level 0.
+__host__ __device__ inline int tree_nodes(int n) {
+  int t = n;
+  while (n > 1) {
+    n = (n + CA_FAN - 1) / CA_FAN;
+    t += n;
+  }
+  return t;
+}
+__host__ __device__ inline int tree_counters(int n) { return n > 1 ? tree_nodes(n) - n : 1; }
+
 struct GramP {
   const void* qkv;
-  float* part;          // [nh][nsplit + ngroups][rec]: split records, then group records
-  unsigned* cnt;        // [nh][CA_MAX_GROUPS + 1]: group counters, then the head's counter
+  float* part;          // [nh][tree_nodes(nsplit)][rec]: level 0 (the splits), then each level up
+  unsigned* cnt;        // [nh][tree_counters(nsplit)]: one arrival counter per node above level 0
   const float* temp;    // [heads]
   float* out;           // [nh][ch][ch]
   int64_t hw, split_len;
-  int c, ch, heads, nsplit, gsize, ngroups;
+  int c, ch, heads, nsplit;
 };
 
 // 8 x 8 transpose of bf16: in[i] = 8 channels of pixel i (u32 pairs), out[c] = 8 pixels of channel c
@@ -77,43 +90,34 @@ __device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&
 // (cache policy SC1), so no cache-wide writeback or invalidate is needed between them.
 constexpr int CA_SC1 = 1 << 4;  // cache-policy operand of the raw buffer loads / stores: SC1
 
-// dst[e] (LDS, e < REC) = sum over records r = 0 .. count - 1 of rec[r * REC + e] (records at
-// record index r0 of rs, a descriptor whose range is exactly rs_bytes), in record order (the
-// first record added to zero); loads 8 records deep. Lanes without a slot load at offset
-// rs_bytes, past the range, and read zero.
+// dst[e] (LDS, e < REC) = sum over records r = 0 .. count - 1 (count <= CA_FAN) of
+// rec[r * REC + e] (records at record index r0 of rs, a descriptor whose range is exactly
+// rs_bytes), in record order (the first record added to zero); every load issued before the
+// first add. Lanes without a slot, and records past count, load at offset rs_bytes, past the
+// range, and read zero.
 template <int REC>
 __device__ __forceinline__ void sum_records(__amdgpu_buffer_rsrc_t rs, uint32_t rs_bytes, int r0, int count,
                                             float* dst, int tid) {
   static_assert(REC % 4 == 0, "records of whole 16-byte groups");
   constexpr int SLOTS = REC / 4;
   constexpr int PER = (SLOTS + 255) / 256;
-  f32x4 acc[PER];
+  f32x4 v[CA_FAN][PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto ld = [&](int r, int i) __attribute__((always_inline)) {
-    const int e4 = tid + 256 * i;
-    const uint32_t o = e4 < SLOTS ? (uint32_t)(((r0 + r) * REC + e4 * 4) * 4) : rs_bytes;
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, CA_SC1));
-  };
-  int r = 0;
-  for (; r + 8 <= count; r += 8) {
-    f32x4 v[8][PER];
+  for (int j = 0; j < CA_FAN; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) v[j][i] = ld(r + j, i);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) acc[i] += v[j][i];
-  }
-  for (; r < count; ++r)
-#pragma unroll
-    for (int i = 0; i < PER; ++i) acc[i] += ld(r, i);
+    for (int i = 0; i < PER; ++i) {
+      const int e4 = tid + 256 * i;
+      const uint32_t o = (e4 < SLOTS && j < count) ? (uint32_t)(((r0 + j) * REC + e4 * 4) * 4) : rs_bytes;
+      v[j][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, CA_SC1));
+    }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < CA_FAN; ++j)
+      if (j < count) acc += v[j][i];
     const int e4 = tid + 256 * i;
-    if (e4 < SLOTS) *reinterpret_cast<f32x4*>(dst + e4 * 4) = acc[i];
+    if (e4 < SLOTS) *reinterpret_cast<f32x4*>(dst + e4 * 4) = acc;
   }
 }
 
@@ -333,7 +337,7 @@ __global__ void __launch_bounds__(256) gram_kernel(GramP p) {
     }
   }
   __syncthreads();
-  const int nrec = p.nsplit + p.ngroups;
+  const int nrec = tree_nodes(p.nsplit);
   const uint32_t recs_bytes = (uint32_t)(nrec * REC * 4);  // this (image, head)'s records
   const __amdgpu_buffer_rsrc_t recs = buf_rsrc_n(p.part + (int64_t)nh * nrec * REC, recs_bytes);
   {
@@ -343,19 +347,23 @@ __global__ void __launch_bounds__(256) gram_kernel(GramP p) {
     store_record<REC>(recs, split, red, tid);
   }
 
-  // ---- the reduction over splits: the last arrival of a group sums the group, the last group
-  // the head (each in a fixed order)
-  unsigned* cnt = p.cnt + (int64_t)nh * (CA_MAX_GROUPS + 1);
-  const int g = split / p.gsize;
-  const int g0 = g * p.gsize;
-  const int g1 = g0 + p.gsize < p.nsplit ? g0 + p.gsize : p.nsplit;
-  if (!arrive_last(cnt + g, (unsigned)(g1 - g0), &s_flag, tid)) return;
-  sum_records<REC>(recs, recs_bytes, g0, g1 - g0, red, tid);
-  if (p.ngroups > 1) {
+  // ---- the reduction over splits, up the tree: the last arrival at a node sums its (up to
+  // CA_FAN) children in order and carries on one level up; the last at the root has the sums
+  unsigned* cnt = p.cnt + (int64_t)nh * tree_counters(p.nsplit);
+  int n = p.nsplit, base = 0, cbase = 0, r = split;
+  for (;;) {
+    const int g = r / CA_FAN, c0 = g * CA_FAN;
+    const int members = n - c0 < CA_FAN ? n - c0 : CA_FAN;
+    if (!arrive_last(cnt + cbase + g, (unsigned)members, &s_flag, tid)) return;
+    sum_records<REC>(recs, recs_bytes, base + c0, members, red, tid);
+    const int up = (n + CA_FAN - 1) / CA_FAN;
+    if (up == 1) break;  // the root: red holds this (image, head)'s sums
     __syncthreads();
-    store_record<REC>(recs, p.nsplit + g, red, tid);
-    if (!arrive_last(cnt + CA_MAX_GROUPS, (unsigned)p.ngroups, &s_flag, tid)) return;
-    sum_records<REC>(recs, recs_bytes, p.nsplit, p.ngroups, red, tid);
+    store_record<REC>(recs, base + n + g, red, tid);
+    base += n;
+    cbase += up;
+    n = up;
+    r = g;
   }
   __syncthreads();
 
@@ -408,39 +416,33 @@ static int pick_nb(int64_t ch) { return (int)((ch + 15) / 16); }
 struct GramPlan {
   int64_t nh;         // (image, head) pairs per launch
   int64_t split_len;  // pixels per split (a multiple of 2 chunks)
-  int nsplit, gsize, ngroups;
+  int nsplit;
 };
 
 // Splits: about 2 workgroups per CU over the launch (measured at the config-4 levels against 3
 // and 4: fewer records to sum, same pixel rate), at least two chunks per split, a split's bytes
-// (plus the chunks read past it) addressable with 32-bit offsets; groups: about sqrt(nsplit)
-// of them, at most CA_MAX_GROUPS.
+// (plus the chunks read past it) addressable with 32-bit offsets. The (image, head) pairs of a
+// launch are bounded by the counters their trees need.
 static GramPlan gram_plan(int64_t batch, int64_t heads, int64_t hw, int64_t c) {
   GramPlan g;
-  const int64_t imgs = batch < CA_MAX_NH / heads ? batch : CA_MAX_NH / heads;
-  g.nh = imgs * heads;
+  int64_t imgs = batch < CA_MAX_NH / heads ? batch : CA_MAX_NH / heads;
   const int64_t chunks = cdiv(hw, GP_CHUNK);
   const int64_t row_bytes = 3 * c * 4;  // fp32 rows: the same plan (and workspace) for both dtypes
-  const int64_t want = cdiv(2LL * device_cus(), g.nh);
+  const int64_t want = cdiv(2LL * device_cus(), imgs * heads);
   int64_t per = cdiv(chunks, want);
   per = per < 2 ? 2 : (per + 1) / 2 * 2;
   const int64_t max_per = ((((int64_t)1 << 30) / (GP_CHUNK * row_bytes)) / 2) * 2;
   if (per > max_per) per = max_per < 2 ? 2 : max_per;
   g.split_len = per * GP_CHUNK;
   g.nsplit = (int)cdiv(hw, g.split_len);
-  int ng = 1;
-  if (g.nsplit > 8) {
-    ng = 1;
-    while ((int64_t)ng * ng < g.nsplit) ++ng;
-    if (ng > CA_MAX_GROUPS) ng = CA_MAX_GROUPS;
-  }
-  g.gsize = (int)cdiv(g.nsplit, ng);
-  g.ngroups = (int)cdiv(g.nsplit, g.gsize);
+  const int64_t per_nh = tree_counters(g.nsplit);
+  if (imgs * heads * per_nh > CA_COUNTERS) imgs = CA_COUNTERS / (per_nh * heads);
+  g.nh = (imgs < 1 ? 1 : imgs) * heads;
   return g;
 }
 
 static int64_t gram_workspace_bytes(const GramPlan& g, int64_t ch) {
-  return CA_COUNTER_BYTES + g.nh * (int64_t)(g.nsplit + g.ngroups) * gram_rec_floats(pick_nb(ch)) * 4;
+  return CA_COUNTER_BYTES + g.nh * (int64_t)tree_nodes(g.nsplit) * gram_rec_floats(pick_nb(ch)) * 4;
 }
 
 // Launches gram_kernel per batch slice of at most CA_MAX_NH (image, head) pairs, with `scratch`
@@ -453,7 +455,7 @@ static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const fl
   const int nb = pick_nb(ch);
   const int64_t imgs = g.nh / heads;
   const int64_t img_bytes = hw * 3 * c * (qkv_dtype == DT_BF16 ? 2 : 4);
-  note_kernel("gram_kernel nb=%d nsplit=%d groups=%d", nb, g.nsplit, g.ngroups);
+  note_kernel("gram_kernel nb=%d nsplit=%d", nb, g.nsplit);
   for (int64_t i0 = 0; i0 < batch; i0 += imgs) {
     const int64_t ni = batch - i0 < imgs ? batch - i0 : imgs;
     GramP p;
@@ -468,8 +470,6 @@ static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const fl
     p.ch = (int)ch;
     p.heads = (int)heads;
     p.nsplit = g.nsplit;
-    p.gsize = g.gsize;
-    p.ngroups = g.ngroups;
     dim3 grid((unsigned)g.nsplit, (unsigned)(ni * heads));
 #define CLARUS_GRAM(NB)                                                                                   \
   do {                                                                                                    \

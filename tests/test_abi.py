@@ -123,7 +123,7 @@ def test_validation_rejects_before_launch(lib):
 def test_noalloc_attention_rejects_oversized_shapes_before_launch(lib):
     """clarus_hip_channel_attention_noalloc checks the partials' size against its static scratch on
     the host, before it looks up the device array or launches anything."""
-    big = (64, 64, 512, 8)  # batch, hw, c, heads: 512 (image, head) records of 64 x 64
+    big = (64, 65536, 512, 8)  # batch, hw, c, heads: 496 (image, head) trees of 3 records of 64 x 64 per launch
     need = lib.clarus_hip_channel_attention_workspace(*big)
     assert need > _lib.CHANNEL_ATTENTION_SCRATCH_MAX
     assert lib.clarus_hip_channel_attention_noalloc(16, _lib.BF16, 16, 16, *big, None) == _lib.EINVAL
