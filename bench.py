@@ -454,7 +454,8 @@ def main() -> None:
                "gbs": round(c.nbytes / us / 1e3, 1), "bound": bound, "t_bound_us": round(tb * 1e6, 2),
                "frac": round(tb * 1e6 / us, 3),
                "frac_hbm": round(c.nbytes / wl.PEAK_HBM * 1e6 / us, 3),
-               "frac_mfma": round(c.flops / wl.PEAK_FLOPS[c.dtype] * 1e6 / us, 3),
+               "frac_mfma": round(c.flops / wl.PEAK_FLOPS[c.mfma or c.dtype] * 1e6 / us, 3),
+               "frac_mfma_fp32": round(c.flops / wl.PEAK_FLOPS["fp32"] * 1e6 / us, 3) if c.dtype == "fp32" else None,
                "timing": timing, "reps": reps, "kernel": wl.kernel_of(c)}
         p = pmc.get(c.name)
         if p:
@@ -471,7 +472,7 @@ def main() -> None:
     if bound == "hbm":
         ach, peak, unit = dc.nbytes / dus / 1e3, wl.PEAK_HBM / 1e9, "GB/s"
     else:
-        ach, peak, unit = dc.flops / dus / 1e6, wl.PEAK_FLOPS[dc.dtype] / 1e12, "TFLOP/s"
+        ach, peak, unit = dc.flops / dus / 1e6, wl.PEAK_FLOPS[dc.mfma or dc.dtype] / 1e12, "TFLOP/s"
     roofline = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": unit, "frac": round(ach / peak, 3),
                 "traffic": pmc.get(dc.name, {}).get("traffic_bytes"), "op": dc.name, "avg_us": round(dus, 2),
                 "kernel": rows[di]["kernel"], "algorithmic_bytes": int(dc.nbytes), "algorithmic_flops": int(dc.flops)}

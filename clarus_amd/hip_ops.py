@@ -213,8 +213,15 @@ class HipOps(Backend):
 
     def _wp_for(self, a, w, k, nout, gate, act, m, res=None):
         """("wr" | "wp", W^T packed) when this plain bf16 GEMM goes to clarus_hip_gemm_wr /
-        clarus_hip_gemm_wp, else None."""
+        clarus_hip_gemm_wp, else None. Square plain GEMMs that clarus_hip_gemm serves on its W-slice
+        kernel (N = K = 128 / 256 / 512, no residual, gate or activation, M <= 80000: the NAFNet SCA
+        GEMMs on the TLC map) stay there: cold, us, 75881 x 128 x 128: 16.3 against 18.0 on
+        clarus_hip_gemm_wr; 19125 x 256 x 256: 14.3 against 16.0. (Other shapes, e.g. conv1's
+        N = 2K, were not measured on it and keep the kernels below.)"""
         nw = (2 if gate else 1) * nout
+        if (res is None and not gate and act == 0 and nout == k and m <= 80000 and k in (128, 256, 512)
+                and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16):
+            return None
         if (self.wres and k in self.wres_ks and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
                 and act in (0, _lib.ACT_GELU) and nout % 16 == 0
                 and (res is None or (nout % 256 == 0 if gate else (nout == 256 or (res.dtype == torch.bfloat16

@@ -9,7 +9,8 @@ plan; they are fixed by the op and shape, not read from counters):
     c -> c + bias, * beta, + residual  : F = 2 M c^2, B = 2Mc + 2 r M c + 2c^2 + 8c,
                                          r = 2 (bf16 residual / output) for c < 512, 4 (fp32) above
   config 3 (patch DFT, fp32, fused fwd 64->80 / filter / inv 80->64) per patch-channel:
-    F = 2*64*80 + 6*40 + 2*80*64, B = 4*64 (in) + 4*64 (out)
+    F = 2*64*80 + 6*40 + 2*80*64, B = 4*64 (in) + 4*64 (out); F priced at the bf16 MFMA peak (the
+    kernels issue bf16 MFMAs, three per fp32-accurate product), so the bound is the HBM floor
   config 4 (Restormer MDTA, level l: C = 48 * 2^l, heads 2^l, HW = 921600 / 4^l), e = element size
     Gram + norms : F = heads (2 * 48^2 HW + 4 * 48 HW), B = 2 C HW e + heads * 48^2 * 4
     attn . V     : F = heads * 2 * 48^2 HW,          B = 2 C HW e
@@ -45,9 +46,14 @@ class OpCase:
     # take minutes); the reported CPU time is the sample's times cpu_scale
     cpu_scale: float = 1.0
     cpu_sample: str = ""
+    # the MFMA instructions the kernel issues, whose peak prices the algorithmic flops (default:
+    # the arithmetic type). The patch DFT ops compute fp32-accurate products as three bf16 MFMAs,
+    # so their flops are priced at the bf16 peak, in config 3 as in the fused FFTformer DFFN op:
+    # one rule for both, with the HBM floor as the bound wherever it is the larger
+    mfma: str = ""
 
     def t_bound(self) -> tuple[float, str]:
-        tm = self.flops / PEAK_FLOPS[self.dtype]
+        tm = self.flops / PEAK_FLOPS[self.mfma or self.dtype]
         tb = self.nbytes / PEAK_HBM
         # fp64 ops (the metrics) run on the vector ALUs; MI355X's fp64 vector and matrix peaks agree
         return (tm, "fp64" if self.dtype == "fp64" else "mfma") if tm >= tb else (tb, "hbm")
@@ -160,7 +166,7 @@ def config3_cases(hip32, device, seed: int = 0) -> list[OpCase]:
         cases.append(OpCase(f"patch_filter fused C{c} {h}x{w}", 3, "fp32",
                             units * (2.0 * 64 * 80 + 6 * 40 + 2.0 * 80 * 64), units * 4.0 * 128,
                             lambda x=x, f=f: hip32.patch_filter(x, f), {"x": xh, "f": fh},
-                            lambda r, x=xh, f=fh: r.patch_filter(x, f)))
+                            lambda r, x=xh, f=fh: r.patch_filter(x, f), mfma="bf16"))
     return cases
 
 
