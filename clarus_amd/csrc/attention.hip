@@ -1,7 +1,7 @@
 // Restormer MDTA attention map on gfx950:
 //   A[n, hd] = softmax( (q / |q|) (k / |k|)^T * t[hd] ),  q, k: [HW, c_h] head slices of qkv.
 //
-// One launch, gram_kernel, grid (nsplit, images * heads), 256 threads.
+// One launch, gram_kernel, one workgroup per (image, split, head), 256 threads.
 // Pixel phase: each workgroup reduces a contiguous pixel range (a split) in chunks of 128
 // pixels. A thread owns one unit of every chunk: 8 consecutive pixels x one 16-byte channel group
 // of q or k (two units for fp32), loaded one chunk ahead through a buffer descriptor whose range
@@ -69,7 +69,7 @@ struct GramP {
   const float* temp;    // [heads]
   float* out;           // [nh][ch][ch]
   int64_t hw, split_len;
-  int c, ch, heads, nsplit;
+  int c, ch, heads, nsplit, nimg;
 };
 
 // 8 x 8 transpose of bf16: in[i] = 8 channels of pixel i (u32 pairs), out[c] = 8 pixels of channel c
@@ -159,8 +159,16 @@ __global__ void __launch_bounds__(256) gram_kernel(GramP p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 15, lg = lane >> 4;
-  const int nh = blockIdx.y, split = blockIdx.x;
-  const int img = nh / p.heads, hd = nh - img * p.heads;
+  // XCD-aware order: workgroup L runs on XCD L % 8; the heads of one (image, split) are workgroups
+  // L, L + 8, L + 16, ... of one XCD, dispatched back to back, so the 128-byte lines that heads
+  // share (a pixel row holds every head's q and k channels) come from HBM into one L2 once.
+  // Workgroups past the last split of a row of 8 have nothing to do.
+  const int L = blockIdx.x, xcd = L & 7, r8 = L >> 3;
+  const int hd = r8 % p.heads, sblk = r8 / p.heads;
+  const int is = sblk * 8 + xcd;            // (image, split) index
+  const int img = is / p.nsplit, split = is - img * p.nsplit;
+  if (img >= p.nimg) return;
+  const int nh = img * p.heads + hd;
   const int ch = p.ch;
   const int64_t p_begin = (int64_t)split * p.split_len;
   const int64_t p_end = p_begin + p.split_len < p.hw ? p_begin + p.split_len : p.hw;
@@ -470,7 +478,8 @@ static int launch_channel_attention(const void* qkv, int32_t qkv_dtype, const fl
     p.ch = (int)ch;
     p.heads = (int)heads;
     p.nsplit = g.nsplit;
-    dim3 grid((unsigned)g.nsplit, (unsigned)(ni * heads));
+    p.nimg = (int)ni;
+    dim3 grid((unsigned)(cdiv(ni * g.nsplit, 8) * 8 * heads));
 #define CLARUS_GRAM(NB)                                                                                   \
   do {                                                                                                    \
     if (qkv_dtype == DT_BF16) hipLaunchKernelGGL((gram_kernel<NB, DT_BF16>), grid, dim3(256), 0, s, p);  \
