@@ -61,6 +61,29 @@ def test_channel_attention_head_widths(ch, hip_f32):
                 rel=1e-5, what=f"channel_attention ch{ch}")
 
 
+def test_channel_attention_launch_slices_and_reuse(hip_f32):
+    """More (image, head) pairs than one launch takes (70 images x 8 heads = 560 > 496: two
+    launches on the same arrival counters), against the oracle; the same call repeated, and again
+    after a larger call on the same cached workspace, bit-identical (every call leaves the counters
+    zero and sums in a fixed order)."""
+    g = gen(3)
+    heads, ch = 8, 8
+    qkv = rnd(g, 70, 6, 10, 3 * heads * ch)
+    t = torch.rand(heads, generator=g) + 0.5
+    print("[attention] 70 images x 8 heads, then 4 heads at 180x320", flush=True)
+    a1 = hip_f32.channel_attention(qkv.cuda(), heads, t.cuda())
+    assert_fp32(a1.cpu(), REF.channel_attention(qkv, heads, t), rel=1e-5, what="channel_attention 70 images")
+    a2 = hip_f32.channel_attention(qkv.cuda(), heads, t.cuda())
+    big = rnd(g, 1, 180, 320, 3 * 192)
+    tb = torch.rand(4, generator=g) + 0.5
+    b1 = hip_f32.channel_attention(big.cuda(), 4, tb.cuda())
+    a3 = hip_f32.channel_attention(qkv.cuda(), heads, t.cuda())
+    b2 = hip_f32.channel_attention(big.cuda(), 4, tb.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(a1, a2) and torch.equal(a1, a3) and torch.equal(b1, b2)
+    assert_fp32(b1.cpu(), REF.channel_attention(big, 4, tb), rel=1e-5, what="channel_attention 180x320")
+
+
 CONFIG4 = [(0, 720, 1280), (1, 360, 640), (2, 180, 320), (3, 90, 160)]
 
 
