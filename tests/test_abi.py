@@ -52,6 +52,13 @@ def test_validation_rejects_before_launch(lib):
     cv = _lib.ConvArgs(x=16, wt=16, out=16, batch=1, h=4, w=4, cin=12, cout=8, ldx=12, ldo=8)
     assert lib.clarus_hip_conv3x3(ctypes.byref(cv), None) == _lib.EINVAL  # cin % 8 != 0
     assert lib.clarus_hip_channel_attention(16, 1, 16, 16, 1, 64, 30, 2, 16, 0, None) == _lib.EINVAL
+    # more heads than one launch's arrival counters cover (496), a workspace short of the size
+    assert lib.clarus_hip_channel_attention(16, 1, 16, 16, 1, 64, 512 * 8, 512, 16, 1 << 30, None) == _lib.EINVAL
+    assert b"heads" in lib.clarus_hip_last_error()
+    need = lib.clarus_hip_channel_attention_workspace(1, 64, 96, 2)
+    assert need > 64 * 1024  # the counters come first
+    assert lib.clarus_hip_channel_attention(16, 1, 16, 16, 1, 64, 96, 2, 16, need - 16, None) == _lib.EINVAL
+    assert b"scratch" in lib.clarus_hip_last_error()
     assert lib.clarus_hip_patch_corr(16, 0, 0, 0, 0, 16, 16, 16, 1, 12, 16, 8, None) == _lib.EINVAL  # h % 8
     a = _lib.GemmArgs(a=16, m=10, k=64, batch=1, lda=64, pro=0, a_dtype=_lib.BF16)
     assert lib.clarus_hip_rows_split(ctypes.byref(a), 16, None) == _lib.EINVAL  # bf16 rows, no prologue
