@@ -23,6 +23,10 @@
 //   * epilogue in the MFMA layout (a lane holds 16 consecutive output channels of one pixel) with
 //     buffer stores bounded to the tile's valid rows, so every wave issues the same number of
 //     stores and the wait at the next tile's top can leave them in flight.
+// A pass with at most 256 real W^T rows (N <= 256, or N <= 128 with the gate) leaves waves 4 - 7
+// holding padding; HALF then gives wave w + 4 the rows of wave w and splits the tile's pixels
+// between them (wave w: pixels 0 .. 31, wave w + 4: 32 .. 63), so every SIMD runs two working
+// waves and one wave's epilogue overlaps the other's products (the same sums, bit for bit).
 // Workgroups go to the XCDs in turn (XCD = block % 8); each XCD owns a contiguous range of pixel
 // tiles and its workgroups split into the passes, so an A tile is fetched into one L2 for all of
 // its passes. Memory waits are explicit vmcnt counts (copies, loads and stores complete in issue
@@ -62,8 +66,9 @@ struct WrP {
 };
 
 // GATE: SimpleGate pairs (256 output channels per pass); RDT: residual dtype (-1 none); CDT:
-// output dtype; K: 128 or 256; RC: residual channels staged per row (256, or 512 without the gate)
-template <bool GATE, int RDT, int CDT, int K, int RC>
+// output dtype; K: 128 or 256; RC: residual channels staged per row (256, or 512 without the gate);
+// HALF: one pass of at most 256 real W^T rows, its pixels split over wave pairs
+template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF>
 __global__ void __launch_bounds__(WR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wres_kernel(const WrP p) {
   constexpr int KS = K / 16;                 // 16-k steps
@@ -75,7 +80,8 @@ wres_kernel(const WrP p) {
   constexpr int RB = wr_res_row_bytes(RC, RDT);
   constexpr int NR = RDT < 0 ? 0 : WR_P * RB / 1024 / WR_WAVES;  // residual copies per wave
   constexpr int OES = CDT == DT_F32 ? 4 : 2;
-  constexpr int NS = 2 * (GATE ? 1 : 2) * (16 * OES / 16);  // 16-byte stores per lane per tile
+  constexpr int NPB = HALF ? 1 : 2;          // 32-pixel blocks per wave and tile
+  constexpr int NS = NPB * (GATE ? 1 : 2) * (16 * OES / 16);  // 16-byte stores per lane per tile
   static_assert(RDT < 0 || (WR_P * RB) % (1024 * WR_WAVES) == 0, "residual copies per wave");
   static_assert(RDT < 0 || RC >= NO || !GATE, "the gate stages all 256 channels");
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -95,13 +101,14 @@ wres_kernel(const WrP p) {
   if (t_first >= t_hi) return;
   const int64_t och = (int64_t)pass * NO;  // first output channel of the pass
   // waves whose 64 W^T rows (32 output channels with the gate) are all padding
-  const bool active = (GATE ? och + 32 * wave : och + 64 * wave) < p.n;
+  const int wrow = HALF ? (wave & 3) : wave;  // the wave whose W^T rows this wave holds
+  const bool active = (GATE ? och + 32 * wrow : och + 64 * wrow) < p.n;
   const bool scaled = p.scale != nullptr || p.out_scale != 1.f;  // else the scale table is all 1
 
   // ---- this wave's W^T fragments of the pass, all of K, into registers
   bf16x8 wf[KS][2];
   {
-    const unsigned char* wsrc = (const unsigned char*)p.wp + (((int64_t)pass * WR_WAVES + wave) * KS * 2 * 64 + lane) * 16;
+    const unsigned char* wsrc = (const unsigned char*)p.wp + (((int64_t)pass * WR_WAVES + wrow) * KS * 2 * 64 + lane) * 16;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -141,7 +148,7 @@ wres_kernel(const WrP p) {
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[NPB][2];
   issue_a(t_first, 0, lane, wave);
   // ---- tables (after the W^T loads and the first copies, so the three latencies overlap): bias of the pass's W^T rows (gate: the first halves' 256, then the second
   // halves'), scale of its output channels (1 for none, 0 bias for none; 0 past n)
@@ -153,9 +160,10 @@ wres_kernel(const WrP p) {
     if (c < NO) tb[512 + c] = ((p.scale && och + c < p.n) ? p.scale[och + c] : 1.f) * p.out_scale;
   }
   // ---- one tile: the products of A(t) from buffer bf into acc, then its epilogue
-  auto kloop = [&](const int bf, const int l32, const int hl) __attribute__((always_inline)) {
+  // pixel block i of this wave: i, or with HALF the wave pair's half ph
+  auto kloop = [&](const int bf, const int l32, const int hl, const int ph) __attribute__((always_inline)) {
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < NPB; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -164,12 +172,12 @@ wres_kernel(const WrP p) {
     // A fragments one 16-k step ahead of the MFMAs (the scheduling barriers keep the reads of
     // later steps from being hoisted, which would take a register per read)
     const unsigned char* ab = lds + bf * ABYTES;
-    bf16x8 af[2][2];
+    bf16x8 af[2][NPB];
     auto read_a = [&](int s, int buf) __attribute__((always_inline)) {
 #pragma unroll
-      for (int pb = 0; pb < 2; ++pb) {
-        const int row = pb * 32 + l32;
-        af[buf][pb] = *reinterpret_cast<const bf16x8*>(ab + row * ROWB + ((2 * s + hl) ^ (row & 15)) * 16);
+      for (int i = 0; i < NPB; ++i) {
+        const int row = (HALF ? ph : i) * 32 + l32;
+        af[buf][i] = *reinterpret_cast<const bf16x8*>(ab + row * ROWB + ((2 * s + hl) ^ (row & 15)) * 16);
       }
     };
     read_a(0, 0);
@@ -177,9 +185,9 @@ wres_kernel(const WrP p) {
     for (int s = 0; s < KS; ++s) {
       if (s + 1 < KS) read_a(s + 1, (s + 1) & 1);
 #pragma unroll
-      for (int pb = 0; pb < 2; ++pb)
+      for (int i = 0; i < NPB; ++i)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) acc[pb][rb] = mfma32_bf16(wf[s][rb], af[s & 1][pb], acc[pb][rb]);
+        for (int rb = 0; rb < 2; ++rb) acc[i][rb] = mfma32_bf16(wf[s][rb], af[s & 1][i], acc[i][rb]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -193,13 +201,15 @@ wres_kernel(const WrP p) {
   const int nval = (int)(p.n - och < NO ? p.n - och : NO);  // output channels of the pass
   const __amdgpu_buffer_rsrc_t cr =
       buf_rsrc_n((unsigned char*)p.c + (q0 * p.ldc + och) * OES, (uint32_t)((rows_ok - 1) * p.ldc * OES + nval * OES));
+  const int wr = HALF ? (wave & 3) : wave, ph = wave >> 2;  // row-owning wave, pixel half
   if (active) {
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb) {
+    for (int ib = 0; ib < NPB; ++ib) {
+      const int pb = HALF ? ph : ib;
       const int px = pb * 32 + l32;
 #pragma unroll
       for (int rb = 0; rb < (GATE ? 1 : 2); ++rb) {
-        const int c0 = GATE ? wave * 32 + hl * 16 : wave * 64 + rb * 32 + hl * 16;
+        const int c0 = GATE ? wr * 32 + hl * 16 : wr * 64 + rb * 32 + hl * 16;
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -207,10 +217,10 @@ wres_kernel(const WrP p) {
           if constexpr (GATE) {
             const f32x4 b2 = *reinterpret_cast<const f32x4*>(tb + 256 + c0 + 4 * i);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[ib][0][4 * i + e] + b1[e]) * (acc[ib][1][4 * i + e] + b2[e]);
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[ib][rb][4 * i + e] + b1[e];
           }
         }
         if (p.act == ACT_GELU) {
@@ -300,7 +310,7 @@ wres_kernel(const WrP p) {
     issue_r(t, ln, wv);
     if (has_next) issue_a(t + R, bf ^ 1, ln, wv);
     asm volatile("" ::: "memory");
-    kloop(bf, l32, hl);
+    kloop(bf, l32, hl, wv >> 2);
     // the residual copies (issued before the next tile's A copies) have landed, in every wave
     if constexpr (RDT >= 0) {
       if (has_next) wait_vmcnt<NA>();
@@ -313,10 +323,10 @@ wres_kernel(const WrP p) {
   }
 }
 
-template <bool GATE, int RDT, int CDT, int K, int RC>
+template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF>
 void launch(const WrP& p, int nblk, hipStream_t s) {
   constexpr int lds = wr_lds_bytes(K, RC, RDT);
-  auto fn = &wres_kernel<GATE, RDT, CDT, K, RC>;
+  auto fn = &wres_kernel<GATE, RDT, CDT, K, RC, HALF>;
   static const bool attr = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
@@ -326,15 +336,20 @@ void launch(const WrP& p, int nblk, hipStream_t s) {
 }
 
 template <bool GATE, int RDT, int CDT, int RC>
-void launch_k(const WrP& p, int k, int nblk, hipStream_t s) {
-  if (k == 128) launch<GATE, RDT, CDT, 128, RC>(p, nblk, s);
-  else launch<GATE, RDT, CDT, 256, RC>(p, nblk, s);
+void launch_k(const WrP& p, int k, bool half, int nblk, hipStream_t s) {
+  if (half) {
+    if (k == 128) launch<GATE, RDT, CDT, 128, RC, true>(p, nblk, s);
+    else launch<GATE, RDT, CDT, 256, RC, true>(p, nblk, s);
+  } else {
+    if (k == 128) launch<GATE, RDT, CDT, 128, RC, false>(p, nblk, s);
+    else launch<GATE, RDT, CDT, 256, RC, false>(p, nblk, s);
+  }
 }
 
 template <bool GATE, int RDT, int RC>
-void launch_c(const WrP& p, int cdt, int k, int nblk, hipStream_t s) {
-  if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC>(p, k, nblk, s);
-  else launch_k<GATE, RDT, DT_BF16, RC>(p, k, nblk, s);
+void launch_c(const WrP& p, int cdt, int k, bool half, int nblk, hipStream_t s) {
+  if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC>(p, k, half, nblk, s);
+  else launch_k<GATE, RDT, DT_BF16, RC>(p, k, half, nblk, s);
 }
 
 }  // namespace
@@ -384,18 +399,20 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
   p.npass = (int)npass; p.ptiles = (int)ptiles; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
   const int rdt = a->res ? a->r_dtype : -1;
-  note_kernel("wres_kernel gate=%d res=%d k=%lld", (int)gate, rdt, (long long)a->k);
+  // one pass with at most 256 real W^T rows: waves 4 - 7 take the pixel halves (HALF)
+  const bool half = npass == 1 && (gate ? a->n <= 128 : a->n <= 256);
+  note_kernel("wres_kernel gate=%d res=%d k=%lld half=%d", (int)gate, rdt, (long long)a->k, (int)half);
   hipStream_t s = (hipStream_t)stream;
   const int k = (int)a->k, cdt = a->c_dtype;
   if (gate) {
-    if (rdt == DT_F32) launch_c<true, DT_F32, 256>(p, cdt, k, nblk, s);
-    else if (rdt == DT_BF16) launch_c<true, DT_BF16, 256>(p, cdt, k, nblk, s);
-    else launch_c<true, -1, 256>(p, cdt, k, nblk, s);
+    if (rdt == DT_F32) launch_c<true, DT_F32, 256>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16) launch_c<true, DT_BF16, 256>(p, cdt, k, half, nblk, s);
+    else launch_c<true, -1, 256>(p, cdt, k, half, nblk, s);
   } else {
-    if (rdt == DT_F32) launch_c<false, DT_F32, 256>(p, cdt, k, nblk, s);
-    else if (rdt == DT_BF16 && rc == 512) launch_c<false, DT_BF16, 512>(p, cdt, k, nblk, s);
-    else if (rdt == DT_BF16) launch_c<false, DT_BF16, 256>(p, cdt, k, nblk, s);
-    else launch_c<false, -1, 256>(p, cdt, k, nblk, s);
+    if (rdt == DT_F32) launch_c<false, DT_F32, 256>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16 && rc == 512) launch_c<false, DT_BF16, 512>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16) launch_c<false, DT_BF16, 256>(p, cdt, k, half, nblk, s);
+    else launch_c<false, -1, 256>(p, cdt, k, half, nblk, s);
   }
   return check_launch("gemm_wr");
 }

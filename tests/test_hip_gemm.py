@@ -303,14 +303,17 @@ def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     (False, 256, 1024, None, torch.bfloat16, None, 3000),
     (False, 128, 96, None, torch.float32, None, 200),
     (True, 128, 256, torch.bfloat16, torch.float32, None, 64 * 40 + 7),
+    (False, 128, 256, torch.float32, torch.float32, None, 64 * 7 + 5),
+    (True, 128, 128, None, torch.bfloat16, None, 64 * 300 + 3),
 ])
 def test_gemm_wr_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     """Through the C ABI, clarus_hip_gemm_wr (persistent workgroups with their W^T pass resident in
     registers, packed and padded by HipOps._wr_pack): K = 128 / 256, SimpleGate, GELU, no / bf16 /
-    fp32 residual, bf16 / fp32 output, out_scale, one to two passes, output widths that leave
-    waves idle (gated 128, plain 96 and 256), a ragged last tile, more tiles than workgroups (3000
-    and 2567 rows), bias / scale left out in one case. Held to the fp32 oracle as
-    clarus_hip_gemm_wp."""
+    fp32 residual, bf16 / fp32 output, out_scale, one to two passes, a ragged last tile, more tiles
+    than workgroups (3000, 2567 and 19203 rows), bias / scale left out in one case. Output widths
+    of one pass with at most 256 real W^T rows (gated 128, plain 96 and 256, with and without a
+    residual) run the wave-pair pixel split; 96 also leaves row groups idle. Held to the fp32
+    oracle as clarus_hip_gemm_wp."""
     import ctypes
 
     from clarus_amd import _lib
