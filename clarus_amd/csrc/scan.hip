@@ -210,19 +210,55 @@ __global__ void __launch_bounds__(64) scan_kernel(const ScanP p) {
   }
 }
 
-// one thread per (crop, state, channel): the segments' start states in order
+// one thread per (crop, state, channel): the segments' start states in order. The chain's inputs
+// (sum delta and end state of each segment) do not depend on it: they are loaded CB segments at a
+// time, the next batch in flight while the current one runs, so the chain waits on memory once
+// per batch. (Loaded inside the chain, after the previous segment's store that the compiler
+// could not tell apart from them, every step waited a full memory round trip: 342 segments of the
+// EVSSM level-0 scan took 179 us.) 2 CB loads per batch: the next batch's stay within the 63
+// loads a wait count can leave in flight.
+constexpr int CB = 16;
+
 __global__ void __launch_bounds__(256) carry_kernel(const ScanP p) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // n * d + channel
   const int64_t t = blockIdx.y;
   if (i >= NS * p.d) return;
   const int64_t n = i / p.d, d = i - n * p.d;
   const float a = p.a2[d * NS + n];
+  const int64_t nseg = p.nseg, sd = p.d, se = NS * p.d;  // strides between segments
+  const float* __restrict__ dsum = p.dsum + t * nseg * sd + d;
+  const float* __restrict__ eh = p.eh + (t * nseg * NS + n) * sd + d;
+  // start states through the crop's range (a wave-uniform descriptor, the lane's element in the
+  // offset): the stores of the padding segments of the last batch go past the range and are
+  // dropped, so every batch issues the same loads and stores (straight-line code: the waits are
+  // exact counts)
+  const __amdgpu_buffer_rsrc_t h0 = buf_rsrc_n(p.h0 + t * nseg * se, (uint32_t)(nseg * se * 4));
+  const int64_t lo = n * sd + d;  // the lane's element within a segment's states
+  float ds[2][CB], e[2][CB];
+  auto load = [&](const int buf, const int64_t s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int64_t s = s0 + j < nseg ? s0 + j : nseg - 1;
+      ds[buf][j] = dsum[s * sd];
+      e[buf][j] = eh[s * se];
+    }
+  };
   float h = 0.f;
-  for (int64_t s = 0; s < p.nseg; ++s) {
-    const int64_t ts = t * p.nseg + s;
-    p.h0[(ts * NS + n) * p.d + d] = h;
-    const float ld = a * p.dsum[ts * p.d + d];
-    h = exp2f(fmaxf(ld, -126.0f)) * (h * exp2f(fminf(ld + 126.0f, 0.0f))) + p.eh[(ts * NS + n) * p.d + d];
+  auto run = [&](const int buf, const int64_t s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int64_t s = s0 + j;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), h0, s < nseg ? (int)((s * se + lo) * 4) : 0x7ffffff0, 0, 0);
+      const float ld = a * ds[buf][j];
+      h = exp2f(fmaxf(ld, -126.0f)) * (h * exp2f(fminf(ld + 126.0f, 0.0f))) + e[buf][j];
+    }
+  };
+  load(0, 0);
+  for (int64_t s0 = 0; s0 < nseg; s0 += 2 * CB) {
+    load(1, s0 + CB);
+    run(0, s0);
+    load(0, s0 + 2 * CB);
+    run(1, s0 + CB);
   }
 }
 
@@ -269,6 +305,8 @@ extern "C" int clarus_hip_selective_scan(const void* u, int32_t u_dtype, const f
   p.t = t; p.l = l; p.d = d; p.nc = nc; p.r = (int)r;
   p.seg = pick_seg(t, l, d);
   p.nseg = cdiv(l, p.seg);
+  // the carry kernel addresses a chain's start states with 32-bit byte offsets
+  CLARUS_REQUIRE(p.nseg * NS * d * (int64_t)sizeof(float) < ((int64_t)1 << 31), "selective_scan: too many segments");
   float* sc = (float*)scratch;
   p.dsum = sc;
   p.eh = sc + t * p.nseg * d;
