@@ -131,27 +131,42 @@ __global__ void __launch_bounds__(256) ssim_tile_kernel(const MetricsP p) {
     }
   }
   __syncthreads();
-  // channel mix + horizontal pass, moments about 128
-  for (int e = threadIdx.x; e < MT_RH * MT_W * 3; e += 256) {
-    const int r = e / (MT_W * 3), rem = e - r * (MT_W * 3), c = rem / 3, k = rem - (rem / 3) * 3;
-    double s[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
-    for (int t = 0; t < 11; ++t) {
-      double m[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+  // channel mix + horizontal pass, moments about 128. A thread takes a run of HR consecutive
+  // output columns of one (row, channel): it mixes the HR + 10 pixels its windows span once per
+  // moment (in registers) and slides the 11 taps over them, instead of mixing every tap's pixel
+  // again for each output (11 times the mixing work). Per output the same sums in the same order.
+  constexpr int HR = 8, HRUNS = MT_W / HR;
+  static_assert(MT_W % HR == 0 && MT_RH * 3 * HRUNS <= 256, "one run per thread");
+  if ((int)threadIdx.x < MT_RH * 3 * HRUNS) {
+    const int e = threadIdx.x;
+    const int r = e / (3 * HRUNS), rem = e - r * (3 * HRUNS), k = rem / HRUNS, c0 = (rem - k * HRUNS) * HR;
+    const double w0 = cm[k * 3], w1 = cm[k * 3 + 1], w2 = cm[k * 3 + 2];
 #pragma unroll
-      for (int kk = 0; kk < 3; ++kk) {
-        const double wgt = cm[k * 3 + kk];
-        const double av = (double)ta[r][c + t][kk] - 128.0, bv = (double)tb[r][c + t][kk] - 128.0;
-        m[0] += wgt * av;
-        m[1] += wgt * bv;
-        m[2] += wgt * av * av;
-        m[3] += wgt * bv * bv;
-        m[4] += wgt * av * bv;
+    for (int q = 0; q < 5; ++q) {
+      double m[HR + 10];
+#pragma unroll
+      for (int j = 0; j < HR + 10; ++j) {
+        double mq = 0.0;
+#pragma unroll
+        for (int kk = 0; kk < 3; ++kk) {
+          const double wgt = kk == 0 ? w0 : (kk == 1 ? w1 : w2);
+          const double av = (double)ta[r][c0 + j][kk] - 128.0, bv = (double)tb[r][c0 + j][kk] - 128.0;
+          if (q == 0) mq += wgt * av;
+          else if (q == 1) mq += wgt * bv;
+          else if (q == 2) mq += wgt * av * av;
+          else if (q == 3) mq += wgt * bv * bv;
+          else mq += wgt * av * bv;
+        }
+        m[j] = mq;
       }
 #pragma unroll
-      for (int q = 0; q < 5; ++q) s[q] += g[t] * m[q];
-    }
+      for (int i = 0; i < HR; ++i) {
+        double sq = 0.0;
 #pragma unroll
-    for (int q = 0; q < 5; ++q) hm[q][r][c][k] = s[q];
+        for (int t = 0; t < 11; ++t) sq += g[t] * m[i + t];
+        hm[q][r][c0 + i][k] = sq;
+      }
+    }
   }
   __syncthreads();
   // vertical pass and the SSIM map, both constant sets
