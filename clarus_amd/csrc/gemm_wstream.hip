@@ -24,8 +24,13 @@
 //   * epilogue in the MFMA layout: a lane holds 16 consecutive output channels of one pixel.
 // Tiles are dealt XCD-aware: a contiguous range of (tile, pass) pairs per XCD, the passes of a
 // pixel tile adjacent, so an A tile is fetched into one XCD's L2 once for all its passes.
+// Without a residual two more forms: two passes per workgroup on one resident A tile (NPW = 2,
+// once one pass per workgroup would need more than one round of the compute units) and
+// wstream128_kernel (128-pixel tiles, K <= 512, while those still cover 3/4 of the units).
 // Memory waits are explicit vmcnt counts: loads and copies complete in issue order.
 // replaces kernels/gemm.py:353-400 (fused_gemm) for these shapes
+#include <utility>
+
 #include "capi.hpp"
 #include "gemm_mfma32.hpp"
 
@@ -44,10 +49,11 @@ __host__ __device__ constexpr int ws_res_row_bytes(bool gate, int rdt) {
 }
 // A area: without a residual the whole A tile stays in LDS (NCH chunks), else the 3-stage ring
 __host__ __device__ constexpr int ws_a_bytes(int rdt, int nch) { return (rdt < 0 ? nch : WS_STAGES) * WS_STAGE; }
-__host__ __device__ constexpr int ws_lds_bytes(bool gate, int rdt, int nch) {
-  return ws_a_bytes(rdt, nch) + WS_P * ws_res_row_bytes(gate, rdt) + WS_TB_FLOATS * 4;
+// npw: W^T passes per workgroup, each with its own bias / scale table
+__host__ __device__ constexpr int ws_lds_bytes(bool gate, int rdt, int nch, int npw) {
+  return ws_a_bytes(rdt, nch) + WS_P * ws_res_row_bytes(gate, rdt) + npw * WS_TB_FLOATS * 4;
 }
-static_assert(ws_lds_bytes(false, DT_F32, 16) <= 160 * 1024 && ws_lds_bytes(false, -1, 16) <= 160 * 1024, "LDS");
+static_assert(ws_lds_bytes(false, DT_F32, 16, 1) <= 160 * 1024 && ws_lds_bytes(false, -1, 16, 2) <= 160 * 1024, "LDS");
 
 struct WsP {
   const bf16_t* a;    // [m][lda]
@@ -66,7 +72,11 @@ struct WsP {
 // run-time trip count the compiler's own wait insertion could not count the loads issued between
 // a register's load and its use across the loop edge and drained every load before each chunk's
 // first MFMA (vmcnt(0)), which undid the prefetch.
-template <bool GATE, int RDT, int NCH>
+// NPW: consecutive W^T passes per workgroup (2 only without a residual). The pixel tile's A is
+// copied into LDS once and serves both passes; the second pass's first two W^T groups are loaded
+// before the first pass's epilogue, so its stores drain under the second pass's products, and the
+// second pass needs no barrier (its A chunks are those the first pass already waited for).
+template <bool GATE, int RDT, int NCH, int NPW>
 __global__ void __launch_bounds__(WS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wstream_kernel(const WsP p) {
   constexpr int NO = GATE ? 256 : 512;                    // output channels per pass
@@ -82,6 +92,7 @@ wstream_kernel(const WsP p) {
   // wave's weight loads; larger batches held up the weight loads behind them (the wait counts
   // are in issue order).
   constexpr bool RESIDENT = RDT < 0;
+  static_assert(NPW == 1 || (NPW == 2 && RESIDENT), "two passes per workgroup only with a resident A tile");
   constexpr int ABYTES = ws_a_bytes(RDT, NCH);
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   float* tb = reinterpret_cast<float*>(lds + ABYTES + WS_P * RB);
@@ -111,9 +122,10 @@ wstream_kernel(const WsP p) {
     }
   }
   asm volatile("" ::: "memory");
-  const int pt = lin / p.npass, ps = lin - pt * p.npass;
+  const int ngrp = p.npass / NPW;  // groups of NPW passes per pixel tile
+  const int pt = lin / ngrp, ps0 = (lin - pt * ngrp) * NPW;
   const int64_t q0 = (int64_t)pt * WS_P;
-  const int64_t och = (int64_t)ps * NO;  // first output channel of the pass
+  const int64_t och0 = (int64_t)ps0 * NO;  // first output channel of the workgroup's first pass
 
   // ---- A chunk c (8 KiB): wave w copies rows 8 w .. 8 w + 7, lane l row 8 w + l / 8, slot l % 8
   const int arow = wave * 8 + (lane >> 3);
@@ -138,7 +150,7 @@ wstream_kernel(const WsP p) {
           int64_t rq = q0 + r;
           if (rq > p.m - 1) rq = p.m - 1;
           const unsigned char* src =
-              (const unsigned char*)p.res + (rq * p.ldr + och) * RSZ + (s ^ (r & 7)) * 16;
+              (const unsigned char*)p.res + (rq * p.ldr + och0) * RSZ + (s ^ (r & 7)) * 16;
           __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                            (__attribute__((address_space(3))) void*)(lds + ABYTES + (wave * CPW + i) * 1024),
                                            16, 0, 0);
@@ -147,8 +159,9 @@ wstream_kernel(const WsP p) {
     }
   };
   // ---- W^T group c (k 64 c .. 64 c + 63): 4 16-k steps x 2 blocks of this wave's 64 rows
+  // (advanced by one pass, WS_WAVES * nch * 8 KiB, between the passes of an NPW = 2 workgroup)
   const unsigned char* wsrc =
-      (const unsigned char*)p.wp + (((int64_t)ps * WS_WAVES + wave) * (nch * 4) * 2 * 64 + lane) * 16;
+      (const unsigned char*)p.wp + (((int64_t)ps0 * WS_WAVES + wave) * (nch * 4) * 2 * 64 + lane) * 16;
   bf16x8 wf[3][4][2];
   auto load_w = [&](int buf, int c) __attribute__((always_inline)) {
 #pragma unroll
@@ -166,22 +179,25 @@ wstream_kernel(const WsP p) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
 
-  // prologue: the tables (direct copies into LDS: bias of the pass's 512 W^T rows, then scale of
-  // its output channels; 1 for a missing scale, 0 for a missing bias), A chunks 0 and 1, W^T
-  // groups 0 and 1
-  {
+  // prologue: the tables of each pass (direct copies into LDS: bias of the pass's 512 W^T rows,
+  // then scale of its output channels; 1 for a missing scale, 0 for a missing bias), A chunks 0
+  // and 1, W^T groups 0 and 1
+#pragma unroll
+  for (int pi = 0; pi < NPW; ++pi) {
+    const int64_t och = och0 + pi * NO;
+    float* tp = tb + pi * WS_TB_FLOATS;
     const int64_t brow = GATE ? (wave < 4 ? och + 64 * wave : p.n + och + 64 * (wave - 4)) : och + 64 * wave;
     if (p.bias)
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.bias + brow + lane),
-                                       (__attribute__((address_space(3))) void*)(tb + 64 * wave), 4, 0, 0);
+                                       (__attribute__((address_space(3))) void*)(tp + 64 * wave), 4, 0, 0);
     else
-      tb[tid] = 0.f;
+      tp[tid] = 0.f;
     if (64 * wave < NO) {
       if (p.scale)
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.scale + och + 64 * wave + lane),
-                                         (__attribute__((address_space(3))) void*)(tb + 512 + 64 * wave), 4, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(tp + 512 + 64 * wave), 4, 0, 0);
       else
-        tb[512 + tid] = 1.f;
+        tp[512 + tid] = 1.f;
     }
   }
   asm volatile("" ::: "memory");
@@ -272,13 +288,13 @@ wstream_kernel(const WsP p) {
     asm volatile("" ::: "memory");
     chunk(buf, c, next);
   };
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) step(c % 3, c);
 
-  // ---- epilogue in the MFMA layout: block (pb, rb), lane (l32, hl): pixel pb * 32 + l32; pass
-  // channel c0 = 64 wave + 32 rb + 16 hl (gate: 32 wave + 16 hl, both blocks) .. c0 + 15
-  wait_vmcnt<0>();
-  barrier_keep_vm();  // every residual row and the tables in LDS
+  // ---- epilogue of pass pi in the MFMA layout: block (pb, rb), lane (l32, hl): pixel
+  // pb * 32 + l32; pass channel c0 = 64 wave + 32 rb + 16 hl (gate: 32 wave + 16 hl, both blocks)
+  // .. c0 + 15
+  auto epilogue = [&](const int pi) __attribute__((always_inline)) {
+  const float* tt = tb + pi * WS_TB_FLOATS;  // the pass's tables
+  const int64_t och = och0 + pi * NO;
 #pragma unroll
   for (int pb = 0; pb < 2; ++pb) {
     const int px = pb * 32 + l32;
@@ -289,9 +305,9 @@ wstream_kernel(const WsP p) {
       float v[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(tb + (GATE ? c0 : c0) + 4 * i);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(tt + c0 + 4 * i);
         if constexpr (GATE) {
-          const f32x4 b2 = *reinterpret_cast<const f32x4*>(tb + 256 + c0 + 4 * i);
+          const f32x4 b2 = *reinterpret_cast<const f32x4*>(tt + 256 + c0 + 4 * i);
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
         } else {
@@ -308,7 +324,7 @@ wstream_kernel(const WsP p) {
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const f32x4 s = *reinterpret_cast<const f32x4*>(tb + 512 + c0 + 4 * i);
+        const f32x4 s = *reinterpret_cast<const f32x4*>(tt + 512 + c0 + 4 * i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[4 * i + e] *= s[e] * p.out_scale;
       }
@@ -351,13 +367,273 @@ wstream_kernel(const WsP p) {
       }
     }
   }
+  };
+
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) step(c % 3, c);
+  if constexpr (NPW == 1) {
+    wait_vmcnt<0>();
+    barrier_keep_vm();  // every residual row and the tables in LDS
+    epilogue(0);
+  } else {
+    wsrc += (int64_t)WS_WAVES * nch * 8 * 1024;  // the second pass's W^T
+    load_w(0, 0);
+    asm volatile("" ::: "memory");
+    load_w(1, 1);
+    asm volatile("" ::: "memory");
+    wait_vmcnt<16>();   // all but those two groups: the tables came first
+    barrier_keep_vm();  // every wave's tables in LDS
+    epilogue(0);
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) chunk(c % 3, c, c + 2 < NCH);
+    epilogue(1);
+  }
   asm volatile("" ::"v"(touch[0]), "v"(touch[1]));
 }
 
-template <bool GATE, int RDT, int NCH>
+// ---- 128-pixel tiles (no residual, K = 256 / 512) ------------------------------------------------
+// With 64-pixel tiles the K loop is bound by the W^T stream from L2: each fragment feeds two MFMAs,
+// and the second pass of a two-pass workgroup (no A copies, no barriers) still ran its 512-k loop at
+// about 60 % of the MFMA rate. Here a wave keeps its 64 W^T rows' products for 128 pixels (4 x 2
+// blocks of 32 x 32, 128 accumulator registers): every fragment feeds four MFMAs and the L2 bytes
+// per product halve. W^T arrives one 16-k step (two fragments, 2 KiB per wave) at a time through a
+// ring of W2_SLOTS register slots, W2_AHEAD steps ahead of its use (9 or 10 steps ran no faster).
+// The A tile (128 pixels x K, 128 KiB at K = 512) is copied into LDS in the prologue and stays
+// there. On the NAFNet level-3 shapes (M = 14400, K = 512, 226 workgroups) the K loop runs at
+// about 83 % of the MFMA rate of the shader clock it gets under this load (s_memtime against
+// s_memrealtime: 1.75 GHz, not the 2.4 GHz peak); the A fill before it (HBM) and the stores after
+// it take the rest.
+constexpr int W2_P = 128, W2_STAGE = W2_P * 128;  // 16 KiB per 64-k chunk
+constexpr int W2_AHEAD = 7, W2_SLOTS = W2_AHEAD + 1;
+
+__host__ __device__ constexpr int w2_lds_bytes(int nch) { return nch * W2_STAGE + WS_TB_FLOATS * 4; }
+static_assert(w2_lds_bytes(8) <= 160 * 1024, "LDS");
+
+// The prologue copies the whole A tile, then loads W^T steps 0 .. W2_AHEAD - 1 (two loads each);
+// each step s then loads step s + W2_AHEAD. Loads and copies complete in issue order, so a copy
+// queued ahead of a W^T load delays that load: copying chunk c + 2 at the top of chunk c tied every
+// W^T load to an HBM round trip with less than two chunks of slack (1.8 us per 64-k chunk against
+// 0.9 us of MFMA time). With outstanding copies the compiler's own wait insertion also stops
+// counting (the copies write LDS): the first use of any register loaded before them drained the
+// counter (vmcnt(0)) whatever the explicit waits. So the tile lands before the K loop (one wait,
+// one barrier) and the loop waits on W^T loads only, with explicit counts:
+// operations a wave has issued after its loads of W^T step t when step t's products start (after
+// that step's load).
+__host__ __device__ constexpr int w2_after_w(int t, int nch) {
+  const int nt = 4 * nch, pre = W2_AHEAD < nt ? W2_AHEAD : nt;
+  int n = 0, s0 = t - W2_AHEAD + 1;   // the first step after the one that loaded step t
+  if (t < W2_AHEAD) {                 // loaded in the prologue
+    n += 2 * (pre - 1 - t);
+    s0 = 0;
+  }
+  for (int s = s0; s <= t; ++s)
+    if (s + W2_AHEAD < nt) n += 2;
+  return n;
+}
+static_assert(w2_after_w(0, 8) == 14 && w2_after_w(6, 8) == 14 && w2_after_w(7, 8) == 14 &&
+                  w2_after_w(31, 8) == 0 && w2_after_w(24, 8) == 14 && w2_after_w(13, 4) == 4,
+              "load counts");
+
+template <class F, int... I>
+__device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <bool GATE, int NCH>
+__global__ void __launch_bounds__(WS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+wstream128_kernel(const WsP p) {
+  constexpr int NO = GATE ? 256 : 512;  // output channels per pass
+  constexpr int NT = 4 * NCH;           // 16-k steps
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  float* tb = reinterpret_cast<float*>(lds + NCH * W2_STAGE);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int b = blockIdx.x;
+  const int lin = (b & 7) * p.per_xcd + (b >> 3);
+  if (lin >= p.tiles) return;  // before any LDS or memory traffic
+
+  // the packed weight into this XCD's L2 first, as in wstream_kernel
+  unsigned int touch[2];
+  {
+    typedef const __attribute__((address_space(1))) unsigned int* gptr;
+    const int64_t wbytes = (int64_t)p.npass * 512 * NCH * 64 * 2;
+    const bool on = wbytes <= ((int64_t)2 << 20);
+    const int lines = (int)(wbytes / 128), slot = b >> 3;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int l = (slot + i * p.per_xcd) * WS_THREADS + tid;
+      l = !on ? 0 : (l < lines ? l : lines - 1);
+      touch[i] = *(gptr)((const unsigned char*)p.wp + (int64_t)l * 128);
+    }
+  }
+  asm volatile("" ::: "memory");
+  const int pt = lin / p.npass, ps = lin - pt * p.npass;
+  const int64_t q0 = (int64_t)pt * W2_P;
+  const int64_t och = (int64_t)ps * NO;  // first output channel of the pass
+
+  // ---- A chunk c (16 KiB): copy j of wave w lands rows 16 w + 8 j .. + 7, lane l row
+  // 16 w + 8 j + l / 8, slot l % 8 (holding the row's unit m32_swz(row, l % 8))
+  const unsigned char* asrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int arow = wave * 16 + j * 8 + (lane >> 3);
+    int64_t aq = q0 + arow;
+    if (aq > p.m - 1) aq = p.m - 1;  // rows past M: any valid row, never stored
+    asrc[j] = (const unsigned char*)(p.a + aq * p.lda) + m32_swz(arow, lane & 7) * 16;
+  }
+  auto issue_a = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(asrc[j] + c * 128),
+                                       (__attribute__((address_space(3))) void*)(lds + c * W2_STAGE + (2 * wave + j) * 1024),
+                                       16, 0, 0);
+  };
+  // ---- W^T 16-k step t of this wave's 64 rows: 2 fragments (blocks) into ring slot t % W2_SLOTS
+  const unsigned char* wsrc =
+      (const unsigned char*)p.wp + (((int64_t)ps * WS_WAVES + wave) * NT * 2 * 64 + lane) * 16;
+  bf16x8 wf[W2_SLOTS][2];
+  auto load_w = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+      wf[t % W2_SLOTS][rb] = *reinterpret_cast<const bf16x8*>(wsrc + ((int64_t)t * 2 + rb) * 1024);
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
+
+  // prologue: the tables (bias of the pass's 512 W^T rows, then scale of its output channels; 0 /
+  // 1 when left out), the A tile, the first W2_AHEAD W^T steps
+  {
+    const int64_t brow = GATE ? (wave < 4 ? och + 64 * wave : p.n + och + 64 * (wave - 4)) : och + 64 * wave;
+    if (p.bias)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.bias + brow + lane),
+                                       (__attribute__((address_space(3))) void*)(tb + 64 * wave), 4, 0, 0);
+    else
+      tb[tid] = 0.f;
+    if (64 * wave < NO) {
+      if (p.scale)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(p.scale + och + 64 * wave + lane),
+                                         (__attribute__((address_space(3))) void*)(tb + 512 + 64 * wave), 4, 0, 0);
+      else
+        tb[512 + tid] = 1.f;
+    }
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) issue_a(c);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int t = 0; t < (W2_AHEAD < NT ? W2_AHEAD : NT); ++t) {
+    load_w(t);
+    asm volatile("" ::: "memory");  // in step order: the wait counts below assume it
+  }
+  wait_vmcnt<2 * (W2_AHEAD < NT ? W2_AHEAD : NT)>();  // the tables and this wave's copies
+  barrier_keep_vm();                                  // ... and every other wave's
+
+  // ---- K loop, unrolled over the 16-k steps (every wait count a constant)
+  unrolled([&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value;
+    if constexpr (t + W2_AHEAD < NT) load_w(t + W2_AHEAD);
+    asm volatile("" ::: "memory");
+    wait_vmcnt<w2_after_w(t, NCH)>();  // this step's W^T fragments
+    const unsigned char* st = lds + (t / 4) * W2_STAGE;
+    bf16x8 af[4];
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      const int r = pb * 32 + l32;
+      af[pb] = *reinterpret_cast<const bf16x8*>(st + r * 128 + m32_swz(r, 2 * (t % 4) + hl) * 16);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) acc[pb][rb] = mfma32_bf16(wf[t % W2_SLOTS][rb], af[pb], acc[pb][rb]);
+  }, std::make_integer_sequence<int, NT>{});
+
+  // ---- epilogue in the MFMA layout: block (pb, rb), lane (l32, hl): pixel pb * 32 + l32; pass
+  // channel c0 = 64 wave + 32 rb + 16 hl (gate: 32 wave + 16 hl, both blocks) .. c0 + 15. The
+  // tables landed before the K loop's wait and barrier.
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    const int64_t q = q0 + pb * 32 + l32;
+#pragma unroll
+    for (int rb = 0; rb < (GATE ? 1 : 2); ++rb) {
+      const int c0 = GATE ? wave * 32 + hl * 16 : wave * 64 + rb * 32 + hl * 16;
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(tb + c0 + 4 * i);
+        if constexpr (GATE) {
+          const f32x4 b2 = *reinterpret_cast<const f32x4*>(tb + 256 + c0 + 4 * i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * i + e] = (acc[pb][0][4 * i + e] + b1[e]) * (acc[pb][1][4 * i + e] + b2[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * i + e] = acc[pb][rb][4 * i + e] + b1[e];
+        }
+      }
+      if (p.act == ACT_GELU) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = gelu_erf(v[j]);
+      } else if (p.act == ACT_LRELU) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = v[j] >= 0.f ? v[j] : v[j] * p.slope;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(tb + 512 + c0 + 4 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * i + e] *= sc[e] * p.out_scale;
+      }
+      if (q < p.m) {
+        const int64_t o = q * p.ldc + och + c0;
+        if (p.c_dt == DT_BF16) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            f32x8 ov;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ov.v[i] = v[8 * h + i];
+            *reinterpret_cast<bf16x8*>((unsigned char*)p.c + (o + 8 * h) * 2) = pack_bf16(ov);
+          }
+        } else {
+          float* op = reinterpret_cast<float*>(p.c) + o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            reinterpret_cast<f32x4*>(op)[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+        }
+      }
+    }
+  }
+  asm volatile("" ::"v"(touch[0]), "v"(touch[1]));
+}
+
+template <bool GATE, int NCH>
+void launch128(const WsP& p, hipStream_t s) {
+  constexpr int lds = w2_lds_bytes(NCH);
+  auto fn = &wstream128_kernel<GATE, NCH>;
+  static const bool attr = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL(fn, dim3((unsigned)(8 * p.per_xcd)), dim3(WS_THREADS), lds, s, p);
+}
+
+template <bool GATE, int RDT, int NCH, int NPW>
 void launch(const WsP& p, hipStream_t s) {
-  constexpr int lds = ws_lds_bytes(GATE, RDT, NCH);
-  auto fn = &wstream_kernel<GATE, RDT, NCH>;
+  constexpr int lds = ws_lds_bytes(GATE, RDT, NCH, NPW);
+  auto fn = &wstream_kernel<GATE, RDT, NCH, NPW>;
   static const bool attr = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
@@ -367,10 +643,18 @@ void launch(const WsP& p, hipStream_t s) {
 }
 
 template <bool GATE, int RDT>
-void launch_k(const WsP& p, hipStream_t s) {
-  if (p.nch == 4) launch<GATE, RDT, 4>(p, s);
-  else if (p.nch == 8) launch<GATE, RDT, 8>(p, s);
-  else launch<GATE, RDT, 16>(p, s);
+void launch_k(const WsP& p, int npw, hipStream_t s) {
+  if constexpr (RDT < 0) {
+    if (npw == 2) {
+      if (p.nch == 4) launch<GATE, RDT, 4, 2>(p, s);
+      else if (p.nch == 8) launch<GATE, RDT, 8, 2>(p, s);
+      else launch<GATE, RDT, 16, 2>(p, s);
+      return;
+    }
+  }
+  if (p.nch == 4) launch<GATE, RDT, 4, 1>(p, s);
+  else if (p.nch == 8) launch<GATE, RDT, 8, 1>(p, s);
+  else launch<GATE, RDT, 16, 1>(p, s);
 }
 
 }  // namespace
@@ -403,23 +687,41 @@ extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void*
   }
   const int64_t ptiles = cdiv(a->m, WS_P), npass = nw / 512;
   CLARUS_REQUIRE(ptiles * npass < ((int64_t)1 << 30), "gemm_wp: too many tiles");
+  // two W^T passes per workgroup (no residual, an even pass count) once one pass per workgroup
+  // would take more than one round of the device's compute units: A is then read once and the
+  // second round's A fill and epilogue are gone
+  const int npw = a->res == nullptr && npass % 2 == 0 && ptiles * npass > device_cus() ? 2 : 1;
+  // 128-pixel tiles (half the L2 weight bytes per product) without a residual at K <= 512, while
+  // their (tile, pass) count still covers at least 3/4 of the compute units
+  const int64_t ptiles128 = cdiv(a->m, W2_P);
+  const bool p128 = a->res == nullptr && a->k <= 512 && 4 * ptiles128 * npass >= 3 * (int64_t)device_cus();
   WsP p{};
   p.a = (const bf16_t*)a->a; p.wp = wp; p.bias = a->bias; p.scale = a->scale; p.res = a->res; p.c = a->c;
   p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
-  p.nch = (int)(a->k / 64); p.npass = (int)npass; p.tiles = (int)(ptiles * npass);
+  p.nch = (int)(a->k / 64); p.npass = (int)npass;
+  p.tiles = (int)(p128 ? ptiles128 * npass : ptiles * npass / npw);
   p.per_xcd = (int)cdiv(p.tiles, 8);
   p.c_dt = a->c_dtype; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
   const int rdt = a->res ? a->r_dtype : -1;
-  note_kernel("wstream_kernel gate=%d res=%d k=%lld", (int)gate, rdt, (long long)a->k);
+  note_kernel("wstream_kernel gate=%d res=%d k=%lld p=%d npw=%d", (int)gate, rdt, (long long)a->k,
+              p128 ? W2_P : WS_P, p128 ? 1 : npw);
   hipStream_t s = (hipStream_t)stream;
-  if (gate) {
-    if (rdt == DT_F32) launch_k<true, DT_F32>(p, s);
-    else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, s);
-    else launch_k<true, -1>(p, s);
+  if (p128) {
+    if (gate) {
+      if (p.nch == 4) launch128<true, 4>(p, s);
+      else launch128<true, 8>(p, s);
+    } else {
+      if (p.nch == 4) launch128<false, 4>(p, s);
+      else launch128<false, 8>(p, s);
+    }
+  } else if (gate) {
+    if (rdt == DT_F32) launch_k<true, DT_F32>(p, npw, s);
+    else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, npw, s);
+    else launch_k<true, -1>(p, npw, s);
   } else {
-    if (rdt == DT_F32) launch_k<false, DT_F32>(p, s);
-    else if (rdt == DT_BF16) launch_k<false, DT_BF16>(p, s);
-    else launch_k<false, -1>(p, s);
+    if (rdt == DT_F32) launch_k<false, DT_F32>(p, npw, s);
+    else if (rdt == DT_BF16) launch_k<false, DT_BF16>(p, npw, s);
+    else launch_k<false, -1>(p, npw, s);
   }
   return check_launch("gemm_wp");
 }

@@ -250,14 +250,28 @@ def test_m32_kernel_epilogues(gate, k, tile, hip_bf16):
     (False, 256, 1024, None, torch.bfloat16, "gelu", 130),
     (False, 1024, 512, torch.float32, torch.bfloat16, None, 64),
     (True, 512, 256, torch.float32, torch.float32, None, 333),
+    # more tiles than compute units, no residual: two passes per workgroup
+    (False, 512, 1024, None, torch.bfloat16, None, 64 * 150 + 7),
+    (True, 256, 512, None, torch.float32, None, 64 * 140 + 33),
+    (False, 1024, 1024, None, torch.bfloat16, "gelu", 64 * 130 + 1),
+    (False, 512, 2048, None, torch.bfloat16, None, 64 * 70),
+    # no residual, K <= 512, (128-pixel tile, pass) pairs >= 3/4 of the compute units: 128-pixel tiles
+    (False, 512, 1024, None, torch.bfloat16, None, 128 * 100 + 5),
+    (True, 256, 512, None, torch.float32, None, 128 * 97 + 64),
+    (False, 512, 512, None, torch.bfloat16, "gelu", 128 * 200),
+    (True, 512, 512, None, torch.bfloat16, None, 90 * 160),
 ])
 def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     """Through the C ABI, clarus_hip_gemm_wp (W^T streamed from L2 into registers, packed by
-    HipOps._w2p): K = 256 / 512 / 1024, one or two 512-row passes, SimpleGate, GELU, no / bf16 /
-    fp32 residual (staged in LDS during the K loop), bf16 / fp32 output, out_scale, a ragged last
-    64-pixel tile, and bias / scale left out in one case. Held to the fp32 oracle: bf16 products
-    are exact in fp32, so an fp32 output matches to summation order and a bf16 one to its
-    rounding."""
+    HipOps._w2p): K = 256 / 512 / 1024, one, two or four 512-row passes, SimpleGate, GELU, no /
+    bf16 / fp32 residual (staged in LDS during the K loop), bf16 / fp32 output, out_scale, a ragged
+    last 64-pixel tile, and bias / scale left out in two cases. Without a residual, an even pass
+    count and more 64-pixel tiles x passes than compute units, a workgroup runs two passes on one
+    resident A tile (npw=2 in the kernel note; the K = 512, N = 2048 case has two such pairs per
+    tile); without a residual at K <= 512 with enough 128-pixel tiles (the last four cases, the
+    last the NAFNet level-3 conv4 shape) the 128-pixel kernel runs (p=128). Held to the fp32
+    oracle: bf16 products are exact in fp32, so an fp32 output matches to summation order and a
+    bf16 one to its rounding."""
     import ctypes
 
     from clarus_amd import _lib
@@ -286,6 +300,10 @@ def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     _lib.check(lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(),
                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "gemm_wp")
     assert _lib.last_kernel().startswith("wstream_kernel"), _lib.last_kernel()
+    npass, cus = nw // 512, torch.cuda.get_device_properties(0).multi_processor_count
+    p128 = rdt is None and k <= 512 and 4 * -(-m // 128) * npass >= 3 * cus
+    two = not p128 and rdt is None and npass % 2 == 0 and -(-m // 64) * npass > cus
+    assert _lib.last_kernel().endswith(f"p={128 if p128 else 64} npw={2 if two else 1}"), (_lib.last_kernel(), cus)
     what = f"gemm_wp gate={gate} K{k} N{nout} res={rdt} out={odt} act={act} M{m}"
     if odt == torch.float32:
         assert_fp32(out.cpu(), ref, rel=1e-5, what=what)
