@@ -23,7 +23,7 @@ void launch_one(GemmP& p, hipStream_t s) {
       per_cu < 1)
     per_cu = 1;
   const int64_t H = (int64_t)p.h << (UP2 ? 1 : 0), W = (int64_t)p.w << (UP2 ? 1 : 0);
-  const int64_t ptiles = (p.m / (H * W)) * cdiv(H, CH_TH) * cdiv(W, CH_TW);
+  const int64_t ptiles = (p.m / (H * W)) * cdiv(H, (int64_t)HaloGeom<UP2>::th) * cdiv(W, CH_TW);
   const int64_t ncol = cdiv(p.n, TR);
   int64_t per_col = (int64_t)device_cus() * per_cu / ncol;  // persistent: every workgroup resident
   if (per_col < 1) per_col = 1;

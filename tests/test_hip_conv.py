@@ -78,22 +78,28 @@ def test_conv3x3_up2(dt, hip_bf16, hip_f32):
     check(got.cpu(), REF.conv3x3(x, w, b, up2=True, act="lrelu"), f"conv3x3 up2 {dt}")
 
 
-@pytest.mark.parametrize("cin,cout,up2,h,w,n", [(64, 32, False, 13, 45, 2), (96, 64, False, 8, 32, 1),
-                                                 (64, 64, True, 11, 19, 2), (192, 64, False, 9, 40, 1),
-                                                 (32, 48, True, 5, 7, 1), (128, 40, False, 17, 33, 1)])
-def test_conv3x3_halo_shapes(cin, cout, up2, h, w, n, hip_bf16):
-    """bf16 convs with cin % 32 == 0 (the halo-tile kernel): ragged 8 x 32 tiles, batch 2, x2
-    upsample, output channels that are not a multiple of the 32 / 64-channel tile, LeakyReLU,
-    out_scale and a residual."""
+@pytest.mark.parametrize("cin,cout,up2,h,w,n,bias", [(64, 32, False, 13, 45, 2, True), (96, 64, False, 8, 32, 1, True),
+                                                      (64, 64, True, 11, 19, 2, True), (192, 64, False, 9, 40, 1, True),
+                                                      (32, 48, True, 5, 7, 1, True), (128, 40, False, 17, 33, 1, True),
+                                                      (64, 64, True, 19, 13, 1, False), (64, 40, False, 10, 70, 2, False)])
+def test_conv3x3_halo_shapes(cin, cout, up2, h, w, n, bias, hip_bf16):
+    """bf16 convs with cin % 32 == 0 (the halo-tile kernel): ragged 8 x 32 tiles (16 x 32 with the
+    x2 upsample), several tiles per workgroup (a tile's stores are issued during the next tile's
+    first chunk), batch 2, x2 upsample, output channels that are not a multiple of the 32 /
+    64-channel tile, LeakyReLU, out_scale, a residual, and no bias (the kernel's bias table then
+    holds zeros)."""
+    from clarus_amd import _lib
     g = gen(13)
     x = rnd(g, n, h, w, cin, dtype=torch.bfloat16)
     wt = rnd(g, cout, cin, 3, 3, scale=(cin * 9) ** -0.5, dtype=torch.bfloat16)
-    b = rnd(g, cout)
+    b = rnd(g, cout) if bias else None
     H, W = (2 * h, 2 * w) if up2 else (h, w)
     res = rnd(g, n, H, W, cout, dtype=torch.bfloat16)
-    got = hip_bf16.conv3x3(x.cuda(), wt.cuda(), b.cuda(), act="lrelu", out_scale=0.5, residual=res.cuda(), up2=up2)
+    got = hip_bf16.conv3x3(x.cuda(), wt.cuda(), None if b is None else b.cuda(), act="lrelu", out_scale=0.5,
+                           residual=res.cuda(), up2=up2)
+    assert _lib.last_kernel().startswith("conv_halo_kernel"), _lib.last_kernel()
     ref = REF.conv3x3(x, wt, b, act="lrelu", out_scale=0.5, residual=res, up2=up2, out_dtype=torch.float32)
-    check(got.cpu(), ref, f"conv3x3 halo cin{cin} cout{cout} up2={up2} {n}x{h}x{w}")
+    check(got.cpu(), ref, f"conv3x3 halo cin{cin} cout{cout} up2={up2} {n}x{h}x{w} bias={bias}")
 
 
 @pytest.mark.parametrize("tile", [12, 4])
