@@ -26,8 +26,8 @@ void launch_one(GemmP& p, hipStream_t s) {
   const int64_t ptiles = (p.m / (H * W)) * cdiv(H, (int64_t)HaloGeom<UP2>::th) * cdiv(W, CH_TW);
   const int64_t ncol = cdiv(p.n, TR);
   int64_t per_col = (int64_t)device_cus() * per_cu / ncol;  // persistent: every workgroup resident
-  if (per_col < 1) per_col = 1;
   if (per_col > ptiles) per_col = ptiles;
+  per_col = per_col < 8 ? 8 : per_col / 8 * 8;  // a multiple of 8: the kernel deals tiles per XCD
   hipLaunchKernelGGL(fn, dim3((unsigned)(per_col * ncol)), dim3(512), lds, s, p);
 }
 

@@ -95,10 +95,17 @@ __global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
   const int tiles_y = (H + TH - 1) / TH, tiles_x = (W + CH_TW - 1) / CH_TW;
   const int nimg = (int)(p.m / ((int64_t)H * W));
   const int ptiles = nimg * tiles_y * tiles_x;
+  // XCD-aware (workgroup b runs on XCD b % 8; the grid is a multiple of 8 x ncol): the column
+  // groups of a tile are adjacent workgroups of one XCD, so its halo comes into that XCD's L2 once
+  // for all of them, and XCD x walks the contiguous tiles [T x / 8, T (x + 1) / 8), so the halo
+  // rows that vertically adjacent tiles share are read there at about the same time. With the
+  // column groups on different XCDs the 192 -> 64 conv (two groups) moved 1.8x its bytes.
   const int ncol = (int)cdiv(p.n, TR);
-  const int col = blockIdx.x % ncol;
-  const int wg = blockIdx.x / ncol, nwg = gridDim.x / ncol;
-  const int ntiles = wg < ptiles ? (ptiles - wg + nwg - 1) / nwg : 0;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int col = slot % ncol;
+  const int kx = slot / ncol, per_xcd = gridDim.x / (8 * ncol);
+  const int t_lo = (int)((int64_t)ptiles * xcd / 8), t_hi = (int)((int64_t)ptiles * (xcd + 1) / 8);
+  const int ntiles = kx < t_hi - t_lo ? (t_hi - t_lo - kx + per_xcd - 1) / per_xcd : 0;
   const int nch = cin / CH_KC;
   const int nsteps = ntiles * nch;
   const unsigned char* X = (const unsigned char*)p.a;
@@ -142,7 +149,7 @@ __global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
   const unsigned char* hsrc[COPIES];
   int is_tile = 0, is_chunk = 0, is_stage = 0;
   auto set_issue_tile = [&]() __attribute__((always_inline)) {
-    const int t = wg + is_tile * nwg;
+    const int t = t_lo + kx + is_tile * per_xcd;
     const int img = t / (tiles_y * tiles_x);
     const int rem = t - img * tiles_y * tiles_x;
     const int ty = rem / tiles_x, tx = rem - (rem / tiles_x) * tiles_x;
@@ -191,7 +198,7 @@ __global__ void __launch_bounds__(512) conv_halo_kernel(const GemmP p) {
   const bool full_n = run0 + RUN <= p.n;
   float pend[RW][2][RUN];
   auto flush = [&](int tl) __attribute__((always_inline)) {
-    const int t = wg + tl * nwg;
+    const int t = t_lo + kx + tl * per_xcd;
     const int img = t / (tiles_y * tiles_x);
     const int rem = t - img * tiles_y * tiles_x;
     const int ty = rem / tiles_x, tx = rem - (rem / tiles_x) * tiles_x;
