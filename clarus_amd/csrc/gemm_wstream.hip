@@ -66,6 +66,7 @@ struct WsP {
   int nch, npass, tiles, per_xcd;
   int c_dt, act;
   float out_scale, slope;
+  float eps;  // LayerNorm / RMS prologue (wstream128_kernel)
 };
 
 // RDT: residual dtype (-1: none); NCH: 64-k chunks (K / 64). The K loop is unrolled: with a
@@ -446,7 +447,24 @@ __device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, I...>
   (f(std::integral_constant<int, I>{}), ...);
 }
 
-template <bool GATE, int NCH>
+// sum over the G lanes of a row group, butterfly in the order 1, 2, .. G / 2 (clarus_hip_rows_
+// prologue's order, so the statistics below are bitwise those of that pass)
+template <int G>
+__device__ __forceinline__ float ws_group_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// PRO: PRO_NONE, or PRO_LN / PRO_RMS applied to whole rows (K <= 512) before the K loop: each row
+// is normalised by one group of K / 8 lanes, lane g holding its k = 8 g .. 8 g + 7 as
+// clarus_hip_rows_prologue does (two-pass statistics, the same butterfly, eps inside the square
+// root) and rounded once to bf16, so the product sees the operand that pass would have written,
+// bit for bit, without the pass's HBM round trip. ADT: the A rows' dtype: bf16 rows are copied
+// into the LDS tile and normalised there; fp32 rows (the NAFNet trunk; 256 KiB a tile, more than
+// LDS) are loaded into registers (all of a wave's rows at once, after the first W^T loads),
+// normalised there and written to the tile as bf16.
+template <bool GATE, int NCH, int PRO, int ADT>
 __global__ void __launch_bounds__(WS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wstream128_kernel(const WsP p) {
   constexpr int NO = GATE ? 256 : 512;  // output channels per pass
@@ -505,13 +523,6 @@ wstream128_kernel(const WsP p) {
       wf[t % W2_SLOTS][rb] = *reinterpret_cast<const bf16x8*>(wsrc + ((int64_t)t * 2 + rb) * 1024);
   };
 
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
 
   // prologue: the tables (bias of the pass's 512 W^T rows, then scale of its output channels; 0 /
   // 1 when left out), the A tile, the first W2_AHEAD W^T steps
@@ -531,16 +542,87 @@ wstream128_kernel(const WsP p) {
     }
   }
   asm volatile("" ::: "memory");
+  constexpr bool REG_ROWS = PRO != PRO_NONE && ADT == DT_F32;  // fp32 rows through registers
+  if constexpr (!REG_ROWS) {
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) issue_a(c);
-  asm volatile("" ::: "memory");
+    for (int c = 0; c < NCH; ++c) issue_a(c);
+    asm volatile("" ::: "memory");
+  }
 #pragma unroll
   for (int t = 0; t < (W2_AHEAD < NT ? W2_AHEAD : NT); ++t) {
     load_w(t);
     asm volatile("" ::: "memory");  // in step order: the wait counts below assume it
   }
+  // ---- prologue geometry: a row is normalised by G = K / 8 lanes (RPW rows per wave at a time);
+  // lane gl holds k = 8 gl .. 8 gl + 7, LDS unit un of chunk ch of the row
+  constexpr int G = NCH * 8;
+  constexpr int RPW = 64 / G;
+  constexpr int NIT = W2_P / (WS_WAVES * RPW);  // rows per lane group of a wave
+  const int sub = lane / G, gl = lane - sub * G;
+  const int ch = gl >> 3, un = gl & 7;
+  const float invk = 1.0f / (float)(NCH * 64);
+  auto normalise = [&](f32x8& x) __attribute__((always_inline)) {
+    float mean = 0.f;
+    if constexpr (PRO == PRO_LN) {
+      float sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm += x.v[i];
+      mean = ws_group_sum<G>(sm) * invk;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float d = x.v[i] - mean;
+      ss += d * d;
+    }
+    const float rstd = rsqrtf(ws_group_sum<G>(ss) * invk + p.eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.v[i] = (x.v[i] - mean) * rstd;
+  };
+  if constexpr (REG_ROWS) {
+    // this wave's rows (wave RPW + 8 RPW it + sub), all loads in flight at once; rows past M
+    // take row M - 1 (never stored)
+    f32x8 xa[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int r = wave * RPW + it * WS_WAVES * RPW + sub;
+      int64_t aq = q0 + r;
+      if (aq > p.m - 1) aq = p.m - 1;
+      xa[it] = load8<DT_F32>(reinterpret_cast<const float*>(p.a) + aq * p.lda + 8 * gl);
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int r = wave * RPW + it * WS_WAVES * RPW + sub;
+      normalise(xa[it]);
+      *reinterpret_cast<bf16x8*>(lds + ch * W2_STAGE + r * 128 + m32_swz(r, un) * 16) = pack_bf16(xa[it]);
+    }
+  }
   wait_vmcnt<2 * (W2_AHEAD < NT ? W2_AHEAD : NT)>();  // the tables and this wave's copies
-  barrier_keep_vm();                                  // ... and every other wave's
+  barrier_keep_vm();                                  // ... and every other wave's (or rows)
+  if constexpr (PRO != PRO_NONE && !REG_ROWS) {
+    for (int r0 = wave * RPW; r0 < W2_P; r0 += WS_WAVES * RPW) {
+      const int r = r0 + sub;
+      unsigned char* up = lds + ch * W2_STAGE + r * 128 + m32_swz(r, un) * 16;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+      f32x8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x.v[2 * e] = __uint_as_float(raw[e] << 16);
+        x.v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u);
+      }
+      normalise(x);
+      *reinterpret_cast<bf16x8*>(up) = pack_bf16(x);
+    }
+    barrier_keep_vm();  // every row normalised
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[x][y][j] = 0.f;
 
   // ---- K loop, unrolled over the 16-k steps (every wait count a constant)
   unrolled([&](auto tc) __attribute__((always_inline)) {
@@ -618,16 +700,27 @@ wstream128_kernel(const WsP p) {
   asm volatile("" ::"v"(touch[0]), "v"(touch[1]));
 }
 
-template <bool GATE, int NCH>
+template <bool GATE, int NCH, int PRO, int ADT>
 void launch128(const WsP& p, hipStream_t s) {
   constexpr int lds = w2_lds_bytes(NCH);
-  auto fn = &wstream128_kernel<GATE, NCH>;
+  auto fn = &wstream128_kernel<GATE, NCH, PRO, ADT>;
   static const bool attr = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
   }();
   (void)attr;
   hipLaunchKernelGGL(fn, dim3((unsigned)(8 * p.per_xcd)), dim3(WS_THREADS), lds, s, p);
+}
+
+template <int PRO, int ADT>
+void launch128_g(const WsP& p, bool gate, hipStream_t s) {
+  if (gate) {
+    if (p.nch == 4) launch128<true, 4, PRO, ADT>(p, s);
+    else launch128<true, 8, PRO, ADT>(p, s);
+  } else {
+    if (p.nch == 4) launch128<false, 4, PRO, ADT>(p, s);
+    else launch128<false, 8, PRO, ADT>(p, s);
+  }
 }
 
 template <bool GATE, int RDT, int NCH, int NPW>
@@ -666,19 +759,26 @@ using namespace clarus;
 extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void* stream) {
   clear_error();
   CLARUS_REQUIRE(a != nullptr && a->a && wp && a->c, "gemm_wp: null operand");
+  const int pro = a->pro;
   const bool gate = a->gate != 0;
   const int64_t nw = gate ? 2 * a->n : a->n;
   CLARUS_REQUIRE(a->m > 0 && a->n > 0 && nw % 512 == 0 && (a->k == 256 || a->k == 512 || a->k == 1024),
                  "gemm_wp: W^T rows a multiple of 512, K = 256, 512 or 1024 (N=%lld K=%lld gate=%d)",
                  (long long)a->n, (long long)a->k, (int)gate);
-  CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16 && (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
-                 "gemm_wp: bf16 A and W, bf16 / fp32 output");
+  CLARUS_REQUIRE((a->a_dtype == DT_BF16 || (a->a_dtype == DT_F32 && pro != PRO_NONE)) && a->w_dtype == DT_BF16 &&
+                     (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
+                 "gemm_wp: bf16 A (fp32 with a prologue) and W, bf16 / fp32 output");
   CLARUS_REQUIRE(a->res == nullptr || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_wp: bf16 / fp32 residual");
-  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
+  // a LayerNorm / RMS prologue (no residual, K <= 512) runs inside the 128-pixel kernel, on the
+  // whole rows its A tile holds
+  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr && a->k <= 512),
+                 "gemm_wp: no prologue, or LayerNorm / RMS without a residual at K <= 512 (pro=%d)", pro);
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 &&
                      (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
-                 "gemm_wp: plain rows (no prologue, batch or pixel shuffle)");
+                 "gemm_wp: plain rows (no batch or pixel shuffle)");
   const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
-  CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
+  const int ea = a->a_dtype == DT_F32 ? 4 : 2;
+  CLARUS_REQUIRE(a->lda >= a->k && (a->lda * ea) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
                  "gemm_wp: 16-byte A rows and packed weight");
   CLARUS_REQUIRE(a->ldc >= a->n && (a->ldc * ec) % 16 == 0 && aligned(a->c, 16), "gemm_wp: 16-byte output rows");
   if (a->res) {
@@ -694,26 +794,24 @@ extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void*
   // 128-pixel tiles (half the L2 weight bytes per product) without a residual at K <= 512, while
   // their (tile, pass) count still covers at least 3/4 of the compute units
   const int64_t ptiles128 = cdiv(a->m, W2_P);
-  const bool p128 = a->res == nullptr && a->k <= 512 && 4 * ptiles128 * npass >= 3 * (int64_t)device_cus();
+  const bool p128 = a->res == nullptr && a->k <= 512 &&
+                    (pro != PRO_NONE || 4 * ptiles128 * npass >= 3 * (int64_t)device_cus());
   WsP p{};
   p.a = (const bf16_t*)a->a; p.wp = wp; p.bias = a->bias; p.scale = a->scale; p.res = a->res; p.c = a->c;
   p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
   p.nch = (int)(a->k / 64); p.npass = (int)npass;
   p.tiles = (int)(p128 ? ptiles128 * npass : ptiles * npass / npw);
   p.per_xcd = (int)cdiv(p.tiles, 8);
-  p.c_dt = a->c_dtype; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
+  p.c_dt = a->c_dtype; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope; p.eps = a->ln_eps;
   const int rdt = a->res ? a->r_dtype : -1;
-  note_kernel("wstream_kernel gate=%d res=%d k=%lld p=%d npw=%d", (int)gate, rdt, (long long)a->k,
+  note_kernel("wstream_kernel gate=%d res=%d pro=%d k=%lld p=%d npw=%d", (int)gate, rdt, pro, (long long)a->k,
               p128 ? W2_P : WS_P, p128 ? 1 : npw);
   hipStream_t s = (hipStream_t)stream;
   if (p128) {
-    if (gate) {
-      if (p.nch == 4) launch128<true, 4>(p, s);
-      else launch128<true, 8>(p, s);
-    } else {
-      if (p.nch == 4) launch128<false, 4>(p, s);
-      else launch128<false, 8>(p, s);
-    }
+    const bool f32 = a->a_dtype == DT_F32;
+    if (pro == PRO_LN) f32 ? launch128_g<PRO_LN, DT_F32>(p, gate, s) : launch128_g<PRO_LN, DT_BF16>(p, gate, s);
+    else if (pro == PRO_RMS) f32 ? launch128_g<PRO_RMS, DT_F32>(p, gate, s) : launch128_g<PRO_RMS, DT_BF16>(p, gate, s);
+    else launch128_g<PRO_NONE, DT_BF16>(p, gate, s);
   } else if (gate) {
     if (rdt == DT_F32) launch_k<true, DT_F32>(p, npw, s);
     else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, npw, s);

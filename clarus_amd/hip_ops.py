@@ -91,6 +91,12 @@ class HipOps(Backend):
     wstream_min_k = 256
     wstream_min_tiles = 200  # (64-pixel tile, 512-row pass) workgroups: fewer leave CUs idle
     wstream_gate_only = False
+    # LayerNorm / RMS linear without a residual at K = 256 / 512 (bf16 or fp32 rows, bf16
+    # weights): the prologue inside clarus_hip_gemm_wp's 128-pixel kernel on whole rows (the
+    # separate pass's operand bit for bit, without its round trip through HBM), while that
+    # kernel's (tile, pass) count covers 3/4 of the compute units; False, or fewer tiles, keep the
+    # separate pass. Reference-block NAFNet-w64 forward: level 3 conv1 and conv4.
+    wstream_prologue = True
     # Plain bf16 GEMMs with K in wres_ks on clarus_hip_gemm_wr (persistent workgroups, each keeping
     # its 512-row W^T pass in registers for all of its pixel tiles, the next A tile copied during the
     # current one); False or other K keep them on the kernels above.
@@ -132,6 +138,7 @@ class HipOps(Backend):
         except (OSError, RuntimeError) as exc:
             raise BackendUnavailable(f"libclarus_hip.so: {exc}") from exc
         self.dev = dev
+        self._cus = None  # compute units of dev, looked up on first use
         # launches of the fused pair kernel (clarus_hip_gemm_ln_gemm) and of the LN-rows GEMM
         # (clarus_hip_gemm_ln_rows) made by linear_ln_linear; counters only, never read by the dispatch
         self.pair_launches = {"gemm_ln_gemm": 0, "gemm_ln_rows": 0}
@@ -190,7 +197,7 @@ class HipOps(Backend):
               ln_eps=1e-6, out_scale=1.0, tile=0, wp=None):
         h, w, oh, ow, pt, pl = geom
         stats = None
-        if (pro & 0xff) in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1:
+        if (pro & 0xff) in (_lib.PRO_LN, _lib.PRO_RMS, _lib.PRO_LNMUL) and k > 128 and batch == 1 and wp is None:
             stats = torch.empty(2 * m, device=a.device, dtype=torch.float32)  # row statistics scratch
         args = _lib.GemmArgs(
             a=a.data_ptr(), wt=wt.data_ptr(), c=c.data_ptr(), bias=_lib.ptr(bias), scale=_lib.ptr(scale),
@@ -231,6 +238,21 @@ class HipOps(Backend):
                 and k >= self.wstream_min_k and k in (256, 512, 1024) and nw % 512 == 0
                 and act in (0, _lib.ACT_GELU) and (gate or not self.wstream_gate_only)
                 and -(-m // 64) * (nw // 512) >= self.wstream_min_tiles):
+            return None
+        return "wp", self._w2p(w, bool(gate))
+
+    def _wp_prologue(self, x, w, pro, k, nout, gate, act, m, res):
+        """("wp", W^T packed) when this LayerNorm / RMS linear runs with its prologue inside
+        clarus_hip_gemm_wp (see wstream_prologue), else None."""
+        nw = (2 if gate else 1) * nout
+        if not (self.wstream and self.wstream_prologue and not self.prologue_split and res is None
+                and pro in (_lib.PRO_LN, _lib.PRO_RMS) and k in (256, 512) and nw % 512 == 0
+                and x.dtype in (torch.bfloat16, torch.float32) and w.dtype == torch.bfloat16
+                and act in (0, _lib.ACT_GELU)):
+            return None
+        if self._cus is None:
+            self._cus = torch.cuda.get_device_properties(self.dev).multi_processor_count
+        if 4 * -(-m // 128) * (nw // 512) < 3 * self._cus:
             return None
         return "wp", self._w2p(w, bool(gate))
 
@@ -297,6 +319,10 @@ class HipOps(Backend):
                    act=_lib.ACT_GELU if act == "gelu" else 0)
         m = n * h * wd
         if self._prologue_pass(w, pro, k):
+            wpp = self._wp_prologue(x, w, pro, k, nout, gate, epi["act"], m, residual)
+            if wpp is not None:
+                return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
+                                  ln_eps=float(ln_eps), wp=wpp, **epi)
             # the separate prologue pass of triton_cuda.py:104-110 (ln_rows / mul_small), then a
             # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K)
             rows = self._prologue_rows(x, pro, sm, geom, ln_eps, m, k)

@@ -311,6 +311,86 @@ def test_gemm_wp_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
         check(out.cpu(), ref, what)
 
 
+@pytest.mark.parametrize("gate,k,nout,pro,xdt,odt,act,m", [
+    (False, 512, 1024, "ln", torch.float32, torch.bfloat16, None, 90 * 160),  # NAFNet level-3 conv1
+    (True, 512, 512, "ln", torch.float32, torch.bfloat16, None, 90 * 160),    # ... conv4 (SimpleGate)
+    (False, 256, 512, "rms", torch.bfloat16, torch.float32, None, 128 * 30 + 7),
+    (True, 256, 256, "ln", torch.bfloat16, torch.bfloat16, "gelu", 1000),
+    (False, 512, 512, "rms", torch.float32, torch.float32, "gelu", 333),
+])
+def test_gemm_wp_prologue(gate, k, nout, pro, xdt, odt, act, m, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wp with a LayerNorm / RMS prologue (128-pixel kernel: bf16
+    rows normalised in the LDS tile, fp32 rows through registers): bit for bit the separate pass
+    (clarus_hip_rows_prologue, rows rounded once to bf16) followed by clarus_hip_gemm_wp on its
+    rows, whichever tile form that plain call takes (the same k-step order per output); and, for
+    fp32 outputs, the prologue rule of check_prologue against the fp32 oracle. Rows offset from
+    zero (x ~ 3 + N(0, 1)), ragged last tiles, bias and scale."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(61 + k + m)
+    nw = 2 * nout if gate else nout
+    x = (3 + rnd(g, m, k)).to(xdt)
+    w = rnd(g, k, nw, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc = rnd(g, nw), rnd(g, nout)
+    xd, wd, bd, sd = dev(x, w, b, sc)
+    wp = hip_bf16._w2p(wd, gate)
+    code = _lib.PRO_LN if pro == "ln" else _lib.PRO_RMS
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def gemm_wp(a, adt, p, out):
+        args = _lib.GemmArgs(a=a.data_ptr(), wt=0, c=out.data_ptr(), bias=bd.data_ptr(), scale=sd.data_ptr(),
+                             m=m, n=nout, k=k, batch=1, lda=k, ldc=nout, a_dtype=adt, w_dtype=_lib.BF16,
+                             c_dtype=_lib.dtype_code(odt), gate=int(gate), pro=p, ln_eps=1e-6,
+                             act=_lib.ACT_GELU if act == "gelu" else 0, out_scale=1.0)
+        _lib.check(lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(), st), "gemm_wp")
+        return _lib.last_kernel()
+
+    fused = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern = gemm_wp(xd, _lib.dtype_code(xdt), code, fused)
+    assert kern.startswith(f"wstream_kernel gate={int(gate)} res=-1 pro={code} k={k} p=128"), kern
+    rows = torch.empty(m, k, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.dtype_code(xdt), pro=code,
+                         ln_eps=1e-6)
+    _lib.check(lib.clarus_hip_rows_prologue(ctypes.byref(args), rows.data_ptr(), st), "rows_prologue")
+    two = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern2 = gemm_wp(rows, _lib.BF16, _lib.PRO_NONE, two)
+    assert torch.equal(fused, two), (f"{kern} vs {kern2}: max|d| "
+                                     f"{(fused.float() - two.float()).abs().max().item():.3e}")
+    if odt == torch.float32:
+        check_prologue(fused.cpu(), k, f"gemm_wp pro={pro} gate={gate} K{k} M{m}", x, w, b,
+                       ln=True if pro == "ln" else "rms", rounded=True, gate=gate, scale=sc,
+                       act=act)
+
+
+def test_linear_ln_routes_to_wstream_prologue(hip_bf16):
+    """HipOps.linear with LayerNorm at the NAFNet level-3 shapes (fp32 trunk rows, 90 x 160 x 512,
+    conv1 to 1024 channels and conv4 with SimpleGate) runs the prologue inside the 128-pixel
+    weight-streaming kernel, bit-identical to the separate pass and GEMM (wstream_prologue
+    False)."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(71)
+    x = (1 + rnd(g, 1, 90, 160, 512)).cuda()
+    for gate, nout in ((False, 1024), (True, 512)):
+        w = rnd(g, 512, 2 * nout if gate else nout, scale=512 ** -0.5, dtype=torch.bfloat16).cuda()
+        b = rnd(g, 2 * nout if gate else nout).cuda()
+        saved = HipOps.wstream_prologue
+        try:
+            HipOps.wstream_prologue = True
+            y1 = hip_bf16.linear(x, w, b, ln=True, gate=gate)
+            k1 = _lib.last_kernel()
+            HipOps.wstream_prologue = False
+            y0 = hip_bf16.linear(x, w, b, ln=True, gate=gate)
+            k0 = _lib.last_kernel()
+        finally:
+            HipOps.wstream_prologue = saved
+        assert "pro=1 k=512 p=128" in k1, k1
+        assert "pro=0" in k0, k0
+        assert torch.equal(y1, y0), f"gate={gate}: max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("gate,k,nout,rdt,odt,act,m", [
     (True, 256, 256, None, torch.bfloat16, None, 64 * 9 + 1),
     (True, 128, 128, None, torch.bfloat16, None, 1000),
