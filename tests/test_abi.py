@@ -86,10 +86,13 @@ def test_validation_rejects_before_launch(lib):
     a.k, a.lda, a.n, a.ldc = 512, 512, 256, 256
     assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # 256 W^T rows
     a.gate = 1
-    a.pro = _lib.PRO_LN
-    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # a prologue
-    assert b"plain rows" in lib.clarus_hip_last_error()
-    a.pro, a.a_dtype = 0, _lib.F32
+    a.pro = _lib.PRO_MUL
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # a prologue other than LN / RMS
+    assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
+    a.pro, a.res, a.r_dtype, a.ldr = _lib.PRO_LN, 16, _lib.F32, 256
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # LN with a residual
+    assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
+    a.pro, a.res, a.a_dtype = 0, 0, _lib.F32
     assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 A
     assert b"bf16 A" in lib.clarus_hip_last_error()
     a = _lib.GemmArgs(a=16, c=16, m=64, n=256, k=512, batch=1, lda=512, ldc=256, a_dtype=_lib.BF16,
