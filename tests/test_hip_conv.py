@@ -205,8 +205,9 @@ def test_config5_upconv(h, w, hip_bf16):
                                           (False, "gelu", 1), (False, None, 2)])
 def test_dwconv(dt, gate, act, dil, c, hip_bf16, hip_f32):
     """Depthwise 3x3 + SimpleGate / GELU gate / GELU / dilation 2 (tools/test_kernels.py:110-121,
-    193-199), odd sizes (two images of 37 x 53); 96 channels take the sliding-window kernel
-    (dilation 1), 528 and 640 the per-pixel one."""
+    193-199), odd sizes (two images of 37 x 53, partial tiles at both edges): bf16 with a gate
+    takes the LDS-tiled kernel; otherwise 96 channels take the sliding-window kernel (dilation
+    1), 528 and 640 the per-pixel one."""
     hip = hip_bf16 if dt == torch.bfloat16 else hip_f32
     g = gen(8)
     x, w, b = rnd(g, 2, 37, 53, c, dtype=dt), rnd(g, c, 1, 3, 3), rnd(g, c)
@@ -218,12 +219,29 @@ def test_dwconv(dt, gate, act, dil, c, hip_bf16, hip_f32):
 @pytest.mark.parametrize("h,w,c", [(90, 160, 1024), (45, 80, 2048), (180, 320, 512)])
 def test_dwconv_nafnet_wide_levels(h, w, c, hip_bf16):
     """NAFNet-w64 720p levels 3, 4 and 2 (dwconv of conv1's 2c channels -> SimpleGate -> c) on the
-    per-pixel kernel."""
+    LDS-tiled kernel."""
     from clarus_amd import _lib
     g = gen(11)
     x, wt, b = rnd(g, 1, h, w, c, dtype=torch.bfloat16), rnd(g, c, 1, 3, 3), rnd(g, c)
     got = hip_bf16.dwconv(x.cuda(), wt.cuda(), b.cuda(), gate=True)
+    assert _lib.last_kernel().startswith("dw_tile_kernel gate=1"), _lib.last_kernel()
     check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=True), f"dwconv {h}x{w}x{c} gate")
+
+
+@pytest.mark.parametrize("n,h,w,c", [(1, 1, 1, 16), (1, 5, 3, 96), (3, 7, 17, 128), (1, 13, 33, 2064)])
+@pytest.mark.parametrize("gate", [True, "gelu"])
+def test_dwconv_tile_edges(n, h, w, c, gate, hip_bf16):
+    """The LDS-tiled kernel (bf16 input with a gate) at its edges: a single pixel, images smaller
+    than one 6 x 16 tile, three images whose tiles end inside the image in both directions, and
+    a channel slice that is partly past the outputs (1032 = 16 x 64 + 8 output channels); no
+    bias in the GELU-gate cases."""
+    from clarus_amd import _lib
+    g = gen(13)
+    x, wt = rnd(g, n, h, w, c, dtype=torch.bfloat16), rnd(g, c, 1, 3, 3)
+    b = None if gate == "gelu" else rnd(g, c)
+    got = hip_bf16.dwconv(x.cuda(), wt.cuda(), None if b is None else b.cuda(), gate=gate)
+    assert _lib.last_kernel().startswith("dw_tile_kernel"), _lib.last_kernel()
+    check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=gate), f"dwconv {n}x{h}x{w}x{c} gate={gate}")
 
 
 def test_dwconv_bf16_in_fp32_out(hip_bf16):
