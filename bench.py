@@ -378,6 +378,7 @@ def main() -> None:
                                      + wl.config4_cases(hip, hip32, dev) + wl.config5_cases(hip, dev)
                                      + [wl.fftformer_dffn_case(hip, dev), wl.nafnet_pair_case(hip, dev),
                                         wl.nafnet_ffn_case(hip, dev), wl.nafnet_lndw_case(hip, dev),
+                                        wl.nafnet_dw_case(hip, dev, 3), wl.nafnet_dw_case(hip, dev, 0),
                                         wl.evssm_scan_case(hip, dev), wl.metrics_case(dev)])
     if args.pmc_pass:  # the last dispatches: two markers, the copy, then a marker before each op and one after
         cases = wl.all_cases(hip, hip32, dev)

@@ -330,6 +330,29 @@ def nafnet_lndw_case(hip, device, seed: int = 0) -> OpCase:
                   lambda r_: run(r_, host))
 
 
+def nafnet_dw_case(hip, device, level: int, seed: int = 0) -> OpCase:
+    """The NAFNet-w64 720p depthwise 3x3 + SimpleGate of one block (dwconv on conv1's 2c channels
+    -> c, bf16, bias; the reference block's and the fused ops' call alike): level 3 (90 x 160,
+    c = 512, 31 calls per forward) or level 0 (720 x 1280, c = 64, 2 calls without the fused first
+    half). M pixels: F = 2 M 2c 9 (taps) + M c (gate); B = 2 M 2c (in) + 2 M c (out) + 4 (9 + 1) 2c
+    (taps, bias)."""
+    g = _gen(seed + 13 + level)
+    h, w, c = {3: (90, 160, 512), 0: (720, 1280, 64)}[level]
+    m = h * w
+    x = torch.randn(1, h, w, 2 * c, generator=g).bfloat16()
+    dw = (torch.rand(2 * c, 1, 3, 3, generator=g) * 2 - 1) / 3.0
+    dwb = torch.rand(2 * c, generator=g) * 0.2 - 0.1
+    host = dict(x=x, dw=dw, dwb=dwb)
+    d = {n: t.to(device) for n, t in host.items()}
+
+    def run(r_=None, d=d):
+        return (r_ or hip).dwconv(d["x"], d["dw"], d["dwb"], gate=True)
+    flops = 2.0 * m * 2 * c * 9 + m * c
+    nbytes = 2.0 * m * 2 * c + 2.0 * m * c + 4.0 * 10 * 2 * c
+    return OpCase(f"nafnet L{level} dwconv 3x3 + SimpleGate {h}x{w} c{2 * c}->{c}", 0, "bf16", flops, nbytes, run,
+                  host, lambda r_: run(r_, host))
+
+
 def fftformer_dffn_case(hip, device, seed: int = 0) -> OpCase:
     """FFTformer level-0 DFFN project_in + frequency filter at 720p as one op (linear_patch_filter:
     LayerNorm eps 1e-5 -> 1x1 conv 48 -> 288 + bias -> per-patch rfft2 * filter -> irfft2, bf16),
@@ -405,12 +428,14 @@ def metrics_case(device, seed: int = 0) -> OpCase:
 
 def all_cases(hip_bf16, hip32, device, seed: int = 0) -> list[OpCase]:
     """Every benchmark op, in the order of bench.py's rows: the config-2 step, configs 1, 3, 4, 5,
-    the fused FFTformer DFFN op, the fused NAFNet pair, feed-forward half and first half, EVSSM's
-    scan and the metrics."""
+    the fused FFTformer DFFN op, the fused NAFNet pair, feed-forward half and first half, the NAFNet
+    depthwise conv at levels 3 and 0, EVSSM's scan and the metrics."""
     return (config2_cases(hip_bf16, device, seed) + config1_cases(hip32, device, seed)
             + config3_cases(hip32, device, seed) + config4_cases(hip_bf16, hip32, device, seed)
             + config5_cases(hip_bf16, device, seed) + [fftformer_dffn_case(hip_bf16, device, seed),
                                                         nafnet_pair_case(hip_bf16, device, seed),
                                                         nafnet_ffn_case(hip_bf16, device, seed),
                                                         nafnet_lndw_case(hip_bf16, device, seed),
+                                                        nafnet_dw_case(hip_bf16, device, 3, seed),
+                                                        nafnet_dw_case(hip_bf16, device, 0, seed),
                                                         evssm_scan_case(hip_bf16, device, seed), metrics_case(device, seed)])

@@ -228,6 +228,18 @@ def test_dwconv_nafnet_wide_levels(h, w, c, hip_bf16):
     check(got.cpu(), TorchRef(torch.float32, "cpu").dwconv(x, wt, b, gate=True), f"dwconv {h}x{w}x{c} gate")
 
 
+@pytest.mark.parametrize("level", [3, 0])
+def test_dwconv_bench_rows(level, hip_bf16):
+    """The bench's NAFNet depthwise rows as timed (workloads.nafnet_dw_case: 90 x 160 x 1024 and
+    720 x 1280 x 128, SimpleGate, bias) against the oracle."""
+    from clarus_amd import _lib, workloads as wl
+    case = wl.nafnet_dw_case(hip_bf16, torch.device("cuda"), level)
+    got = case.run()
+    assert _lib.last_kernel().startswith("dw_tile_kernel gate=1"), _lib.last_kernel()
+    ref = case.cpu_run(TorchRef(torch.float32, "cpu"))
+    check(got.cpu(), ref, case.name)
+
+
 @pytest.mark.parametrize("n,h,w,c", [(1, 1, 1, 16), (1, 5, 3, 96), (3, 7, 17, 128), (1, 13, 33, 2064)])
 @pytest.mark.parametrize("gate", [True, "gelu"])
 def test_dwconv_tile_edges(n, h, w, c, gate, hip_bf16):
