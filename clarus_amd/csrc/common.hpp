@@ -82,6 +82,16 @@ __device__ __forceinline__ void store1(void* p, int dt, int64_t i, float v) {
     reinterpret_cast<float*>(p)[i] = v;
 }
 
+// sum over the G consecutive lanes of a group (G a power of two <= 64), xor butterfly 1 .. G / 2:
+// the reduction order of the row prologues (clarus_hip_rows_prologue and the GEMMs that apply it
+// to whole rows in LDS or registers), so their statistics agree bit for bit
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 // pack 8 fp32 into 8 bf16 (RNE)
 __device__ __forceinline__ bf16x8 pack_bf16(const f32x8& a) {
   bf16x8 r;

@@ -62,13 +62,14 @@ struct WrP {
   void* c;            // [m][ldc]
   int64_t m, n, lda, ldr, ldc;
   int npass, ptiles, act;
-  float out_scale, slope;
+  float out_scale, slope, eps;
 };
 
 // GATE: SimpleGate pairs (256 output channels per pass); RDT: residual dtype (-1 none); CDT:
 // output dtype; K: 128 or 256; RC: residual channels staged per row (256, or 512 without the gate);
-// HALF: one pass of at most 256 real W^T rows, its pixels split over wave pairs
-template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF>
+// HALF: one pass of at most 256 real W^T rows, its pixels split over wave pairs; PRO: PRO_NONE, or
+// PRO_LN / PRO_RMS applied to the A tile's rows in LDS before its products (no residual)
+template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF, int PRO>
 __global__ void __launch_bounds__(WR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wres_kernel(const WrP p) {
   constexpr int KS = K / 16;                 // 16-k steps
@@ -84,6 +85,7 @@ wres_kernel(const WrP p) {
   constexpr int NS = NPB * (GATE ? 1 : 2) * (16 * OES / 16);  // 16-byte stores per lane per tile
   static_assert(RDT < 0 || (WR_P * RB) % (1024 * WR_WAVES) == 0, "residual copies per wave");
   static_assert(RDT < 0 || RC >= NO || !GATE, "the gate stages all 256 channels");
+  static_assert(PRO == PRO_NONE || RDT < 0, "a row prologue only without a residual");
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int NBUF = wr_nbuf(RDT);
   unsigned char* rbuf = lds + NBUF * ABYTES;
@@ -159,6 +161,46 @@ wres_kernel(const WrP p) {
     tb[c] = (p.bias && ch < p.n) ? p.bias[brow] : 0.f;
     if (c < NO) tb[512 + c] = ((p.scale && och + c < p.n) ? p.scale[och + c] : 1.f) * p.out_scale;
   }
+  // ---- LayerNorm / RMS of the rows of the A tile in buffer bf, in place, in clarus_hip_rows_
+  // prologue's order: a row is normalised by G = K / 8 consecutive lanes, lane gl holding its
+  // k = 8 gl .. 8 gl + 7 (the row's unit gl, at slot gl ^ (row % 16)); two-pass statistics, the
+  // same butterfly, eps inside the square root; rounded once to bf16. The products then see the
+  // operand that pass would have written, bit for bit, without its round trip through HBM.
+  auto normalise_tile = [&](const int bf, const int ln, const int wv) __attribute__((always_inline)) {
+    constexpr int G = K / 8, RPW = 64 / G;  // lanes per row, rows per wave at a time
+    const int sub = ln / G, gl = ln - sub * G;
+    const float invk = 1.0f / (float)K;
+    unsigned char* ab = lds + bf * ABYTES;
+#pragma unroll
+    for (int r0 = 0; r0 < WR_P; r0 += WR_WAVES * RPW) {
+      const int r = r0 + wv * RPW + sub;
+      unsigned char* up = ab + r * ROWB + (gl ^ (r & 15)) * 16;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+      f32x8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x.v[2 * e] = __uint_as_float(raw[e] << 16);
+        x.v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u);
+      }
+      float mean = 0.f;
+      if constexpr (PRO == PRO_LN) {
+        float sm = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sm += x.v[i];
+        mean = group_sum<G>(sm) * invk;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = x.v[i] - mean;
+        ss += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<G>(ss) * invk + p.eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x.v[i] = (x.v[i] - mean) * rstd;
+      *reinterpret_cast<bf16x8*>(up) = pack_bf16(x);
+    }
+  };
   // ---- one tile: the products of A(t) from buffer bf into acc, then its epilogue
   // pixel block i of this wave: i, or with HALF the wave pair's half ph
   auto kloop = [&](const int bf, const int l32, const int hl, const int ph) __attribute__((always_inline)) {
@@ -310,6 +352,11 @@ wres_kernel(const WrP p) {
     issue_r(t, ln, wv);
     if (has_next) issue_a(t + R, bf ^ 1, ln, wv);
     asm volatile("" ::: "memory");
+    if constexpr (PRO != PRO_NONE) {
+      normalise_tile(bf, ln, wv);
+      barrier_keep_vm();  // every row of the tile normalised
+      asm volatile("" ::: "memory");
+    }
     kloop(bf, l32, hl, wv >> 2);
     // the residual copies (issued before the next tile's A copies) have landed, in every wave
     if constexpr (RDT >= 0) {
@@ -323,10 +370,10 @@ wres_kernel(const WrP p) {
   }
 }
 
-template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF>
+template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF, int PRO>
 void launch(const WrP& p, int nblk, hipStream_t s) {
   constexpr int lds = wr_lds_bytes(K, RC, RDT);
-  auto fn = &wres_kernel<GATE, RDT, CDT, K, RC, HALF>;
+  auto fn = &wres_kernel<GATE, RDT, CDT, K, RC, HALF, PRO>;
   static const bool attr = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
@@ -335,21 +382,21 @@ void launch(const WrP& p, int nblk, hipStream_t s) {
   hipLaunchKernelGGL(fn, dim3((unsigned)nblk), dim3(WR_THREADS), lds, s, p);
 }
 
-template <bool GATE, int RDT, int CDT, int RC>
+template <bool GATE, int RDT, int CDT, int RC, int PRO>
 void launch_k(const WrP& p, int k, bool half, int nblk, hipStream_t s) {
   if (half) {
-    if (k == 128) launch<GATE, RDT, CDT, 128, RC, true>(p, nblk, s);
-    else launch<GATE, RDT, CDT, 256, RC, true>(p, nblk, s);
+    if (k == 128) launch<GATE, RDT, CDT, 128, RC, true, PRO>(p, nblk, s);
+    else launch<GATE, RDT, CDT, 256, RC, true, PRO>(p, nblk, s);
   } else {
-    if (k == 128) launch<GATE, RDT, CDT, 128, RC, false>(p, nblk, s);
-    else launch<GATE, RDT, CDT, 256, RC, false>(p, nblk, s);
+    if (k == 128) launch<GATE, RDT, CDT, 128, RC, false, PRO>(p, nblk, s);
+    else launch<GATE, RDT, CDT, 256, RC, false, PRO>(p, nblk, s);
   }
 }
 
-template <bool GATE, int RDT, int RC>
+template <bool GATE, int RDT, int RC, int PRO = PRO_NONE>
 void launch_c(const WrP& p, int cdt, int k, bool half, int nblk, hipStream_t s) {
-  if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC>(p, k, half, nblk, s);
-  else launch_k<GATE, RDT, DT_BF16, RC>(p, k, half, nblk, s);
+  if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC, PRO>(p, k, half, nblk, s);
+  else launch_k<GATE, RDT, DT_BF16, RC, PRO>(p, k, half, nblk, s);
 }
 
 }  // namespace
@@ -367,9 +414,13 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16 && (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
                  "gemm_wr: bf16 A and W, bf16 / fp32 output");
   CLARUS_REQUIRE(a->res == nullptr || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_wr: bf16 / fp32 residual");
-  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 &&
                      (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
-                 "gemm_wr: plain rows (no prologue, batch or pixel shuffle)");
+                 "gemm_wr: plain rows (no batch or pixel shuffle)");
+  // a LayerNorm / RMS prologue on the A tile's rows in LDS, without a residual
+  const int pro = a->pro;
+  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr),
+                 "gemm_wr: no prologue, or LayerNorm / RMS without a residual (pro=%d)", pro);
   const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
   CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
                  "gemm_wr: 16-byte A rows and packed weight");
@@ -398,13 +449,22 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   p.a = (const bf16_t*)a->a; p.wp = wp; p.bias = a->bias; p.scale = a->scale; p.res = a->res; p.c = a->c;
   p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
   p.npass = (int)npass; p.ptiles = (int)ptiles; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
+  p.eps = a->ln_eps;
   const int rdt = a->res ? a->r_dtype : -1;
   // one pass with at most 256 real W^T rows: waves 4 - 7 take the pixel halves (HALF)
   const bool half = npass == 1 && (gate ? a->n <= 128 : a->n <= 256);
-  note_kernel("wres_kernel gate=%d res=%d k=%lld half=%d", (int)gate, rdt, (long long)a->k, (int)half);
+  note_kernel("wres_kernel gate=%d res=%d k=%lld half=%d pro=%d", (int)gate, rdt, (long long)a->k, (int)half, pro);
   hipStream_t s = (hipStream_t)stream;
   const int k = (int)a->k, cdt = a->c_dtype;
-  if (gate) {
+  if (pro != PRO_NONE) {
+    if (gate) {
+      if (pro == PRO_LN) launch_c<true, -1, 256, PRO_LN>(p, cdt, k, half, nblk, s);
+      else launch_c<true, -1, 256, PRO_RMS>(p, cdt, k, half, nblk, s);
+    } else {
+      if (pro == PRO_LN) launch_c<false, -1, 256, PRO_LN>(p, cdt, k, half, nblk, s);
+      else launch_c<false, -1, 256, PRO_RMS>(p, cdt, k, half, nblk, s);
+    }
+  } else if (gate) {
     if (rdt == DT_F32) launch_c<true, DT_F32, 256>(p, cdt, k, half, nblk, s);
     else if (rdt == DT_BF16) launch_c<true, DT_BF16, 256>(p, cdt, k, half, nblk, s);
     else launch_c<true, -1, 256>(p, cdt, k, half, nblk, s);

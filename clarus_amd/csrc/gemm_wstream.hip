@@ -449,13 +449,6 @@ __device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, I...>
 
 // sum over the G lanes of a row group, butterfly in the order 1, 2, .. G / 2 (clarus_hip_rows_
 // prologue's order, so the statistics below are bitwise those of that pass)
-template <int G>
-__device__ __forceinline__ float ws_group_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 // PRO: PRO_NONE, or PRO_LN / PRO_RMS applied to whole rows (K <= 512) before the K loop: each row
 // is normalised by one group of K / 8 lanes, lane g holding its k = 8 g .. 8 g + 7 as
 // clarus_hip_rows_prologue does (two-pass statistics, the same butterfly, eps inside the square
@@ -567,7 +560,7 @@ wstream128_kernel(const WsP p) {
       float sm = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) sm += x.v[i];
-      mean = ws_group_sum<G>(sm) * invk;
+      mean = group_sum<G>(sm) * invk;
     }
     float ss = 0.f;
 #pragma unroll
@@ -575,7 +568,7 @@ wstream128_kernel(const WsP p) {
       const float d = x.v[i] - mean;
       ss += d * d;
     }
-    const float rstd = rsqrtf(ws_group_sum<G>(ss) * invk + p.eps);
+    const float rstd = rsqrtf(group_sum<G>(ss) * invk + p.eps);
 #pragma unroll
     for (int i = 0; i < 8; ++i) x.v[i] = (x.v[i] - mean) * rstd;
   };

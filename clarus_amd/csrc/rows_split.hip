@@ -40,13 +40,6 @@ struct SplitP {
   float eps;
 };
 
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 template <int TA, int G, int FR, bool SPLIT>
 __global__ void __launch_bounds__(256) rows_split_kernel(const SplitP p) {
   constexpr int ES = TA == DT_BF16 ? 2 : 4;

@@ -102,6 +102,11 @@ class HipOps(Backend):
     # current one); False or other K keep them on the kernels above.
     wres = True
     wres_ks = (128, 256)
+    # LayerNorm / RMS linear without a residual, bf16 rows and weights, K in wres_ks: the prologue
+    # inside clarus_hip_gemm_wr on each A tile in LDS (the separate pass's operand bit for bit,
+    # without its round trip through HBM); False keeps the separate pass (K = 128) or the 128-pixel
+    # kernel's prologue (K = 256). NAFNet-w64 levels 1 and 2, conv1 and conv4.
+    wres_prologue = True
     # linear_patch_filter as one kernel (GEMM output straight into the patch DFT); False runs
     # linear (fp32 output) and patch_filter as two ops.
     fuse_patch_filter = True
@@ -241,6 +246,17 @@ class HipOps(Backend):
             return None
         return "wp", self._w2p(w, bool(gate))
 
+    def _wr_prologue(self, x, w, pro, k, nout, gate, act, res):
+        """("wr", W^T packed) when this LayerNorm / RMS linear runs with its prologue inside
+        clarus_hip_gemm_wr (see wres_prologue): the shapes whose separate pass would feed that
+        kernel, else None."""
+        if not (self.wres and self.wres_prologue and not self.prologue_split and res is None
+                and pro in (_lib.PRO_LN, _lib.PRO_RMS) and k in self.wres_ks and x.dtype == torch.bfloat16
+                and w.dtype == torch.bfloat16 and act in (0, _lib.ACT_GELU) and nout % 16 == 0
+                and (gate or act != 0 or nout != k)):
+            return None
+        return "wr", self._wr_pack(w, bool(gate))
+
     def _wp_prologue(self, x, w, pro, k, nout, gate, act, m, res):
         """("wp", W^T packed) when this LayerNorm / RMS linear runs with its prologue inside
         clarus_hip_gemm_wp (see wstream_prologue), else None."""
@@ -319,7 +335,8 @@ class HipOps(Backend):
                    act=_lib.ACT_GELU if act == "gelu" else 0)
         m = n * h * wd
         if self._prologue_pass(w, pro, k):
-            wpp = self._wp_prologue(x, w, pro, k, nout, gate, epi["act"], m, residual)
+            wpp = (self._wr_prologue(x, w, pro, k, nout, gate, epi["act"], residual)
+                   or self._wp_prologue(x, w, pro, k, nout, gate, epi["act"], m, residual))
             if wpp is not None:
                 return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
                                   ln_eps=float(ln_eps), wp=wpp, **epi)

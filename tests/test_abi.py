@@ -104,6 +104,12 @@ def test_validation_rejects_before_launch(lib):
     assert b"residual" in lib.clarus_hip_last_error()
     a.gate, a.n, a.ldc, a.ldr = 0, 512, 512, 512
     assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 residual, 512 outputs
+    a.pro = _lib.PRO_LN
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # LN with a residual
+    assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
+    a.pro, a.res = _lib.PRO_MUL, 0
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # a map prologue
+    assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
     # clarus_hip_ffn: c, dtype, prologue, alignment and overlap are checked before any launch
     ffn = lib.clarus_hip_ffn
     assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 256, 1, 1e-6, 1.0, None) == _lib.EINVAL

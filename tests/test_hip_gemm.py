@@ -391,6 +391,86 @@ def test_linear_ln_routes_to_wstream_prologue(hip_bf16):
         assert torch.equal(y1, y0), f"gate={gate}: max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("gate,k,nout,pro,odt,act,m", [
+    (False, 128, 256, "ln", torch.bfloat16, None, 360 * 640),  # NAFNet level-1 conv1
+    (True, 128, 128, "ln", torch.bfloat16, None, 360 * 640),   # ... conv4 (SimpleGate; half passes)
+    (False, 256, 512, "ln", torch.bfloat16, None, 64 * 7 + 5),
+    (True, 256, 256, "rms", torch.float32, "gelu", 1000),
+    (False, 128, 64, "rms", torch.float32, None, 333),         # N <= 256: half passes
+    (True, 256, 512, "ln", torch.bfloat16, None, 130),         # two passes
+])
+def test_gemm_wr_prologue(gate, k, nout, pro, odt, act, m, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wr with a LayerNorm / RMS prologue on the A tile's rows in
+    LDS: bit for bit the separate pass (clarus_hip_rows_prologue, rows rounded once to bf16)
+    followed by clarus_hip_gemm_wr on its rows; for fp32 outputs also the prologue rule of
+    check_prologue against the fp32 oracle. Rows offset from zero (x ~ 3 + N(0, 1)), ragged last
+    tiles, the half-pass form, two passes, bias and scale."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(91 + k + m)
+    nw = 2 * nout if gate else nout
+    x = (3 + rnd(g, m, k)).bfloat16()
+    w = rnd(g, k, nw, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc = rnd(g, nw), rnd(g, nout)
+    xd, wd, bd, sd = dev(x, w, b, sc)
+    wp = hip_bf16._wr_pack(wd, gate)
+    code = _lib.PRO_LN if pro == "ln" else _lib.PRO_RMS
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def gemm_wr(a, p, out):
+        args = _lib.GemmArgs(a=a.data_ptr(), wt=0, c=out.data_ptr(), bias=bd.data_ptr(), scale=sd.data_ptr(),
+                             m=m, n=nout, k=k, batch=1, lda=k, ldc=nout, a_dtype=_lib.BF16, w_dtype=_lib.BF16,
+                             c_dtype=_lib.dtype_code(odt), gate=int(gate), pro=p, ln_eps=1e-6,
+                             act=_lib.ACT_GELU if act == "gelu" else 0, out_scale=1.0)
+        _lib.check(lib.clarus_hip_gemm_wr(ctypes.byref(args), wp.data_ptr(), st), "gemm_wr")
+        return _lib.last_kernel()
+
+    fused = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern = gemm_wr(xd, code, fused)
+    assert kern.startswith(f"wres_kernel gate={int(gate)} res=-1 k={k}") and kern.endswith(f"pro={code}"), kern
+    rows = torch.empty(m, k, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.BF16, pro=code, ln_eps=1e-6)
+    _lib.check(lib.clarus_hip_rows_prologue(ctypes.byref(args), rows.data_ptr(), st), "rows_prologue")
+    two = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern2 = gemm_wr(rows, _lib.PRO_NONE, two)
+    assert torch.equal(fused, two), (f"{kern} vs {kern2}: max|d| "
+                                     f"{(fused.float() - two.float()).abs().max().item():.3e}")
+    if odt == torch.float32:
+        # offset rows through a gate: the stress case check_prologue scales its 2e-2 to the outputs
+        check_prologue(fused.cpu(), k, f"gemm_wr pro={pro} gate={gate} K{k} M{m}", x, w, b,
+                       ln=True if pro == "ln" else "rms", rounded=True, scaled=gate, gate=gate, scale=sc, act=act)
+
+
+def test_linear_ln_routes_to_wres_prologue(hip_bf16):
+    """HipOps.linear with LayerNorm at the NAFNet level-1 and level-2 shapes (bf16 rows, 360 x 640 x
+    128 and 180 x 320 x 256; conv1 to 2c channels and conv4 with SimpleGate) runs the prologue
+    inside clarus_hip_gemm_wr, bit-identical to the separate pass followed by the same kernel
+    (wres_prologue and wstream_prologue False)."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(73)
+    for h, wd, c in ((360, 640, 128), (180, 320, 256)):
+        x = (1 + rnd(g, 1, h, wd, c)).bfloat16().cuda()
+        for gate, nout in ((False, 2 * c), (True, c)):
+            w = rnd(g, c, 2 * nout if gate else nout, scale=c ** -0.5, dtype=torch.bfloat16).cuda()
+            b = rnd(g, 2 * nout if gate else nout).cuda()
+            saved = HipOps.wres_prologue, HipOps.wstream_prologue
+            try:
+                HipOps.wres_prologue = True
+                y1 = hip_bf16.linear(x, w, b, ln=True, gate=gate)
+                k1 = _lib.last_kernel()
+                HipOps.wres_prologue = HipOps.wstream_prologue = False
+                y0 = hip_bf16.linear(x, w, b, ln=True, gate=gate)
+                k0 = _lib.last_kernel()
+            finally:
+                HipOps.wres_prologue, HipOps.wstream_prologue = saved
+            assert k1.startswith("wres_kernel") and k1.endswith("pro=1"), k1
+            assert k0.startswith("wres_kernel") and k0.endswith("pro=0"), k0
+            assert torch.equal(y1, y0), f"c{c} gate={gate}: max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("gate,k,nout,rdt,odt,act,m", [
     (True, 256, 256, None, torch.bfloat16, None, 64 * 9 + 1),
     (True, 128, 128, None, torch.bfloat16, None, 1000),
