@@ -67,6 +67,10 @@ struct WsP {
   int c_dt, act;
   float out_scale, slope;
   float eps;  // LayerNorm / RMS prologue (wstream128_kernel)
+  // map prologue (wstream_kernel with MUL): A row q times the bf16 map row of its pixel, the
+  // map [n][oh][ow][K] replicate-padded to the h x w image by the offsets pt, pl
+  const bf16_t* small;
+  int h, w, oh, ow, pt, pl;
 };
 
 // RDT: residual dtype (-1: none); NCH: 64-k chunks (K / 64). The K loop is unrolled: with a
@@ -77,7 +81,11 @@ struct WsP {
 // copied into LDS once and serves both passes; the second pass's first two W^T groups are loaded
 // before the first pass's epilogue, so its stores drain under the second pass's products, and the
 // second pass needs no barrier (its A chunks are those the first pass already waited for).
-template <bool GATE, int RDT, int NCH, int NPW>
+// MUL (ring only): the map prologue of clarus_hip_rows_prologue applied to A in LDS. Each lane
+// multiplies the 16-byte unit it copied of chunk c by the map values of its row, loaded at kernel
+// start, once its own copies of the chunk have landed and before the barrier that publishes the
+// chunk: widened to fp32, multiplied, rounded once to bf16, bit for bit the pass's rows.
+template <bool GATE, int RDT, int NCH, int NPW, bool MUL>
 __global__ void __launch_bounds__(WS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wstream_kernel(const WsP p) {
   constexpr int NO = GATE ? 256 : 512;                    // output channels per pass
@@ -94,6 +102,7 @@ wstream_kernel(const WsP p) {
   // are in issue order).
   constexpr bool RESIDENT = RDT < 0;
   static_assert(NPW == 1 || (NPW == 2 && RESIDENT), "two passes per workgroup only with a resident A tile");
+  static_assert(!MUL || (!RESIDENT && NCH <= 8), "the map prologue on the ring, K <= 512");
   constexpr int ABYTES = ws_a_bytes(RDT, NCH);
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   float* tb = reinterpret_cast<float*>(lds + ABYTES + WS_P * RB);
@@ -102,6 +111,29 @@ wstream_kernel(const WsP p) {
   const int b = blockIdx.x;
   const int lin = (b & 7) * p.per_xcd + (b >> 3);
   if (lin >= p.tiles) return;  // before any LDS or memory traffic
+  const int ngrp = p.npass / NPW;  // groups of NPW passes per pixel tile
+  const int pt = lin / ngrp, ps0 = (lin - pt * ngrp) * NPW;
+  const int64_t q0 = (int64_t)pt * WS_P;
+  // ---- A chunk c (8 KiB): wave w copies rows 8 w .. 8 w + 7, lane l row 8 w + l / 8, slot l % 8
+  const int arow = wave * 8 + (lane >> 3);
+  int64_t aq = q0 + arow;
+  if (aq > p.m - 1) aq = p.m - 1;  // rows past M: any valid row, never stored
+  // ---- map values of this lane's unit in every chunk (the kernel's first memory operations: the
+  // first chunk's wait covers them)
+  u32x4 mv[MUL ? NCH : 1];
+  if constexpr (MUL) {
+    const int64_t hw = (int64_t)p.h * p.w;
+    const int64_t im = aq / hw;
+    const int rr = (int)(aq - im * hw);
+    const int yq = rr / p.w;
+    int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
+    sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
+    sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
+    const bf16_t* mrow = p.small + ((im * p.oh + sy) * p.ow + sx) * (int64_t)(NCH * 64) + m32_swz(arow, lane & 7) * 8;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) mv[c] = *reinterpret_cast<const u32x4*>(mrow + c * 64);
+    asm volatile("" ::: "memory");
+  }
 
   // ---- the packed weight into this XCD's L2 first, when it fits comfortably (<= 2 MiB): the
   // XCD's workgroups read it all, in step, so from a cold cache each 64-k group would miss in all
@@ -123,15 +155,7 @@ wstream_kernel(const WsP p) {
     }
   }
   asm volatile("" ::: "memory");
-  const int ngrp = p.npass / NPW;  // groups of NPW passes per pixel tile
-  const int pt = lin / ngrp, ps0 = (lin - pt * ngrp) * NPW;
-  const int64_t q0 = (int64_t)pt * WS_P;
   const int64_t och0 = (int64_t)ps0 * NO;  // first output channel of the workgroup's first pass
-
-  // ---- A chunk c (8 KiB): wave w copies rows 8 w .. 8 w + 7, lane l row 8 w + l / 8, slot l % 8
-  const int arow = wave * 8 + (lane >> 3);
-  int64_t aq = q0 + arow;
-  if (aq > p.m - 1) aq = p.m - 1;  // rows past M: any valid row, never stored
   const unsigned char* asrc = (const unsigned char*)(p.a + aq * p.lda) + m32_swz(arow, lane & 7) * 16;
   auto issue_a = [&](int c) __attribute__((always_inline)) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(asrc + c * 128),
@@ -273,6 +297,17 @@ wstream_kernel(const WsP p) {
       else if (n >= 9) wait_vmcnt<9>();
       else if (n >= RPC) wait_vmcnt<RPC>();
       else wait_vmcnt<0>();
+    }
+    if constexpr (MUL) {  // this lane's unit of chunk c (its copy has landed) times the map
+      unsigned char* up = lds + (c % WS_STAGES) * WS_STAGE + wave * 1024 + lane * 16;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+      f32x8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x.v[2 * e] = __uint_as_float(raw[e] << 16) * __uint_as_float(mv[c][e] << 16);
+        x.v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u) * __uint_as_float(mv[c][e] & 0xffff0000u);
+      }
+      *reinterpret_cast<bf16x8*>(up) = pack_bf16(x);
     }
     // ring: every wave's share of A chunk c, and chunk c - 1 read by all (its stage is refilled);
     // resident: every wave's share of the chunks up to the next batch
@@ -716,10 +751,10 @@ void launch128_g(const WsP& p, bool gate, hipStream_t s) {
   }
 }
 
-template <bool GATE, int RDT, int NCH, int NPW>
+template <bool GATE, int RDT, int NCH, int NPW, bool MUL = false>
 void launch(const WsP& p, hipStream_t s) {
   constexpr int lds = ws_lds_bytes(GATE, RDT, NCH, NPW);
-  auto fn = &wstream_kernel<GATE, RDT, NCH, NPW>;
+  auto fn = &wstream_kernel<GATE, RDT, NCH, NPW, MUL>;
   static const bool attr = [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
@@ -729,7 +764,14 @@ void launch(const WsP& p, hipStream_t s) {
 }
 
 template <bool GATE, int RDT>
-void launch_k(const WsP& p, int npw, hipStream_t s) {
+void launch_k(const WsP& p, int npw, hipStream_t s, bool mul = false) {
+  if constexpr (RDT >= 0) {
+    if (mul) {
+      if (p.nch == 4) launch<GATE, RDT, 4, 1, true>(p, s);
+      else launch<GATE, RDT, 8, 1, true>(p, s);
+      return;
+    }
+  }
   if constexpr (RDT < 0) {
     if (npw == 2) {
       if (p.nch == 4) launch<GATE, RDT, 4, 2>(p, s);
@@ -763,9 +805,18 @@ extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void*
                  "gemm_wp: bf16 A (fp32 with a prologue) and W, bf16 / fp32 output");
   CLARUS_REQUIRE(a->res == nullptr || a->r_dtype == DT_BF16 || a->r_dtype == DT_F32, "gemm_wp: bf16 / fp32 residual");
   // a LayerNorm / RMS prologue (no residual, K <= 512) runs inside the 128-pixel kernel, on the
-  // whole rows its A tile holds
-  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr && a->k <= 512),
-                 "gemm_wp: no prologue, or LayerNorm / RMS without a residual at K <= 512 (pro=%d)", pro);
+  // whole rows its A tile holds; the map prologue (a residual, K <= 512, bf16 A and map) on the
+  // 64-pixel ring's chunks
+  const bool mul = pro == PRO_MUL;
+  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr && a->k <= 512) ||
+                     (mul && a->res != nullptr && a->k <= 512),
+                 "gemm_wp: no prologue, LayerNorm / RMS without a residual at K <= 512, or the map prologue "
+                 "with a residual at K <= 512 (pro=%d)", pro);
+  if (mul) {
+    CLARUS_REQUIRE(a->small && a->s_dtype == DT_BF16 && a->a_dtype == DT_BF16 && aligned(a->small, 16) &&
+                       a->h > 0 && a->w > 0 && a->oh > 0 && a->ow > 0 && a->m % ((int64_t)a->h * a->w) == 0,
+                   "gemm_wp: the map prologue needs a bf16 map (16-byte aligned), bf16 A and m a multiple of h w");
+  }
   CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 &&
                      (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
                  "gemm_wp: plain rows (no batch or pixel shuffle)");
@@ -796,6 +847,8 @@ extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void*
   p.tiles = (int)(p128 ? ptiles128 * npass : ptiles * npass / npw);
   p.per_xcd = (int)cdiv(p.tiles, 8);
   p.c_dt = a->c_dtype; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope; p.eps = a->ln_eps;
+  p.small = (const bf16_t*)a->small;
+  p.h = (int)a->h; p.w = (int)a->w; p.oh = (int)a->oh; p.ow = (int)a->ow; p.pt = (int)a->pt; p.pl = (int)a->pl;
   const int rdt = a->res ? a->r_dtype : -1;
   note_kernel("wstream_kernel gate=%d res=%d pro=%d k=%lld p=%d npw=%d", (int)gate, rdt, pro, (long long)a->k,
               p128 ? W2_P : WS_P, p128 ? 1 : npw);
@@ -806,12 +859,12 @@ extern "C" int clarus_hip_gemm_wp(const ClarusGemmArgs* a, const void* wp, void*
     else if (pro == PRO_RMS) f32 ? launch128_g<PRO_RMS, DT_F32>(p, gate, s) : launch128_g<PRO_RMS, DT_BF16>(p, gate, s);
     else launch128_g<PRO_NONE, DT_BF16>(p, gate, s);
   } else if (gate) {
-    if (rdt == DT_F32) launch_k<true, DT_F32>(p, npw, s);
-    else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, npw, s);
+    if (rdt == DT_F32) launch_k<true, DT_F32>(p, npw, s, mul);
+    else if (rdt == DT_BF16) launch_k<true, DT_BF16>(p, npw, s, mul);
     else launch_k<true, -1>(p, npw, s);
   } else {
-    if (rdt == DT_F32) launch_k<false, DT_F32>(p, npw, s);
-    else if (rdt == DT_BF16) launch_k<false, DT_BF16>(p, npw, s);
+    if (rdt == DT_F32) launch_k<false, DT_F32>(p, npw, s, mul);
+    else if (rdt == DT_BF16) launch_k<false, DT_BF16>(p, npw, s, mul);
     else launch_k<false, -1>(p, npw, s);
   }
   return check_launch("gemm_wp");

@@ -97,6 +97,11 @@ class HipOps(Backend):
     # kernel's (tile, pass) count covers 3/4 of the compute units; False, or fewer tiles, keep the
     # separate pass. Reference-block NAFNet-w64 forward: level 3 conv1 and conv4.
     wstream_prologue = True
+    # TLC-map multiply linear with a residual, bf16 rows and map, K <= 512, whose rows the separate
+    # pass would feed to clarus_hip_gemm_wp's 64-pixel ring: the multiply inside that kernel on each
+    # A chunk in LDS (the pass's operand bit for bit); False keeps the separate pass. Reference-
+    # block NAFNet-w64 forward: level-3 conv3.
+    wstream_mul = True
     # Plain bf16 GEMMs with K in wres_ks on clarus_hip_gemm_wr (persistent workgroups, each keeping
     # its 512-row W^T pass in registers for all of its pixel tiles, the next A tile copied during the
     # current one); False or other K keep them on the kernels above.
@@ -257,6 +262,15 @@ class HipOps(Backend):
             return None
         return "wr", self._wr_pack(w, bool(gate))
 
+    def _wp_mul(self, x, w, pro, sm, k, nout, gate, act, m, res):
+        """("wp", W^T packed) when this map-prologue linear runs with the multiply inside
+        clarus_hip_gemm_wp's 64-pixel ring (see wstream_mul), else None."""
+        if not (self.wstream_mul and not self.prologue_split and pro == _lib.PRO_MUL and res is not None
+                and sm is not None and sm.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and k <= 512):
+            return None
+        wp = self._wp_for(x, w, k, nout, gate, act, m, res)
+        return wp if wp is not None and wp[0] == "wp" else None
+
     def _wp_prologue(self, x, w, pro, k, nout, gate, act, m, res):
         """("wp", W^T packed) when this LayerNorm / RMS linear runs with its prologue inside
         clarus_hip_gemm_wp (see wstream_prologue), else None."""
@@ -336,10 +350,11 @@ class HipOps(Backend):
         m = n * h * wd
         if self._prologue_pass(w, pro, k):
             wpp = (self._wr_prologue(x, w, pro, k, nout, gate, epi["act"], residual)
-                   or self._wp_prologue(x, w, pro, k, nout, gate, epi["act"], m, residual))
+                   or self._wp_prologue(x, w, pro, k, nout, gate, epi["act"], m, residual)
+                   or self._wp_mul(x, w, pro, sm, k, nout, gate, epi["act"], m, residual))
             if wpp is not None:
                 return self._gemm("linear", a=x, wt=self._wt(w), c=out, m=m, n=nout, k=k, lda=k, ldc=nout, pro=pro,
-                                  ln_eps=float(ln_eps), wp=wpp, **epi)
+                                  small=sm, geom=geom, ln_eps=float(ln_eps), wp=wpp, **epi)
             # the separate prologue pass of triton_cuda.py:104-110 (ln_rows / mul_small), then a
             # plain bf16 GEMM: rows rounded once to bf16 (K), or as [hi | lo] (K' = 2K)
             rows = self._prologue_rows(x, pro, sm, geom, ln_eps, m, k)

@@ -120,8 +120,10 @@ int clarus_hip_gemm(const ClarusGemmArgs* args, void* stream);
  * clarus_hip_gemm for plain bf16 rows (a_mode rows, pro none, batch 1, c_mode rows) with bf16 W,
  * K = 256, 512 or 1024 and W^T rows (n, or 2 n with gate) a multiple of 512, with W^T
  * also passed packed. pro may also be CLARUS_PRO_LN / CLARUS_PRO_RMS (ln_eps) without a residual
- * at K <= 512, on bf16 or fp32 rows: the result is bit for bit clarus_hip_rows_prologue's rows
- * (rounded once to bf16) through this entry point, in one launch.
+ * at K <= 512, on bf16 or fp32 rows, or CLARUS_PRO_MUL (bf16 rows and map; small, s_dtype, h, w,
+ * oh, ow, pt, pl as for clarus_hip_gemm, m a multiple of h w) with a residual at K <= 512: the
+ * result is bit for bit clarus_hip_rows_prologue's rows (rounded once to bf16) through this entry
+ * point, in one launch.
  * wp holds W^T in the fragment order of clarus_hip_gemm_ln_gemm's w2p (K
  * columns instead of 512: for pass P, wave w, 16-k step s (0 .. K / 16 - 1), block b, lane l, the
  * 8 values W^T[row(P, 64 w + 32 b + l % 32)][16 s + 8 (l / 32) + e], with gate2 = gate).

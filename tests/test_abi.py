@@ -92,6 +92,12 @@ def test_validation_rejects_before_launch(lib):
     a.pro, a.res, a.r_dtype, a.ldr = _lib.PRO_LN, 16, _lib.F32, 256
     assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # LN with a residual
     assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
+    a.pro, a.res = _lib.PRO_MUL, 0
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # the map prologue without a residual
+    assert b"map prologue with a residual" in lib.clarus_hip_last_error()
+    a.res = 16
+    assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # ... without a map
+    assert b"bf16 map" in lib.clarus_hip_last_error()
     a.pro, a.res, a.a_dtype = 0, 0, _lib.F32
     assert lib.clarus_hip_gemm_wp(ctypes.byref(a), 16, None) == _lib.EINVAL  # fp32 A
     assert b"bf16 A" in lib.clarus_hip_last_error()

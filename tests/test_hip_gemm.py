@@ -391,6 +391,84 @@ def test_linear_ln_routes_to_wstream_prologue(hip_bf16):
         assert torch.equal(y1, y0), f"gate={gate}: max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("gate,k,nout,n,h,w,rdt,odt", [
+    (False, 512, 512, 1, 90, 160, torch.float32, torch.float32),   # NAFNet level-3 conv3
+    (False, 256, 512, 2, 37, 53, torch.bfloat16, torch.bfloat16),  # two images, ragged last tile
+    (True, 512, 256, 1, 20, 30, torch.float32, torch.bfloat16),
+    (True, 256, 512, 3, 9, 11, torch.bfloat16, torch.float32),
+])
+def test_gemm_wp_mul(gate, k, nout, n, h, w, rdt, odt, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wp with the TLC-map multiply prologue (64-pixel ring, a
+    residual): bit for bit the separate pass (clarus_hip_rows_prologue with PRO_MUL) followed by
+    clarus_hip_gemm_wp on its rows; maps smaller than the image on both axes (replicate padding
+    at every edge), several images, bias, scale and residual."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(97 + k + h)
+    m = n * h * w
+    nw = 2 * nout if gate else nout
+    _, _, oh, ow, pt, pl = box_geometry(h, w, (max(2, h // 2), max(2, w // 2)))
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    smap = rnd(g, n, oh, ow, k, scale=0.5, dtype=torch.bfloat16)
+    wt = rnd(g, k, nw, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc, r = rnd(g, nw), rnd(g, nout), rnd(g, m, nout).to(rdt)
+    xd, sd, wd, bd, scd, rd = dev(x, smap, wt, b, sc, r)
+    wp = hip_bf16._w2p(wd, gate)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    geo = dict(h=h, w=w, oh=oh, ow=ow, pt=pt, pl=pl)
+
+    def gemm_wp(a, p, out):
+        args = _lib.GemmArgs(a=a.data_ptr(), wt=0, c=out.data_ptr(), bias=bd.data_ptr(), scale=scd.data_ptr(),
+                             res=rd.data_ptr(), small=sd.data_ptr(), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout,
+                             ldr=nout, a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+                             r_dtype=_lib.dtype_code(rdt), s_dtype=_lib.BF16, gate=int(gate), pro=p,
+                             out_scale=1.0, **geo)
+        _lib.check(lib.clarus_hip_gemm_wp(ctypes.byref(args), wp.data_ptr(), st), "gemm_wp")
+        return _lib.last_kernel()
+
+    fused = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern = gemm_wp(xd, _lib.PRO_MUL, fused)
+    assert kern.startswith(f"wstream_kernel gate={int(gate)} res={_lib.dtype_code(rdt)} pro={_lib.PRO_MUL}"), kern
+    rows = torch.empty(m, k, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.BF16, pro=_lib.PRO_MUL,
+                         small=sd.data_ptr(), s_dtype=_lib.BF16, **geo)
+    _lib.check(lib.clarus_hip_rows_prologue(ctypes.byref(args), rows.data_ptr(), st), "rows_prologue")
+    two = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern2 = gemm_wp(rows, _lib.PRO_NONE, two)
+    assert torch.equal(fused, two), (f"{kern} vs {kern2}: max|d| "
+                                     f"{(fused.float() - two.float()).abs().max().item():.3e}")
+
+
+def test_linear_mul_routes_to_wstream(hip_bf16):
+    """HipOps.linear with the TLC-map multiply at the NAFNet level-3 conv3 shape (90 x 160 x 512,
+    the 43 x 113 map of the 48 x 48 local mean, scale and fp32 residual) runs the multiply inside
+    the 64-pixel ring, bit-identical to the separate pass and the same kernel (wstream_mul
+    False)."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(79)
+    t = rnd(g, 1, 90, 160, 512, dtype=torch.bfloat16).cuda()
+    _, _, oh, ow, pt, pl = box_geometry(90, 160, (48, 48))
+    s = Small(rnd(g, 1, oh, ow, 512, scale=0.5, dtype=torch.bfloat16).cuda(), pt, pl, 90, 160)
+    w = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda()
+    b, beta, res = rnd(g, 512).cuda(), rnd(g, 512, scale=0.2).cuda(), rnd(g, 1, 90, 160, 512).cuda()
+    saved = HipOps.wstream_mul
+    try:
+        HipOps.wstream_mul = True
+        y1 = hip_bf16.linear(t, w, b, mul=s, scale=beta, residual=res, out_dtype=torch.float32)
+        k1 = _lib.last_kernel()
+        HipOps.wstream_mul = False
+        y0 = hip_bf16.linear(t, w, b, mul=s, scale=beta, residual=res, out_dtype=torch.float32)
+        k0 = _lib.last_kernel()
+    finally:
+        HipOps.wstream_mul = saved
+    assert k1.startswith(f"wstream_kernel gate=0 res=0 pro={_lib.PRO_MUL}"), k1
+    assert k0.startswith("wstream_kernel gate=0 res=0 pro=0"), k0
+    assert torch.equal(y1, y0), f"max|d| {(y1 - y0).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("gate,k,nout,pro,odt,act,m", [
     (False, 128, 256, "ln", torch.bfloat16, None, 360 * 640),  # NAFNet level-1 conv1
     (True, 128, 128, "ln", torch.bfloat16, None, 360 * 640),   # ... conv4 (SimpleGate; half passes)
