@@ -63,12 +63,19 @@ struct WrP {
   int64_t m, n, lda, ldr, ldc;
   int npass, ptiles, act;
   float out_scale, slope, eps;
+  // PRO_MUL: A row q times the bf16 map row of its pixel ([n][oh][ow][K], replicate-padded to the
+  // h x w image by the offsets pt, pl)
+  const bf16_t* small;
+  int h, w, oh, ow, pt, pl;
 };
 
 // GATE: SimpleGate pairs (256 output channels per pass); RDT: residual dtype (-1 none); CDT:
 // output dtype; K: 128 or 256; RC: residual channels staged per row (256, or 512 without the gate);
-// HALF: one pass of at most 256 real W^T rows, its pixels split over wave pairs; PRO: PRO_NONE, or
-// PRO_LN / PRO_RMS applied to the A tile's rows in LDS before its products (no residual)
+// HALF: one pass of at most 256 real W^T rows, its pixels split over wave pairs; PRO: PRO_NONE,
+// PRO_LN / PRO_RMS applied to the A tile's rows in LDS before its products (no residual), or PRO_MUL
+// (no gate): each lane multiplies the units it copied of a tile by their map values (loaded just
+// before the tile's copies, so they land first) once its copies have landed, before the barrier
+// that publishes the tile; widened to fp32, multiplied, rounded once to bf16 as the separate pass
 template <bool GATE, int RDT, int CDT, int K, int RC, bool HALF, int PRO>
 __global__ void __launch_bounds__(WR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 wres_kernel(const WrP p) {
@@ -85,7 +92,8 @@ wres_kernel(const WrP p) {
   constexpr int NS = NPB * (GATE ? 1 : 2) * (16 * OES / 16);  // 16-byte stores per lane per tile
   static_assert(RDT < 0 || (WR_P * RB) % (1024 * WR_WAVES) == 0, "residual copies per wave");
   static_assert(RDT < 0 || RC >= NO || !GATE, "the gate stages all 256 channels");
-  static_assert(PRO == PRO_NONE || RDT < 0, "a row prologue only without a residual");
+  static_assert(PRO == PRO_NONE || PRO == PRO_MUL || RDT < 0, "a row prologue only without a residual");
+  static_assert(PRO != PRO_MUL || !GATE, "the map prologue without the gate");
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int NBUF = wr_nbuf(RDT);
   unsigned char* rbuf = lds + NBUF * ABYTES;
@@ -150,7 +158,32 @@ wres_kernel(const WrP p) {
     }
   };
 
+  // map values of the units this lane copies of tile t (the row and unit of issue_a's copy i)
+  u32x4 mv[PRO == PRO_MUL ? NA : 1];
+  auto load_map = [&](int t, int lane, int wave) __attribute__((always_inline)) {
+    if constexpr (PRO == PRO_MUL) {
+      const int64_t hw = (int64_t)p.h * p.w;
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int off = (wave * NA + i) * 1024 + lane * 16;
+        const int row = off / ROWB, s = (off % ROWB) / 16;
+        int64_t q = (int64_t)t * WR_P + row;
+        if (q > p.m - 1) q = p.m - 1;
+        const int64_t im = q / hw;
+        const int rr = (int)(q - im * hw);
+        const int yq = rr / p.w;
+        int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
+        sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
+        sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
+        mv[i] = *reinterpret_cast<const u32x4*>(p.small + ((im * p.oh + sy) * p.ow + sx) * (int64_t)K +
+                                                (s ^ (row & 15)) * 8);
+      }
+    }
+  };
+
   f32x16 acc[NPB][2];
+  load_map(t_first, lane, wave);
+  asm volatile("" ::: "memory");
   issue_a(t_first, 0, lane, wave);
   // ---- tables (after the W^T loads and the first copies, so the three latencies overlap): bias of the pass's W^T rows (gate: the first halves' 256, then the second
   // halves'), scale of its output channels (1 for none, 0 bias for none; 0 past n)
@@ -347,12 +380,30 @@ wres_kernel(const WrP p) {
     // stores; a wave without outputs issues none), then every wave's
     if (t == t_first || !active) wait_vmcnt<0>();
     else wait_vmcnt<NS>();
+    if constexpr (PRO == PRO_MUL) {  // this lane's units of A(t) (its copies have landed) times the map
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        unsigned char* up = lds + bf * ABYTES + (wv * NA + i) * 1024 + ln * 16;
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+        f32x8 xm;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xm.v[2 * e] = __uint_as_float(raw[e] << 16) * __uint_as_float(mv[i][e] << 16);
+          xm.v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u) * __uint_as_float(mv[i][e] & 0xffff0000u);
+        }
+        *reinterpret_cast<bf16x8*>(up) = pack_bf16(xm);
+      }
+    }
     barrier_keep_vm();
     asm volatile("" ::: "memory");
     issue_r(t, ln, wv);
-    if (has_next) issue_a(t + R, bf ^ 1, ln, wv);
+    if (has_next) {
+      load_map(t + R, ln, wv);  // before the copies: landed when they have
+      asm volatile("" ::: "memory");
+      issue_a(t + R, bf ^ 1, ln, wv);
+    }
     asm volatile("" ::: "memory");
-    if constexpr (PRO != PRO_NONE) {
+    if constexpr (PRO == PRO_LN || PRO == PRO_RMS) {
       normalise_tile(bf, ln, wv);
       barrier_keep_vm();  // every row of the tile normalised
       asm volatile("" ::: "memory");
@@ -393,6 +444,23 @@ void launch_k(const WrP& p, int k, bool half, int nblk, hipStream_t s) {
   }
 }
 
+// the map prologue: at K = 256 the half-pass form only (the full-pass forms with it spill)
+template <int RDT, int CDT, int RC>
+void launch_mul_k(const WrP& p, int k, bool half, int nblk, hipStream_t s) {
+  if (k == 128) {
+    if (half) launch<false, RDT, CDT, 128, RC, true, PRO_MUL>(p, nblk, s);
+    else launch<false, RDT, CDT, 128, RC, false, PRO_MUL>(p, nblk, s);
+  } else {
+    launch<false, RDT, CDT, 256, RC, true, PRO_MUL>(p, nblk, s);
+  }
+}
+
+template <int RDT, int RC>
+void launch_mul(const WrP& p, int cdt, int k, bool half, int nblk, hipStream_t s) {
+  if (cdt == DT_F32) launch_mul_k<RDT, DT_F32, RC>(p, k, half, nblk, s);
+  else launch_mul_k<RDT, DT_BF16, RC>(p, k, half, nblk, s);
+}
+
 template <bool GATE, int RDT, int RC, int PRO = PRO_NONE>
 void launch_c(const WrP& p, int cdt, int k, bool half, int nblk, hipStream_t s) {
   if (cdt == DT_F32) launch_k<GATE, RDT, DT_F32, RC, PRO>(p, k, half, nblk, s);
@@ -417,10 +485,18 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 &&
                      (a->act == ACT_NONE || a->act == ACT_GELU || a->act == ACT_LRELU),
                  "gemm_wr: plain rows (no batch or pixel shuffle)");
-  // a LayerNorm / RMS prologue on the A tile's rows in LDS, without a residual
+  // a LayerNorm / RMS prologue on the A tile's rows in LDS, without a residual; the map prologue
+  // without the gate
   const int pro = a->pro;
-  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr),
-                 "gemm_wr: no prologue, or LayerNorm / RMS without a residual (pro=%d)", pro);
+  CLARUS_REQUIRE(pro == PRO_NONE || ((pro == PRO_LN || pro == PRO_RMS) && a->res == nullptr) ||
+                     (pro == PRO_MUL && !gate),
+                 "gemm_wr: no prologue, LayerNorm / RMS without a residual, or the map prologue without the gate "
+                 "(pro=%d)", pro);
+  if (pro == PRO_MUL) {
+    CLARUS_REQUIRE(a->small && a->s_dtype == DT_BF16 && aligned(a->small, 16) && a->h > 0 && a->w > 0 && a->oh > 0 &&
+                       a->ow > 0 && a->m % ((int64_t)a->h * a->w) == 0,
+                   "gemm_wr: the map prologue needs a bf16 map (16-byte aligned) and m a multiple of h w");
+  }
   const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
   CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(wp, 16),
                  "gemm_wr: 16-byte A rows and packed weight");
@@ -450,13 +526,21 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   p.m = a->m; p.n = a->n; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc;
   p.npass = (int)npass; p.ptiles = (int)ptiles; p.act = a->act; p.out_scale = a->out_scale; p.slope = a->slope;
   p.eps = a->ln_eps;
+  p.small = (const bf16_t*)a->small;
+  p.h = a->h; p.w = a->w; p.oh = a->oh; p.ow = a->ow; p.pt = a->pt; p.pl = a->pl;
   const int rdt = a->res ? a->r_dtype : -1;
   // one pass with at most 256 real W^T rows: waves 4 - 7 take the pixel halves (HALF)
   const bool half = npass == 1 && (gate ? a->n <= 128 : a->n <= 256);
   note_kernel("wres_kernel gate=%d res=%d k=%lld half=%d pro=%d", (int)gate, rdt, (long long)a->k, (int)half, pro);
   hipStream_t s = (hipStream_t)stream;
   const int k = (int)a->k, cdt = a->c_dtype;
-  if (pro != PRO_NONE) {
+  if (pro == PRO_MUL) {
+    CLARUS_REQUIRE(k == 128 || half, "gemm_wr: the map prologue at K = 256 needs N <= 256 (one half pass)");
+    if (rdt == DT_F32) launch_mul<DT_F32, 256>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16 && rc == 512) launch_mul<DT_BF16, 512>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16) launch_mul<DT_BF16, 256>(p, cdt, k, half, nblk, s);
+    else launch_mul<-1, 256>(p, cdt, k, half, nblk, s);
+  } else if (pro != PRO_NONE) {
     if (gate) {
       if (pro == PRO_LN) launch_c<true, -1, 256, PRO_LN>(p, cdt, k, half, nblk, s);
       else launch_c<true, -1, 256, PRO_RMS>(p, cdt, k, half, nblk, s);

@@ -102,6 +102,9 @@ class HipOps(Backend):
     # A chunk in LDS (the pass's operand bit for bit); False keeps the separate pass. Reference-
     # block NAFNet-w64 forward: level-3 conv3.
     wstream_mul = True
+    # The same multiply inside clarus_hip_gemm_wr (no gate; at K = 256 one half pass, N <= 256)
+    # where the separate pass would feed that kernel: NAFNet level-2 conv3.
+    wres_mul = True
     # Plain bf16 GEMMs with K in wres_ks on clarus_hip_gemm_wr (persistent workgroups, each keeping
     # its 512-row W^T pass in registers for all of its pixel tiles, the next A tile copied during the
     # current one); False or other K keep them on the kernels above.
@@ -263,13 +266,17 @@ class HipOps(Backend):
         return "wr", self._wr_pack(w, bool(gate))
 
     def _wp_mul(self, x, w, pro, sm, k, nout, gate, act, m, res):
-        """("wp", W^T packed) when this map-prologue linear runs with the multiply inside
-        clarus_hip_gemm_wp's 64-pixel ring (see wstream_mul), else None."""
-        if not (self.wstream_mul and not self.prologue_split and pro == _lib.PRO_MUL and res is not None
-                and sm is not None and sm.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and k <= 512):
+        """("wp" | "wr", W^T packed) when this map-prologue linear runs with the multiply inside the
+        kernel its separate pass would feed (see wstream_mul, wres_mul), else None."""
+        if not (not self.prologue_split and pro == _lib.PRO_MUL and sm is not None and sm.dtype == torch.bfloat16
+                and x.dtype == torch.bfloat16 and k <= 512):
             return None
         wp = self._wp_for(x, w, k, nout, gate, act, m, res)
-        return wp if wp is not None and wp[0] == "wp" else None
+        if wp is None:
+            return None
+        if wp[0] == "wp":
+            return wp if self.wstream_mul and res is not None else None
+        return wp if self.wres_mul and not gate and (k == 128 or nout <= 256) else None
 
     def _wp_prologue(self, x, w, pro, k, nout, gate, act, m, res):
         """("wp", W^T packed) when this LayerNorm / RMS linear runs with its prologue inside

@@ -138,8 +138,10 @@ int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream)
  * clarus_hip_gemm for plain bf16 rows (a_mode rows, pro none, batch 1, c_mode rows) with bf16 W,
  * K = 128 or 256 and N a multiple of 16, on a persistent kernel that keeps each workgroup's
  * 512-row W^T pass in registers for all of its pixel tiles. pro may also be CLARUS_PRO_LN /
- * CLARUS_PRO_RMS (ln_eps) without a residual: each A tile's rows are normalised in LDS before its
- * products, bit for bit what clarus_hip_rows_prologue would have written. wp is W^T packed as for
+ * CLARUS_PRO_RMS (ln_eps) without a residual, or CLARUS_PRO_MUL without gate (bf16 map; small,
+ * s_dtype, h, w, oh, ow, pt, pl as for clarus_hip_gemm; at K = 256 n <= 256): each A tile's rows are
+ * normalised / multiplied in LDS before its products, bit for bit what clarus_hip_rows_prologue
+ * would have written. wp is W^T packed as for
  * clarus_hip_gemm_wp after padding: with gate each half of W^T padded to a multiple of 256 rows
  * (n2w = 2 * 256 * ceil(n / 256)), without it W^T padded to a multiple of 512 rows, the padding
  * zero. A residual (bf16 / fp32) needs n a multiple of 256 with gate, n = 256 without it, or a

@@ -114,8 +114,11 @@ def test_validation_rejects_before_launch(lib):
     assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # LN with a residual
     assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
     a.pro, a.res = _lib.PRO_MUL, 0
-    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # a map prologue
-    assert b"LayerNorm / RMS without a residual" in lib.clarus_hip_last_error()
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # the map prologue without a map
+    assert b"bf16 map" in lib.clarus_hip_last_error()
+    a.gate = 1
+    assert lib.clarus_hip_gemm_wr(ctypes.byref(a), 16, None) == _lib.EINVAL  # ... with the gate
+    assert b"map prologue without the gate" in lib.clarus_hip_last_error()
     # clarus_hip_ffn: c, dtype, prologue, alignment and overlap are checked before any launch
     ffn = lib.clarus_hip_ffn
     assert ffn(16, 1 << 20, _lib.BF16, 16, None, 16, None, None, 64, 256, 1, 1e-6, 1.0, None) == _lib.EINVAL

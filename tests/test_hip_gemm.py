@@ -441,6 +441,83 @@ def test_gemm_wp_mul(gate, k, nout, n, h, w, rdt, odt, hip_bf16):
                                      f"{(fused.float() - two.float()).abs().max().item():.3e}")
 
 
+@pytest.mark.parametrize("k,nout,n,h,w,rdt,odt", [
+    (256, 256, 1, 180, 320, torch.bfloat16, torch.bfloat16),  # NAFNet level-2 conv3 (half pass)
+    (128, 512, 2, 37, 53, torch.bfloat16, torch.float32),     # two images, ragged, 512 residual rows
+    (128, 128, 1, 20, 30, None, torch.bfloat16),              # no residual, half pass
+    (256, 256, 3, 9, 11, torch.float32, torch.float32),
+])
+def test_gemm_wr_mul(k, nout, n, h, w, rdt, odt, hip_bf16):
+    """Through the C ABI, clarus_hip_gemm_wr with the TLC-map multiply prologue: bit for bit the
+    separate pass (clarus_hip_rows_prologue with PRO_MUL) followed by clarus_hip_gemm_wr on its
+    rows; maps smaller than the image on both axes, several images, with and without a residual."""
+    import ctypes
+
+    from clarus_amd import _lib
+    lib = _lib.load()
+    g = gen(101 + k + h)
+    m = n * h * w
+    _, _, oh, ow, pt, pl = box_geometry(h, w, (max(2, h // 2), max(2, w // 2)))
+    x = rnd(g, m, k, dtype=torch.bfloat16)
+    smap = rnd(g, n, oh, ow, k, scale=0.5, dtype=torch.bfloat16)
+    wt = rnd(g, k, nout, scale=k ** -0.5, dtype=torch.bfloat16)
+    b, sc = rnd(g, nout), rnd(g, nout)
+    xd, sd, wd, bd, scd = dev(x, smap, wt, b, sc)
+    rd = rnd(g, m, nout).to(rdt).cuda() if rdt is not None else None
+    wp = hip_bf16._wr_pack(wd, False)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    geo = dict(h=h, w=w, oh=oh, ow=ow, pt=pt, pl=pl)
+
+    def gemm_wr(a, p, out):
+        args = _lib.GemmArgs(a=a.data_ptr(), wt=0, c=out.data_ptr(), bias=bd.data_ptr(), scale=scd.data_ptr(),
+                             res=_lib.ptr(rd), small=sd.data_ptr(), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout,
+                             ldr=nout, a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
+                             r_dtype=_lib.dtype_code(rdt) if rdt is not None else 0, s_dtype=_lib.BF16, pro=p,
+                             out_scale=1.0, **geo)
+        _lib.check(lib.clarus_hip_gemm_wr(ctypes.byref(args), wp.data_ptr(), st), "gemm_wr")
+        return _lib.last_kernel()
+
+    fused = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern = gemm_wr(xd, _lib.PRO_MUL, fused)
+    assert kern.startswith("wres_kernel gate=0") and kern.endswith(f"pro={_lib.PRO_MUL}"), kern
+    rows = torch.empty(m, k, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemmArgs(a=xd.data_ptr(), m=m, k=k, batch=1, lda=k, a_dtype=_lib.BF16, pro=_lib.PRO_MUL,
+                         small=sd.data_ptr(), s_dtype=_lib.BF16, **geo)
+    _lib.check(lib.clarus_hip_rows_prologue(ctypes.byref(args), rows.data_ptr(), st), "rows_prologue")
+    two = torch.empty(m, nout, device="cuda", dtype=odt)
+    kern2 = gemm_wr(rows, _lib.PRO_NONE, two)
+    assert torch.equal(fused, two), (f"{kern} vs {kern2}: max|d| "
+                                     f"{(fused.float() - two.float()).abs().max().item():.3e}")
+
+
+def test_linear_mul_routes_to_wres(hip_bf16):
+    """HipOps.linear with the TLC-map multiply at the NAFNet level-2 conv3 shape (180 x 320 x 256,
+    the 85 x 225 map of the 96 x 96 local mean, scale and bf16 residual) runs the multiply inside
+    clarus_hip_gemm_wr, bit-identical to the separate pass and the same kernel (wres_mul False)."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(83)
+    t = rnd(g, 1, 180, 320, 256, dtype=torch.bfloat16).cuda()
+    _, _, oh, ow, pt, pl = box_geometry(180, 320, (96, 96))
+    s = Small(rnd(g, 1, oh, ow, 256, scale=0.5, dtype=torch.bfloat16).cuda(), pt, pl, 180, 320)
+    w = rnd(g, 256, 256, scale=256 ** -0.5, dtype=torch.bfloat16).cuda()
+    b, beta = rnd(g, 256).cuda(), rnd(g, 256, scale=0.2).cuda()
+    res = rnd(g, 1, 180, 320, 256, dtype=torch.bfloat16).cuda()
+    saved = HipOps.wres_mul
+    try:
+        HipOps.wres_mul = True
+        y1 = hip_bf16.linear(t, w, b, mul=s, scale=beta, residual=res)
+        k1 = _lib.last_kernel()
+        HipOps.wres_mul = False
+        y0 = hip_bf16.linear(t, w, b, mul=s, scale=beta, residual=res)
+        k0 = _lib.last_kernel()
+    finally:
+        HipOps.wres_mul = saved
+    assert k1.startswith("wres_kernel gate=0 res=1") and k1.endswith(f"pro={_lib.PRO_MUL}"), k1
+    assert k0.startswith("wres_kernel gate=0 res=1") and k0.endswith("pro=0"), k0
+    assert torch.equal(y1, y0), f"max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
+
+
 def test_linear_mul_routes_to_wstream(hip_bf16):
     """HipOps.linear with the TLC-map multiply at the NAFNet level-3 conv3 shape (90 x 160 x 512,
     the 43 x 113 map of the 48 x 48 local mean, scale and fp32 residual) runs the multiply inside
