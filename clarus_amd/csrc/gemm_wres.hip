@@ -507,13 +507,13 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   if (a->res) {
     const int rs = a->r_dtype == DT_BF16 ? 2 : 4;
     CLARUS_REQUIRE(a->ldr >= a->n && (a->ldr * rs) % 16 == 0 && aligned(a->res, 16), "gemm_wr: 16-byte residual rows");
-    // staged residual rows: 256 channels, or 512 (bf16, no gate, N a multiple of 512)
     // staged residual rows [och, och + rc) of every pass lie inside [0, n): rc = 256 with the gate
-    // (N a multiple of 256) or for N = 256, else 512 (bf16, N a multiple of 512)
-    rc = (gate || a->n <= 256) ? 256 : 512;
+    // (N a multiple of 256) or for N = 256, 128 for N = 128 (bf16, no gate), else 512 (bf16, N a
+    // multiple of 512)
+    rc = (!gate && a->n == 128) ? 128 : ((gate || a->n <= 256) ? 256 : 512);
     CLARUS_REQUIRE(a->n % rc == 0 && (rc == 256 || a->r_dtype == DT_BF16),
                    "gemm_wr: a residual needs N a multiple of 256 with the gate, N = 256, or a bf16 residual "
-                   "with N a multiple of 512");
+                   "with N = 128 or a multiple of 512");
   }
   const int64_t ptiles = cdiv(a->m, WR_P);
   CLARUS_REQUIRE(ptiles < ((int64_t)1 << 30) && a->m * a->ldc * ec < ((int64_t)1 << 40), "gemm_wr: too many tiles");
@@ -537,6 +537,7 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
   if (pro == PRO_MUL) {
     CLARUS_REQUIRE(k == 128 || half, "gemm_wr: the map prologue at K = 256 needs N <= 256 (one half pass)");
     if (rdt == DT_F32) launch_mul<DT_F32, 256>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16 && rc == 128) launch_mul<DT_BF16, 128>(p, cdt, k, half, nblk, s);
     else if (rdt == DT_BF16 && rc == 512) launch_mul<DT_BF16, 512>(p, cdt, k, half, nblk, s);
     else if (rdt == DT_BF16) launch_mul<DT_BF16, 256>(p, cdt, k, half, nblk, s);
     else launch_mul<-1, 256>(p, cdt, k, half, nblk, s);
@@ -554,6 +555,7 @@ extern "C" int clarus_hip_gemm_wr(const ClarusGemmArgs* a, const void* wp, void*
     else launch_c<true, -1, 256>(p, cdt, k, half, nblk, s);
   } else {
     if (rdt == DT_F32) launch_c<false, DT_F32, 256>(p, cdt, k, half, nblk, s);
+    else if (rdt == DT_BF16 && rc == 128) launch_c<false, DT_BF16, 128>(p, cdt, k, half, nblk, s);
     else if (rdt == DT_BF16 && rc == 512) launch_c<false, DT_BF16, 512>(p, cdt, k, half, nblk, s);
     else if (rdt == DT_BF16) launch_c<false, DT_BF16, 256>(p, cdt, k, half, nblk, s);
     else launch_c<false, -1, 256>(p, cdt, k, half, nblk, s);

@@ -110,6 +110,11 @@ class HipOps(Backend):
     # current one); False or other K keep them on the kernels above.
     wres = True
     wres_ks = (128, 256)
+    # N = 128 with a bf16 residual on clarus_hip_gemm_wr when the map prologue rides along (128
+    # residual channels staged per tile): NAFNet level-1 conv3, whose separate 23 us map pass it
+    # replaces. Plain c128 c->c + residual stays on clarus_hip_gemm (config-2 c128 c->c: 39.9-40.4
+    # us there against 40.5-40.6 on clarus_hip_gemm_wr).
+    wres_res128 = True
     # LayerNorm / RMS linear without a residual, bf16 rows and weights, K in wres_ks: the prologue
     # inside clarus_hip_gemm_wr on each A tile in LDS (the separate pass's operand bit for bit,
     # without its round trip through HBM); False keeps the separate pass (K = 128) or the 128-pixel
@@ -231,7 +236,7 @@ class HipOps(Backend):
             _lib.check(self.lib.clarus_hip_gemm(ctypes.byref(args), self._stream(a)), what)
         return c
 
-    def _wp_for(self, a, w, k, nout, gate, act, m, res=None):
+    def _wp_for(self, a, w, k, nout, gate, act, m, res=None, res128=False):
         """("wr" | "wp", W^T packed) when this plain bf16 GEMM goes to clarus_hip_gemm_wr /
         clarus_hip_gemm_wp, else None. Square plain GEMMs that clarus_hip_gemm serves on its W-slice
         kernel (N = K = 128 / 256 / 512, no residual, gate or activation, M <= 80000: the NAFNet SCA
@@ -245,7 +250,8 @@ class HipOps(Backend):
         if (self.wres and k in self.wres_ks and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
                 and act in (0, _lib.ACT_GELU) and nout % 16 == 0
                 and (res is None or (nout % 256 == 0 if gate else (nout == 256 or (res.dtype == torch.bfloat16
-                                                                                     and nout % 512 == 0))))):
+                                                                                     and ((nout == 128 and res128)
+                                                                                          or nout % 512 == 0)))))):
             return "wr", self._wr_pack(w, bool(gate))
         if not (self.wstream and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
                 and k >= self.wstream_min_k and k in (256, 512, 1024) and nw % 512 == 0
@@ -271,7 +277,7 @@ class HipOps(Backend):
         if not (not self.prologue_split and pro == _lib.PRO_MUL and sm is not None and sm.dtype == torch.bfloat16
                 and x.dtype == torch.bfloat16 and k <= 512):
             return None
-        wp = self._wp_for(x, w, k, nout, gate, act, m, res)
+        wp = self._wp_for(x, w, k, nout, gate, act, m, res, res128=self.wres_res128)
         if wp is None:
             return None
         if wp[0] == "wp":

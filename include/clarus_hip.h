@@ -145,7 +145,7 @@ int clarus_hip_gemm_wp(const ClarusGemmArgs* args, const void* wp, void* stream)
  * clarus_hip_gemm_wp after padding: with gate each half of W^T padded to a multiple of 256 rows
  * (n2w = 2 * 256 * ceil(n / 256)), without it W^T padded to a multiple of 512 rows, the padding
  * zero. A residual (bf16 / fp32) needs n a multiple of 256 with gate, n = 256 without it, or a
- * bf16 residual with n a multiple of 512. args->wt is not read. Epilogue as clarus_hip_gemm.
+ * bf16 residual with n = 128 or a multiple of 512. args->wt is not read. Epilogue as clarus_hip_gemm.
  * replaces kernels/gemm.py:353-400 fused_gemm for those shapes (the weight packed once per
  * weight by the host, as the reference's ops cache their transposed weights)
  */

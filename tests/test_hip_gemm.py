@@ -443,6 +443,7 @@ def test_gemm_wp_mul(gate, k, nout, n, h, w, rdt, odt, hip_bf16):
 
 @pytest.mark.parametrize("k,nout,n,h,w,rdt,odt", [
     (256, 256, 1, 180, 320, torch.bfloat16, torch.bfloat16),  # NAFNet level-2 conv3 (half pass)
+    (128, 128, 1, 360, 640, torch.bfloat16, torch.bfloat16),  # NAFNet level-1 conv3 (128 residual channels)
     (128, 512, 2, 37, 53, torch.bfloat16, torch.float32),     # two images, ragged, 512 residual rows
     (128, 128, 1, 20, 30, None, torch.bfloat16),              # no residual, half pass
     (256, 256, 3, 9, 11, torch.float32, torch.float32),
@@ -516,6 +517,30 @@ def test_linear_mul_routes_to_wres(hip_bf16):
     assert k1.startswith("wres_kernel gate=0 res=1") and k1.endswith(f"pro={_lib.PRO_MUL}"), k1
     assert k0.startswith("wres_kernel gate=0 res=1") and k0.endswith("pro=0"), k0
     assert torch.equal(y1, y0), f"max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
+
+
+def test_linear_mul_level1_routes_to_wres(hip_bf16):
+    """HipOps.linear with the TLC-map multiply at the NAFNet level-1 conv3 shape (360 x 640 x 128,
+    the 169 x 449 map of the 192 x 192 local mean, scale and bf16 residual) runs on
+    clarus_hip_gemm_wr with the multiply inside (128 residual channels staged), against the fp32
+    oracle by the rounded-prologue rule (fp32 output); bit-identity with the separate pass at this
+    shape is test_gemm_wr_mul's. Without the map the same c->c + residual stays on clarus_hip_gemm."""
+    from clarus_amd import _lib
+    g = gen(87)
+    t = rnd(g, 1, 360, 640, 128, dtype=torch.bfloat16)
+    _, _, oh, ow, pt, pl = box_geometry(360, 640, (192, 192))
+    s = Small(rnd(g, 1, oh, ow, 128, scale=0.5, dtype=torch.bfloat16), pt, pl, 360, 640)
+    w = rnd(g, 128, 128, scale=128 ** -0.5, dtype=torch.bfloat16)
+    b, beta = rnd(g, 128), rnd(g, 128, scale=0.2)
+    res = rnd(g, 1, 360, 640, 128, dtype=torch.bfloat16)
+    td, wd, bd, betad, resd = dev(t, w, b, beta, res)
+    got = hip_bf16.linear(td, wd, bd, mul=Small(s.data.cuda(), pt, pl, 360, 640), scale=betad, residual=resd,
+                          out_dtype=torch.float32)
+    kern = _lib.last_kernel()
+    assert kern.startswith("wres_kernel gate=0 res=1 k=128") and kern.endswith(f"pro={_lib.PRO_MUL}"), kern
+    check_prologue(got.cpu(), 128, "L1 conv3 TLC mul", t, w, b, mul=s, rounded=True, scale=beta, residual=res)
+    hip_bf16.linear(td, wd, bd, scale=betad, residual=resd)
+    assert not _lib.last_kernel().startswith("wres_kernel"), _lib.last_kernel()
 
 
 def test_linear_mul_routes_to_wstream(hip_bf16):
@@ -638,6 +663,9 @@ def test_linear_ln_routes_to_wres_prologue(hip_bf16):
     (True, 128, 256, torch.bfloat16, torch.float32, None, 64 * 40 + 7),
     (False, 128, 256, torch.float32, torch.float32, None, 64 * 7 + 5),
     (True, 128, 128, None, torch.bfloat16, None, 64 * 300 + 3),
+    # N = 128 with a bf16 residual (128 residual channels staged; config-2 c128 c->c, NAFNet level 1)
+    (False, 128, 128, torch.bfloat16, torch.bfloat16, None, 64 * 50 + 9),
+    (False, 128, 128, torch.bfloat16, torch.float32, "gelu", 333),
 ])
 def test_gemm_wr_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     """Through the C ABI, clarus_hip_gemm_wr (persistent workgroups with their W^T pass resident in
@@ -661,8 +689,8 @@ def test_gemm_wr_kernel(gate, k, nout, rdt, odt, act, m, hip_bf16):
     res = None if rdt is None else rnd(g, m, nout).to(rdt)
     out_scale = 0.5 if k == 128 else 1.0
     ref = REF.linear(x, w, b, gate=gate, act=act, scale=None if sc is None else sc * out_scale, residual=res)
-    if plain and out_scale != 1.0:
-        ref = ref * out_scale
+    if plain and out_scale != 1.0:  # out_scale applies before the residual: act(x w) * out_scale + res
+        ref = REF.linear(x, w, b, gate=gate, act=act) * out_scale + (0.0 if res is None else res.float())
     xd, wd, bd, sd, rd = dev(x, w, b, sc, res)
     wp = hip_bf16._wr_pack(wd, gate)
     out = torch.full((m, nout), float("nan"), device="cuda", dtype=odt)
