@@ -56,9 +56,16 @@ struct PairP {
   int64_t m, lda, ldr, ldc, ld2;
   int c_dt, rms, gate, n2w;
   float eps, out_scale;
+  // MUL: A row q times the bf16 map row of its pixel ([n][oh][ow][512], replicate-padded to the
+  // h x w image by the offsets pt, pl), the TLC-map prologue of the first GEMM
+  const bf16_t* small;
+  int h, w, oh, ow, pt, pl;
 };
 
-template <bool CF32, bool GATE>
+// MUL: each lane multiplies the 16-byte unit it copied of A chunk c by the map values of its row
+// (loaded at kernel start), once its own copies have landed and before the barrier that publishes
+// the chunk: widened to fp32, multiplied, rounded once to bf16, bit for bit the separate pass's rows.
+template <bool CF32, bool GATE, bool MUL>
 __global__ void __launch_bounds__(PR_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 pair_kernel(const PairP p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -100,6 +107,20 @@ pair_kernel(const PairP p) {
   int64_t aq = q0 + arow;
   if (aq > p.m - 1) aq = p.m - 1;  // rows past M: any valid row, not stored
   const unsigned char* asrc = (const unsigned char*)(p.a + aq * p.lda) + m32_swz(arow, lane & 7) * 16;
+  u32x4 mv[MUL ? PR_NCH : 1];  // map values of this lane's unit in every chunk (chunk 0 waits for all)
+  if constexpr (MUL) {
+    const int64_t hw = (int64_t)p.h * p.w;
+    const int64_t im = aq / hw;
+    const int rr = (int)(aq - im * hw);
+    const int yq = rr / p.w;
+    int sy = yq - p.pt, sx = rr - yq * p.w - p.pl;
+    sy = sy < 0 ? 0 : (sy > p.oh - 1 ? p.oh - 1 : sy);
+    sx = sx < 0 ? 0 : (sx > p.ow - 1 ? p.ow - 1 : sx);
+    const bf16_t* mrow = p.small + ((im * p.oh + sy) * p.ow + sx) * (int64_t)PR_K + m32_swz(arow, lane & 7) * 8;
+#pragma unroll
+    for (int c = 0; c < PR_NCH; ++c) mv[c] = *reinterpret_cast<const u32x4*>(mrow + c * 64);
+    asm volatile("" ::: "memory");
+  }
   auto issue_a = [&](int c) __attribute__((always_inline)) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(asrc + c * 128),
                                      (__attribute__((address_space(3))) void*)(lds + (c % PR_STAGES) * PR_STAGE + wave * 1024),
@@ -172,6 +193,17 @@ pair_kernel(const PairP p) {
     if (c == 0) wait_vmcnt<0>();  // (the tables' loads, if any, follow W1 group 0)
     else if (c + 1 < PR_NCH) wait_vmcnt<3>();  // after W1 group c: A c + 1, residual c - 1 (2 copies)
     else wait_vmcnt<2>();                      // c = 7: after W1 group 7 only residual 6
+    if constexpr (MUL) {  // this lane's unit of chunk c (its copy has landed) times the map
+      unsigned char* up = lds + (c % PR_STAGES) * PR_STAGE + wave * 1024 + lane * 16;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+      f32x8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x.v[2 * e] = __uint_as_float(raw[e] << 16) * __uint_as_float(mv[c][e] << 16);
+        x.v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u) * __uint_as_float(mv[c][e] & 0xffff0000u);
+      }
+      *reinterpret_cast<bf16x8*>(up) = pack_bf16(x);
+    }
     barrier_keep_vm();                 // every wave's share of A chunk c; chunk c - 1 read by all
     asm volatile("" ::: "memory");
     if (c + 1 < PR_NCH) load_w1((c + 1) & 1, c + 1);
@@ -450,9 +482,16 @@ extern "C" int clarus_hip_gemm_ln_gemm_w1p(const ClarusGemmArgs* a, const void* 
   CLARUS_REQUIRE(a->a_dtype == DT_BF16 && a->w_dtype == DT_BF16 && a->r_dtype == DT_F32 &&
                      (a->c_dtype == DT_BF16 || a->c_dtype == DT_F32),
                  "gemm_ln_gemm_w1p: bf16 A and W, fp32 residual, bf16 / fp32 output");
-  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 && a->pro == PRO_NONE &&
-                     !a->gate && a->act == ACT_NONE,
-                 "gemm_ln_gemm_w1p: plain rows (no prologue, gate, activation, batch or pixel shuffle)");
+  CLARUS_REQUIRE(a->a_mode == CLARUS_A_ROWS && a->c_mode == CLARUS_C_ROWS && a->batch == 1 &&
+                     (a->pro == PRO_NONE || a->pro == PRO_MUL) && !a->gate && a->act == ACT_NONE,
+                 "gemm_ln_gemm_w1p: plain rows or the TLC-map prologue (no other prologue, gate, activation, "
+                 "batch or pixel shuffle)");
+  const bool mul = a->pro == PRO_MUL;
+  if (mul) {
+    CLARUS_REQUIRE(a->small && a->s_dtype == DT_BF16 && aligned(a->small, 16) && a->h > 0 && a->w > 0 && a->oh > 0 &&
+                       a->ow > 0 && a->m % ((int64_t)a->h * a->w) == 0,
+                   "gemm_ln_gemm_w1p: the map prologue needs a bf16 map (16-byte aligned) and m a multiple of h w");
+  }
   const int ec = a->c_dtype == DT_BF16 ? 2 : 4;
   CLARUS_REQUIRE(a->lda >= a->k && (a->lda * 2) % 16 == 0 && aligned(a->a, 16) && aligned(w1p, 16) && aligned(w2p, 16),
                  "gemm_ln_gemm_w1p: 16-byte A rows and packed weights");
@@ -470,11 +509,17 @@ extern "C" int clarus_hip_gemm_ln_gemm_w1p(const ClarusGemmArgs* a, const void* 
   p.m = a->m; p.lda = a->lda; p.ldr = a->ldr; p.ldc = a->ldc; p.ld2 = gate2 ? n2w / 2 : n2w;
   p.c_dt = a->c_dtype; p.rms = rms; p.gate = gate2; p.n2w = (int)n2w;
   p.eps = eps; p.out_scale = a->out_scale;
-  note_kernel("pair_kernel gate=%d c=%s", (int)gate2, a->c_dtype == DT_F32 ? "fp32" : "bf16");
-  auto kern = a->c_dtype == DT_F32 ? (gate2 ? pair_kernel<true, true> : pair_kernel<true, false>)
-                                   : (gate2 ? pair_kernel<false, true> : pair_kernel<false, false>);
+  p.small = (const bf16_t*)a->small;
+  p.h = a->h; p.w = a->w; p.oh = a->oh; p.ow = a->ow; p.pt = a->pt; p.pl = a->pl;
+  note_kernel("pair_kernel gate=%d c=%s mul=%d", (int)gate2, a->c_dtype == DT_F32 ? "fp32" : "bf16", (int)mul);
+  auto kern = mul ? (a->c_dtype == DT_F32 ? (gate2 ? pair_kernel<true, true, true> : pair_kernel<true, false, true>)
+                                          : (gate2 ? pair_kernel<false, true, true> : pair_kernel<false, false, true>))
+                  : (a->c_dtype == DT_F32 ? (gate2 ? pair_kernel<true, true, false> : pair_kernel<true, false, false>)
+                                          : (gate2 ? pair_kernel<false, true, false> : pair_kernel<false, false, false>));
   static const bool attr = [] {
-    for (auto k : {pair_kernel<true, true>, pair_kernel<true, false>, pair_kernel<false, true>, pair_kernel<false, false>})
+    for (auto k : {pair_kernel<true, true, false>, pair_kernel<true, false, false>, pair_kernel<false, true, false>,
+                   pair_kernel<false, false, false>, pair_kernel<true, true, true>, pair_kernel<true, false, true>,
+                   pair_kernel<false, true, true>, pair_kernel<false, false, true>})
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, PR_LDS);
     return true;
   }();

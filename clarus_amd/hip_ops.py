@@ -84,6 +84,9 @@ class HipOps(Backend):
     # streamed into registers, the residual staged in LDS during the first GEMM); False keeps it on
     # clarus_hip_gemm_ln_gemm (the first GEMM's weights staged through LDS).
     pair_w1p = True
+    # With pair_w1p, the first GEMM's TLC-map multiply (NAFNet conv3) inside that kernel on each A
+    # chunk in LDS (the separate pass's operand bit for bit); False keeps the separate pass.
+    pair_mul = True
     # Plain bf16 GEMMs with K = 256, 512 or 1024 (>= wstream_min_k) and W^T rows a multiple of 512 on
     # clarus_hip_gemm_wp (W^T packed once per weight and streamed from L2 into registers, the
     # residual staged in LDS during the K loop); False keeps them on clarus_hip_gemm.
@@ -419,10 +422,11 @@ class HipOps(Backend):
             return self._frag_pack(tp.contiguous(), gate)
         return self.cached(w, "wr_gate" if gate else "wr", pack)
 
-    def _pair_first(self, x, w, bias, scale, residual, mul, out_dtype, ln):
+    def _pair_first(self, x, w, bias, scale, residual, mul, out_dtype, ln, mul_in=False):
         """The first GEMM of linear_ln_linear on the LN-rows kernel: (A rows, W^T, output,
         epilogue, m) when it fits (bf16 backend, plain bf16 rows after any prologue pass, N = 512,
-        K % 64 == 0, a residual, no gate / activation), else None."""
+        K % 64 == 0, a residual, no gate / activation), else None. mul_in: a bf16 TLC map at K = 512
+        stays with x (pro = MUL in the epilogue args) for the pair kernel to apply."""
         if not (self.fuse_ln_rows and not self.prologue_split and self.dtype == torch.bfloat16
                 and ln in (True, "rms") and not is_small(x) and residual is not None):
             return None
@@ -434,7 +438,11 @@ class HipOps(Backend):
         if not (nout == 512 and k % 64 == 0 and w.dtype == torch.bfloat16 and n * h * wd > 0):
             return None
         m = n * h * wd
-        if pro != _lib.PRO_NONE:
+        inside = (mul_in and pro == _lib.PRO_MUL and k == 512 and sm.dtype == torch.bfloat16
+                  and x.dtype == torch.bfloat16)
+        if inside:
+            a = x
+        elif pro != _lib.PRO_NONE:
             if not self._prologue_pass(w, pro, k):
                 return None
             a = self._prologue_rows(x, pro, sm, geom, 1e-6, m, k)
@@ -443,11 +451,14 @@ class HipOps(Backend):
         else:
             return None
         out = torch.empty((n, h, wd, nout), device=x.device, dtype=odt)
+        hh, ww, oh, ow, pt, pl = geom if inside else (0, 0, 0, 0, 0, 0)
         epi = _lib.GemmArgs(
             a=a.data_ptr(), wt=self._wt(w).data_ptr(), c=out.data_ptr(), bias=_lib.ptr(self._bias(bias)),
             scale=_lib.ptr(self._bias(scale)), res=residual.data_ptr(), m=m, n=nout, k=k, batch=1, lda=k, ldc=nout,
             ldr=nout, a_dtype=_lib.BF16, w_dtype=_lib.BF16, c_dtype=_lib.dtype_code(odt),
-            r_dtype=_lib.dtype_code(residual.dtype), out_scale=1.0)
+            r_dtype=_lib.dtype_code(residual.dtype), out_scale=1.0, pro=_lib.PRO_MUL if inside else 0,
+            small=_lib.ptr(sm) if inside else None, s_dtype=_lib.BF16 if inside else 0,
+            h=hh, w=ww, oh=oh, ow=ow, pt=pt, pl=pl)
         return a, out, epi, m
 
     def linear_ln_linear(self, x, w, bias=None, scale=None, residual=None, mul=None, out_dtype=None,
@@ -458,7 +469,13 @@ class HipOps(Backend):
         [512, 512 j] weight; the first GEMM writing the LN rows of its output and a plain GEMM
         on them when only the first fits; otherwise the two linear ops."""
         pairable = w2 is not None and w2.dtype == torch.bfloat16 and w2.dim() == 2 and w2.shape[0] == 512
-        first = self._pair_first(x, w, bias, scale, residual, mul, out_dtype, ln) if pairable else None
+        b2 = self._bias(bias2) if pairable else None
+        # the first GEMM's TLC-map multiply inside clarus_hip_gemm_ln_gemm_w1p (the branch below that
+        # takes it: W2 [512, 512 j], an fp32 residual, K = 512 checked in _pair_first)
+        mul_in = (pairable and self.pair_mul and self.pair_w1p and mul is not None and residual is not None
+                  and residual.dtype == torch.float32 and w2.shape[1] % 512 == 0 and w2.is_contiguous()
+                  and (b2 is None or _vec16(b2)))
+        first = self._pair_first(x, w, bias, scale, residual, mul, out_dtype, ln, mul_in) if pairable else None
         if first is None:
             return linear_ln_linear_unfused(self, x, w, bias, scale, residual, mul, out_dtype, w2, bias2, gate2,
                                             ln, ln_eps)

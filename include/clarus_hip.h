@@ -251,7 +251,9 @@ int clarus_hip_gemm_ln_gemm(const ClarusGemmArgs* args, float eps, int32_t rms, 
  * the gate (n2w = 512, gate2 = 0), and args->wt is not read. Both weights stream from L2 into
  * registers and the residual tile is staged in LDS during the first GEMM; args->c is written,
  * bit-identical to clarus_hip_gemm_ln_rows's output, and out2 as clarus_hip_gemm_ln_gemm's up
- * to the row statistics' summation order.
+ * to the row statistics' summation order. args->pro may be CLARUS_PRO_MUL (bf16 A and map; small,
+ * s_dtype, h, w, oh, ow, pt, pl as for clarus_hip_gemm, m a multiple of h w): the first GEMM's
+ * A rows times the map, bit for bit clarus_hip_rows_prologue's rows, applied in the kernel.
  * No counterpart in the reference: the same fusion as clarus_hip_gemm_ln_gemm, for NAFNet's
  * level-3 pairs (conv3 -> conv4, conv5 -> conv1).
  */

@@ -1243,6 +1243,38 @@ def test_linear_ln_linear_w1p_vs_pair(gate2, odt, m, n2w, with_b2, hip_bf16):
     assert d.max().item() <= 0.25, d.max().item()
 
 
+@pytest.mark.parametrize("n,h,w,gate2,odt", [(1, 90, 160, True, torch.float32),   # NAFNet level-3 conv3 -> conv4
+                                             (2, 37, 53, False, torch.bfloat16)])  # two images, ragged tiles
+def test_linear_ln_linear_mul_inside_pair(n, h, w, gate2, odt, hip_bf16):
+    """linear_ln_linear with the TLC-map multiply on the first GEMM (NAFNet conv3 -> LN -> conv4):
+    the multiply inside clarus_hip_gemm_ln_gemm_w1p's A ring (HipOps.pair_mul) against the
+    separate pass followed by the same kernel: y and u bit-identical, the map smaller than the
+    image on both axes."""
+    from clarus_amd import _lib
+    from clarus_amd.hip_ops import HipOps
+    g = gen(49)
+    x = rnd(g, n, h, w, 512, dtype=torch.bfloat16).cuda()
+    _, _, oh, ow, pt, pl = box_geometry(h, w, (min(48, h // 2), min(48, w // 2)))
+    s = Small(rnd(g, n, oh, ow, 512, scale=0.5, dtype=torch.bfloat16).cuda(), pt, pl, h, w)
+    w3, b3 = rnd(g, 512, 512, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 512).cuda()
+    w4, b4 = rnd(g, 512, 1024, scale=512 ** -0.5, dtype=torch.bfloat16).cuda(), rnd(g, 1024).cuda()
+    beta, inp = rnd(g, 512).cuda(), (1 + rnd(g, n, h, w, 512)).cuda()
+    saved = HipOps.pair_mul
+    outs, kernels = [], []
+    try:
+        for on in (True, False):
+            HipOps.pair_mul = on
+            outs.append(hip_bf16.linear_ln_linear(x, w3, b3, scale=beta, residual=inp, mul=s, out_dtype=odt,
+                                                  w2=w4, bias2=b4, gate2=gate2, ln=True))
+            kernels.append(_lib.last_kernel())
+    finally:
+        HipOps.pair_mul = saved
+    assert kernels[0].endswith("mul=1") and kernels[1].endswith("mul=0"), kernels
+    (y1, u1), (y0, u0) = outs
+    assert torch.equal(y1, y0), f"y: max|d| {(y1.float() - y0.float()).abs().max().item():.3e}"
+    assert torch.equal(u1, u0), f"u: max|d| {(u1.float() - u0.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("k,nout,gate", [(64, 32, False), (64, 96, False), (256, 48, False), (64, 32, True)])
 def test_linear_range(k, nout, gate, hip_bf16):
     """|x| ~ 400, |w| ~ 200, scale 1e-4 -> fp32 (tools/test_ops_contracts.py:76-86): bf16
