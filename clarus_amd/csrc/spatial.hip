@@ -310,6 +310,10 @@ extern "C" int clarus_hip_boxmean(const void* x, int32_t x_dtype, void* out, int
     int T = T0;
     while (T < 256 && T * groups < 256) T *= 2;
     if (T == T0 && T < 256 && lines * T < 131072) T *= 2;
+    // long windows take more threads while each keeps >= 6 positions (NAFNet-w64 720p, cold, us:
+    // level 0, k = 384, 128.7 -> 117.4; level 1, k = 192, 62.5 -> 60.9); at 3 positions per
+    // thread (k = 96, 48) the exchange outweighs the rows: 35.1 -> 47.7 and 24.9 -> 35.7
+    while (T < 256 && lines * T < 262144 && cdiv(k, (int64_t)(2 * T)) >= 6) T *= 2;
     q.T = T;
     q.R = (int)cdiv(k, T);
     q.QW = 256 / T;

@@ -372,11 +372,12 @@ def test_boxmean_exact_float64():
     assert ((got - ref).abs() / ref.abs()).max().item() < 2e-7
 
 
-@pytest.mark.parametrize("h,w,c,k", [(720, 1280, 64, 384), (360, 640, 128, 192)])
+@pytest.mark.parametrize("h,w,c,k", [(720, 1280, 64, 384), (360, 640, 128, 192), (600, 1024, 64, 300)])
 def test_boxmean_nafnet_levels(h, w, c, k, hip_bf16):
-    """NAFNet-w64 levels 0 and 1 at 720p: windows 384 / 192 (maps 337 x 897 / 169 x 449); the
-    passes that keep all of a thread's rows in registers (24 bf16 rows of the vertical pass at
-    level 0, 12 fp32 rows of the horizontal pass at level 1)."""
+    """NAFNet-w64 levels 0 and 1 at 720p: windows 384 / 192 (maps 337 x 897 / 169 x 449), 32
+    threads per line block; and a 300 window whose passes keep all of a thread's rows in
+    registers (19 bf16 rows of the vertical pass in the 24-row form, 10 fp32 rows of the
+    horizontal pass in the 16-row form)."""
     g = gen(12)
     x = rnd(g, 1, h, w, c, dtype=torch.bfloat16)
     got = hip_bf16.boxmean(x.cuda(), k)
